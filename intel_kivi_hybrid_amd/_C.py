@@ -1,0 +1,388 @@
+"""``_C`` -- the drop-in for the reference's compiled module ``kivi_sycl._C``.
+
+Same twelve functions, keyword names, argument meaning and error behaviour as
+the reference binding (src/csrc/bindings/pybind_module.cpp:9-82): the caller
+allocates every output, the ops write in place, the blocking ops return
+``None`` after the device work has finished and the ``*_async`` ops return a
+:class:`KiviEvent`.  Validation follows src/csrc/ops/kv_cache_ops.cpp:19-171
+message for message and raises ``RuntimeError`` (what ``TORCH_CHECK`` raises
+in Python); the device check expects ROCm-torch's ``cuda`` device type where
+the reference expected ``xpu`` (src/csrc/include/kivi/common.hpp:64-75).
+
+Work is launched on ``torch.cuda.current_stream()`` of the tensors' device,
+through the C ABI of ``libkivi_hip.so``; nothing here computes on the host.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _native
+
+_lib = _native.load()
+
+__all__ = [
+    "KiviEvent",
+    "quantize_keys", "quantize_values", "dequantize_keys", "dequantize_values",
+    "quant_dequant_roundtrip_keys", "quant_dequant_roundtrip_values",
+    "quantize_keys_async", "quantize_values_async", "dequantize_keys_async",
+    "dequantize_values_async", "quant_dequant_roundtrip_keys_async",
+    "quant_dequant_roundtrip_values_async",
+]
+
+_DEVICE_TYPE = "cuda"   # ROCm torch reports HIP devices as "cuda"
+
+# torch::toString(ScalarType) spellings used in the reference's messages.
+_DTYPE_NAMES = {
+    torch.float32: "Float", torch.float64: "Double", torch.float16: "Half",
+    torch.bfloat16: "BFloat16", torch.uint8: "Byte", torch.int8: "Char",
+    torch.int16: "Short", torch.int32: "Int", torch.int64: "Long",
+    torch.bool: "Bool",
+}
+
+
+def _dtype_name(dt) -> str:
+    return _DTYPE_NAMES.get(dt, str(dt).replace("torch.", ""))
+
+
+def _fail(*parts) -> None:
+    raise RuntimeError("".join(str(p) for p in parts))
+
+
+def _check(cond: bool, *parts) -> None:
+    if not cond:
+        _fail(*parts)
+
+
+def _check_int(value, name: str) -> int:
+    if isinstance(value, bool) or not isinstance(value, int):
+        raise TypeError(f"{name} must be an int, got {type(value).__name__}")
+    if not -(1 << 31) <= value < (1 << 31):
+        raise TypeError(f"{name} does not fit in a C int: {value}")
+    return value
+
+
+def _check_tensor(t, name: str, dtype) -> None:
+    """common.hpp:64-75: contiguous, exact dtype, device type."""
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    _check(t.is_contiguous(), name, " must be contiguous")
+    _check(t.dtype == dtype, name, " must be ", _dtype_name(dtype), " but got ",
+           _dtype_name(t.dtype))
+    _check(t.device.type == _DEVICE_TYPE, name, " must be on ", _DEVICE_TYPE,
+           " but got ", t.device.type)
+
+
+def _check_same_device(*tensors) -> torch.device:
+    dev = tensors[0].device
+    for t in tensors[1:]:
+        _check(t.device == dev, "all tensors must be on the same device, got ",
+               dev, " and ", t.device)
+    return dev
+
+
+# --------------------------------------------------------------------------
+# Validation: kv_cache_ops.cpp:19-171.  Each returns the count the kernel
+# launch needs.
+# --------------------------------------------------------------------------
+def _validate_quant_keys(input, output, scales, zeros, group_size) -> int:
+    _check_tensor(input, "input", torch.float32)
+    _check_tensor(output, "output", torch.uint8)
+    _check_tensor(scales, "scales", torch.float32)
+    _check_tensor(zeros, "zeros", torch.float32)
+    _check(group_size > 0 and group_size % 4 == 0,
+           "group_size must be positive and divisible by 4, got ", group_size)
+    n = scales.numel()
+    _check(n > 0, "scales must be non-empty")
+    _check(zeros.numel() == n, "zeros size (", zeros.numel(),
+           ") must match scales size (", n, ")")
+    _check(input.numel() == n * group_size, "input size (", input.numel(),
+           ") must equal num_channels(", n, ") * group_size(", group_size, ") = ",
+           n * group_size)
+    _check(output.numel() == n * (group_size // 4), "output size (", output.numel(),
+           ") must equal num_channels(", n, ") * (group_size/4) = ",
+           n * (group_size // 4))
+    return n
+
+
+def _validate_quant_values(input, output, scales, zeros, head_dim, group_size) -> int:
+    _check_tensor(input, "input", torch.float32)
+    _check_tensor(output, "output", torch.uint8)
+    _check_tensor(scales, "scales", torch.float32)
+    _check_tensor(zeros, "zeros", torch.float32)
+    _check(group_size > 0 and group_size % 4 == 0,
+           "group_size must be positive and divisible by 4")
+    _check(head_dim > 0 and head_dim % group_size == 0,
+           "head_dim must be positive and divisible by group_size")
+    _check(input.numel() % head_dim == 0, "input.numel() (", input.numel(),
+           ") must be divisible by head_dim (", head_dim,
+           ") — refusing to silently truncate trailing elements")
+    n_tok = input.numel() // head_dim
+    gpt = head_dim // group_size
+    _check(n_tok > 0, "input must be non-empty")
+    _check(scales.numel() == n_tok * gpt, "scales size (", scales.numel(),
+           ") must equal num_tokens(", n_tok, ") * groups_per_token(", gpt, ")")
+    _check(zeros.numel() == scales.numel(), "zeros size (", zeros.numel(),
+           ") must match scales size (", scales.numel(), ")")
+    _check(output.numel() == n_tok * (head_dim // 4), "output size (", output.numel(),
+           ") must equal num_tokens(", n_tok, ") * (head_dim/4) = ",
+           n_tok * (head_dim // 4))
+    return n_tok
+
+
+def _validate_dequant_keys(input, scales, zeros, output, group_size) -> int:
+    _check_tensor(input, "input", torch.uint8)
+    _check_tensor(scales, "scales", torch.float32)
+    _check_tensor(zeros, "zeros", torch.float32)
+    _check_tensor(output, "output", torch.float32)
+    _check(group_size > 0 and group_size % 4 == 0,
+           "group_size must be positive and divisible by 4, got ", group_size)
+    n = scales.numel()
+    _check(n > 0, "scales must be non-empty")
+    _check(zeros.numel() == n, "zeros size (", zeros.numel(),
+           ") must match scales size (", n, ")")
+    _check(input.numel() == n * (group_size // 4), "input (packed) size (", input.numel(),
+           ") must equal num_channels(", n, ") * (group_size/4) = ", n * (group_size // 4))
+    _check(output.numel() == n * group_size, "output size (", output.numel(),
+           ") must equal num_channels(", n, ") * group_size = ", n * group_size)
+    return n
+
+
+def _validate_dequant_values(input, scales, zeros, output, head_dim, group_size) -> int:
+    _check_tensor(input, "input", torch.uint8)
+    _check_tensor(scales, "scales", torch.float32)
+    _check_tensor(zeros, "zeros", torch.float32)
+    _check_tensor(output, "output", torch.float32)
+    _check(group_size > 0 and group_size % 4 == 0,
+           "group_size must be positive and divisible by 4, got ", group_size)
+    _check(head_dim > 0 and head_dim % group_size == 0,
+           "head_dim must be positive and divisible by group_size")
+    n = scales.numel()
+    _check(n > 0, "scales must be non-empty")
+    _check(zeros.numel() == n, "zeros size (", zeros.numel(),
+           ") must match scales size (", n, ")")
+    _check(input.numel() == n * (group_size // 4), "input (packed) size (", input.numel(),
+           ") must equal num_groups(", n, ") * (group_size/4) = ", n * (group_size // 4))
+    _check(output.numel() == n * group_size, "output size (", output.numel(),
+           ") must equal num_groups(", n, ") * group_size = ", n * group_size)
+    return n
+
+
+def _validate_roundtrip_keys(input, output, group_size) -> int:
+    _check_tensor(input, "input", torch.float32)
+    _check_tensor(output, "output", torch.float32)
+    _check(group_size > 0 and group_size % 4 == 0,
+           "group_size must be positive and divisible by 4, got ", group_size)
+    _check(input.numel() % group_size == 0, "input.numel() (", input.numel(),
+           ") must be divisible by group_size (", group_size, ")")
+    _check(output.numel() == input.numel(), "output size (", output.numel(),
+           ") must equal input size (", input.numel(),
+           ") — round-trip is shape-preserving")
+    n = input.numel() // group_size
+    _check(n > 0, "input must be non-empty")
+    return n
+
+
+def _validate_roundtrip_values(input, output, head_dim, group_size) -> int:
+    _check_tensor(input, "input", torch.float32)
+    _check_tensor(output, "output", torch.float32)
+    _check(group_size > 0 and group_size % 4 == 0,
+           "group_size must be positive and divisible by 4")
+    _check(head_dim > 0 and head_dim % group_size == 0,
+           "head_dim must be positive and divisible by group_size")
+    _check(input.numel() % head_dim == 0, "input.numel() (", input.numel(),
+           ") must be divisible by head_dim (", head_dim, ")")
+    _check(output.numel() == input.numel(), "output size (", output.numel(),
+           ") must equal input size (", input.numel(),
+           ") — round-trip is shape-preserving")
+    n = input.numel() // head_dim
+    _check(n > 0, "input must be non-empty")
+    return n
+
+
+# --------------------------------------------------------------------------
+# Launch plumbing.
+# --------------------------------------------------------------------------
+def _stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+class KiviEvent:
+    """Handle for work submitted by a ``*_async`` op (event.hpp:16-31).
+
+    ``wait()`` blocks until the work completes and raises ``RuntimeError`` on
+    a device-side error.  The tensors passed to the op are kept alive until
+    then."""
+
+    __slots__ = ("_ev", "_keep")
+
+    def __init__(self, stream: int, keep=()):
+        ev = ctypes.c_void_p()
+        _native.check(_lib.kivi_event_record(ctypes.c_void_p(stream), ctypes.byref(ev)),
+                      "kivi_event_record")
+        self._ev = ev
+        self._keep = keep
+
+    def wait(self) -> None:
+        if self._ev is None:
+            return
+        try:
+            _native.check(_lib.kivi_event_wait(self._ev), "KiviEvent.wait")
+        finally:
+            _lib.kivi_event_destroy(self._ev)
+            self._ev = None
+            self._keep = ()
+
+    def query(self) -> bool:
+        """True once the work has completed (non-blocking)."""
+        if self._ev is None:
+            return True
+        rc = _lib.kivi_event_query(self._ev)
+        if rc < 0:
+            _native.check(-rc, "KiviEvent.query")
+        return rc == 1
+
+    def __del__(self):
+        ev = getattr(self, "_ev", None)
+        if ev is not None and _lib is not None:
+            try:
+                _lib.kivi_event_destroy(ev)
+            except Exception:   # interpreter shutdown
+                pass
+
+
+def _run(device: torch.device, blocking: bool, what: str, fn, *args, keep=()):
+    with torch.cuda.device(device):
+        stream = _stream_of(device)
+        _native.check(fn(*args, ctypes.c_void_p(stream)), what)
+        if blocking:
+            _native.check(_lib.kivi_stream_synchronize(ctypes.c_void_p(stream)), what)
+            return None
+        return KiviEvent(stream, keep)
+
+
+# --------------------------------------------------------------------------
+# The twelve ops (pybind_module.cpp:18-81).
+# --------------------------------------------------------------------------
+def _quantize_keys(input, output, scales, zeros, group_size, blocking):
+    group_size = _check_int(group_size, "group_size")
+    n = _validate_quant_keys(input, output, scales, zeros, group_size)
+    dev = _check_same_device(input, output, scales, zeros)
+    return _run(dev, blocking, "quantize_keys", _lib.kivi_quantize_keys_per_channel,
+                _ptr(input), _ptr(output), _ptr(scales), _ptr(zeros), n, group_size,
+                keep=(input, output, scales, zeros))
+
+
+def _quantize_values(input, output, scales, zeros, head_dim, group_size, blocking):
+    head_dim = _check_int(head_dim, "head_dim")
+    group_size = _check_int(group_size, "group_size")
+    n_tok = _validate_quant_values(input, output, scales, zeros, head_dim, group_size)
+    dev = _check_same_device(input, output, scales, zeros)
+    return _run(dev, blocking, "quantize_values", _lib.kivi_quantize_values_per_token,
+                _ptr(input), _ptr(output), _ptr(scales), _ptr(zeros), n_tok, head_dim,
+                group_size, keep=(input, output, scales, zeros))
+
+
+def _dequantize_keys(input, scales, zeros, output, group_size, blocking):
+    group_size = _check_int(group_size, "group_size")
+    n = _validate_dequant_keys(input, scales, zeros, output, group_size)
+    dev = _check_same_device(input, scales, zeros, output)
+    return _run(dev, blocking, "dequantize_keys", _lib.kivi_dequantize_keys_per_channel,
+                _ptr(input), _ptr(scales), _ptr(zeros), _ptr(output), n, group_size,
+                keep=(input, scales, zeros, output))
+
+
+def _dequantize_values(input, scales, zeros, output, head_dim, group_size, blocking):
+    head_dim = _check_int(head_dim, "head_dim")
+    group_size = _check_int(group_size, "group_size")
+    n = _validate_dequant_values(input, scales, zeros, output, head_dim, group_size)
+    dev = _check_same_device(input, scales, zeros, output)
+    return _run(dev, blocking, "dequantize_values", _lib.kivi_dequantize_values_per_token,
+                _ptr(input), _ptr(scales), _ptr(zeros), _ptr(output), n, group_size,
+                keep=(input, scales, zeros, output))
+
+
+def _roundtrip_keys(input, output, group_size, blocking):
+    group_size = _check_int(group_size, "group_size")
+    n = _validate_roundtrip_keys(input, output, group_size)
+    dev = _check_same_device(input, output)
+    return _run(dev, blocking, "quant_dequant_roundtrip_keys",
+                _lib.kivi_quant_dequant_roundtrip_keys, _ptr(input), _ptr(output), n,
+                group_size, keep=(input, output))
+
+
+def _roundtrip_values(input, output, head_dim, group_size, blocking):
+    head_dim = _check_int(head_dim, "head_dim")
+    group_size = _check_int(group_size, "group_size")
+    n_tok = _validate_roundtrip_values(input, output, head_dim, group_size)
+    dev = _check_same_device(input, output)
+    return _run(dev, blocking, "quant_dequant_roundtrip_values",
+                _lib.kivi_quant_dequant_roundtrip_values, _ptr(input), _ptr(output),
+                n_tok, head_dim, group_size, keep=(input, output))
+
+
+def quantize_keys(input, output, scales, zeros, group_size):
+    """Asymmetric 2-bit key quantization (per-channel)."""
+    return _quantize_keys(input, output, scales, zeros, group_size, True)
+
+
+def quantize_values(input, output, scales, zeros, head_dim, group_size):
+    """Asymmetric 2-bit value quantization (per-token)."""
+    return _quantize_values(input, output, scales, zeros, head_dim, group_size, True)
+
+
+def dequantize_keys(input, scales, zeros, output, group_size):
+    """Asymmetric 2-bit key dequantization (per-channel)."""
+    return _dequantize_keys(input, scales, zeros, output, group_size, True)
+
+
+def dequantize_values(input, scales, zeros, output, head_dim, group_size):
+    """Asymmetric 2-bit value dequantization (per-token)."""
+    return _dequantize_values(input, scales, zeros, output, head_dim, group_size, True)
+
+
+def quant_dequant_roundtrip_keys(input, output, group_size):
+    """Fused quantize->dequantize round-trip (per-channel); output is
+    bit-identical to quantize_keys followed by dequantize_keys."""
+    return _roundtrip_keys(input, output, group_size, True)
+
+
+def quant_dequant_roundtrip_values(input, output, head_dim, group_size):
+    """Fused quantize->dequantize round-trip (per-token)."""
+    return _roundtrip_values(input, output, head_dim, group_size, True)
+
+
+def quantize_keys_async(input, output, scales, zeros, group_size):
+    """Non-blocking quantize_keys -- returns a KiviEvent, does not wait."""
+    return _quantize_keys(input, output, scales, zeros, group_size, False)
+
+
+def quantize_values_async(input, output, scales, zeros, head_dim, group_size):
+    """Non-blocking quantize_values -- returns a KiviEvent, does not wait."""
+    return _quantize_values(input, output, scales, zeros, head_dim, group_size, False)
+
+
+def dequantize_keys_async(input, scales, zeros, output, group_size):
+    """Non-blocking dequantize_keys -- returns a KiviEvent, does not wait."""
+    return _dequantize_keys(input, scales, zeros, output, group_size, False)
+
+
+def dequantize_values_async(input, scales, zeros, output, head_dim, group_size):
+    """Non-blocking dequantize_values -- returns a KiviEvent, does not wait."""
+    return _dequantize_values(input, scales, zeros, output, head_dim, group_size, False)
+
+
+def quant_dequant_roundtrip_keys_async(input, output, group_size):
+    """Non-blocking quant_dequant_roundtrip_keys -- returns a KiviEvent."""
+    return _roundtrip_keys(input, output, group_size, False)
+
+
+def quant_dequant_roundtrip_values_async(input, output, head_dim, group_size):
+    """Non-blocking quant_dequant_roundtrip_values -- returns a KiviEvent."""
+    return _roundtrip_values(input, output, head_dim, group_size, False)

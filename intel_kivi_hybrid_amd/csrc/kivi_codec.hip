@@ -1,0 +1,331 @@
+// KIVI 2-bit asymmetric codec for gfx950: quantise + pack, unpack +
+// dequantise, and the fused round-trip.
+//
+// Replaces the reference's six SYCL kernels
+// (src/csrc/kernels/quantize_kernels.cpp:24-120,
+//  src/csrc/kernels/dequantize_kernels.cpp:32-124,
+//  src/csrc/kernels/roundtrip_kernels.cpp:14-91).  Keys (per channel, grouped
+// along tokens) and values (per token, grouped along channels) both reduce
+// contiguous runs of G floats and write group g's bytes at g*G/4, so one
+// flat-group kernel body serves both.
+//
+// Layout of the work (wave64): lane i of a wave loads float4 number i of a
+// 64-float4 tile, so every load instruction reads 1 KiB contiguously.  A group
+// of G floats is G/4 consecutive lanes; its min/max is a segmented butterfly
+// (DPP quad permutes and row mirrors, then ds_swizzle / ds_bpermute for 32/64
+// lanes).  Each lane turns its 4 floats into one packed byte in registers.
+// Group sizes whose G/4 is not a power of two <= 64 take a one-thread-per-
+// group kernel with the same arithmetic.
+#include "kivi_common.hpp"
+#include "../../include/kivi_hip.h"
+
+namespace kivi {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 4;
+
+__device__ __forceinline__ void min_max4(const float4& v, float& mn, float& mx) {
+    mn = fmin_nan(fmin_nan(v.x, v.y), fmin_nan(v.z, v.w));
+    mx = fmax_nan(fmax_nan(v.x, v.y), fmax_nan(v.z, v.w));
+}
+
+// ----------------------------------------------------------------------------
+// Segmented kernels: LANES = G/4 lanes per group.
+// ----------------------------------------------------------------------------
+template <int LANES>
+__global__ __launch_bounds__(kBlock) void quantize_seg_kernel(
+    const float4* __restrict__ in, uint8_t* __restrict__ packed,
+    float* __restrict__ scales, float* __restrict__ zeros, int64_t n_vec) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t base = (int64_t)blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
+    float4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t idx = base + (int64_t)u * kBlock;
+        v[u] = idx < n_vec ? in[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t idx = base + (int64_t)u * kBlock;
+        float mn, mx, scale;
+        min_max4(v[u], mn, mx);
+        seg_min_max<LANES>(mn, mx);
+        finish_group(mn, mx, scale);
+        const uint32_t byte = encode4(v[u].x, v[u].y, v[u].z, v[u].w, mn, scale);
+        if (idx < n_vec) {
+            packed[idx] = (uint8_t)byte;
+            if ((lane & (LANES - 1)) == 0) {
+                scales[idx / LANES] = scale;
+                zeros[idx / LANES] = mn;
+            }
+        }
+    }
+}
+
+template <int LANES>
+__global__ __launch_bounds__(kBlock) void roundtrip_seg_kernel(
+    const float4* __restrict__ in, float4* __restrict__ out, int64_t n_vec) {
+    const int64_t base = (int64_t)blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
+    float4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t idx = base + (int64_t)u * kBlock;
+        v[u] = idx < n_vec ? in[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t idx = base + (int64_t)u * kBlock;
+        float mn, mx, scale;
+        min_max4(v[u], mn, mx);
+        seg_min_max<LANES>(mn, mx);
+        finish_group(mn, mx, scale);
+        const uint32_t byte = encode4(v[u].x, v[u].y, v[u].z, v[u].w, mn, scale);
+        if (idx < n_vec) out[idx] = decode4(byte, scale, mn);
+    }
+}
+
+// ----------------------------------------------------------------------------
+// One thread per group: any G divisible by 4, any alignment.
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ void serial_group_stats(const float* x, int G, float& mn,
+                                                   float& mx, float& scale) {
+    mn = 1e30f;
+    mx = -1e30f;
+    for (int i = 0; i < G; i += 4) {
+        float lmn = fmin_nan(fmin_nan(x[i], x[i + 1]), fmin_nan(x[i + 2], x[i + 3]));
+        float lmx = fmax_nan(fmax_nan(x[i], x[i + 1]), fmax_nan(x[i + 2], x[i + 3]));
+        mn = fmin_nan(mn, lmn);
+        mx = fmax_nan(mx, lmx);
+    }
+    finish_group(mn, mx, scale);
+}
+
+__global__ __launch_bounds__(kBlock) void quantize_serial_kernel(
+    const float* __restrict__ in, uint8_t* __restrict__ packed,
+    float* __restrict__ scales, float* __restrict__ zeros, int64_t n_groups, int G) {
+    const int64_t g = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (g >= n_groups) return;
+    const float* x = in + g * G;
+    float mn, mx, scale;
+    serial_group_stats(x, G, mn, mx, scale);
+    scales[g] = scale;
+    zeros[g] = mn;
+    uint8_t* o = packed + g * (G / 4);
+    for (int j = 0; j < G / 4; ++j)
+        o[j] = (uint8_t)encode4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3], mn, scale);
+}
+
+__global__ __launch_bounds__(kBlock) void roundtrip_serial_kernel(
+    const float* __restrict__ in, float* __restrict__ out, int64_t n_groups, int G) {
+    const int64_t g = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (g >= n_groups) return;
+    const float* x = in + g * G;
+    float* o = out + g * G;
+    float mn, mx, scale;
+    serial_group_stats(x, G, mn, mx, scale);
+    for (int j = 0; j < G / 4; ++j) {
+        const uint32_t b = encode4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3], mn, scale);
+        const float4 d = decode4(b, scale, mn);
+        o[4 * j] = d.x;
+        o[4 * j + 1] = d.y;
+        o[4 * j + 2] = d.z;
+        o[4 * j + 3] = d.w;
+    }
+}
+
+// ----------------------------------------------------------------------------
+// Dequantise: one lane per packed byte -> one float4 (lane-contiguous 16 B
+// stores, so each store instruction writes 1 KiB).  BPG = G/4 bytes per group
+// when it is a power of two (shift), 0 for the generic divide.
+// ----------------------------------------------------------------------------
+template <int BPG, bool kAligned>
+__global__ __launch_bounds__(kBlock) void dequantize_kernel(
+    const uint8_t* __restrict__ packed, const float* __restrict__ scales,
+    const float* __restrict__ zeros, float* __restrict__ out, int64_t n_bytes, int bpg) {
+    const int64_t base = (int64_t)blockIdx.x * (kBlock * kUnroll) + threadIdx.x;
+    uint32_t b[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t idx = base + (int64_t)u * kBlock;
+        b[u] = idx < n_bytes ? (uint32_t)packed[idx] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int64_t idx = base + (int64_t)u * kBlock;
+        if (idx >= n_bytes) continue;
+        const int64_t g = BPG ? (idx / BPG) : (idx / bpg);
+        const float4 d = decode4(b[u], scales[g], zeros[g]);
+        if constexpr (kAligned) {
+            reinterpret_cast<float4*>(out)[idx] = d;
+        } else {
+            out[4 * idx] = d.x;
+            out[4 * idx + 1] = d.y;
+            out[4 * idx + 2] = d.z;
+            out[4 * idx + 3] = d.w;
+        }
+    }
+}
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+inline unsigned grid_for(int64_t items, int64_t per_block) {
+    return (unsigned)((items + per_block - 1) / per_block);
+}
+
+int check_common(const void* a, const void* b, int64_t n_groups, int32_t G) {
+    if (a == nullptr || b == nullptr)
+        return set_error(kErrInvalidArgument, "null tensor pointer");
+    if (G <= 0 || G % 4 != 0)
+        return set_error(kErrInvalidArgument,
+                         "group_size must be positive and divisible by 4, got %d", G);
+    if (n_groups <= 0)
+        return set_error(kErrInvalidArgument, "number of groups must be positive, got %lld",
+                         (long long)n_groups);
+    if (n_groups > (int64_t(1) << 40) / G)
+        return set_error(kErrInvalidArgument, "tensor too large");
+    return kOk;
+}
+
+}  // namespace
+
+// ----------------------------------------------------------------------------
+// Launchers shared with the store kernels.
+// ----------------------------------------------------------------------------
+int launch_quantize_groups(const float* in, uint8_t* packed, float* scales, float* zeros,
+                           int64_t n_groups, int32_t G, hipStream_t stream) {
+    int rc = check_common(in, packed, n_groups, G);
+    if (rc) return rc;
+    if (scales == nullptr || zeros == nullptr)
+        return set_error(kErrInvalidArgument, "null scales/zeros pointer");
+    const int lanes = G / 4;
+    const int64_t n_vec = n_groups * lanes;
+    const bool pow2 = (lanes & (lanes - 1)) == 0 && lanes <= kWave;
+    if (pow2 && aligned16(in)) {
+        const unsigned grid = grid_for(n_vec, kBlock * kUnroll);
+        const float4* in4 = reinterpret_cast<const float4*>(in);
+        switch (lanes) {
+#define KIVI_Q(L) case L: quantize_seg_kernel<L><<<grid, kBlock, 0, stream>>>(in4, packed, scales, zeros, n_vec); break;
+            KIVI_Q(1) KIVI_Q(2) KIVI_Q(4) KIVI_Q(8) KIVI_Q(16) KIVI_Q(32) KIVI_Q(64)
+#undef KIVI_Q
+        }
+    } else {
+        quantize_serial_kernel<<<grid_for(n_groups, kBlock), kBlock, 0, stream>>>(
+            in, packed, scales, zeros, n_groups, G);
+    }
+    return check_launch("quantize");
+}
+
+int launch_roundtrip_groups(const float* in, float* out, int64_t n_groups, int32_t G,
+                            hipStream_t stream) {
+    int rc = check_common(in, out, n_groups, G);
+    if (rc) return rc;
+    const int lanes = G / 4;
+    const int64_t n_vec = n_groups * lanes;
+    const bool pow2 = (lanes & (lanes - 1)) == 0 && lanes <= kWave;
+    if (pow2 && aligned16(in) && aligned16(out)) {
+        const unsigned grid = grid_for(n_vec, kBlock * kUnroll);
+        const float4* in4 = reinterpret_cast<const float4*>(in);
+        float4* out4 = reinterpret_cast<float4*>(out);
+        switch (lanes) {
+#define KIVI_R(L) case L: roundtrip_seg_kernel<L><<<grid, kBlock, 0, stream>>>(in4, out4, n_vec); break;
+            KIVI_R(1) KIVI_R(2) KIVI_R(4) KIVI_R(8) KIVI_R(16) KIVI_R(32) KIVI_R(64)
+#undef KIVI_R
+        }
+    } else {
+        roundtrip_serial_kernel<<<grid_for(n_groups, kBlock), kBlock, 0, stream>>>(
+            in, out, n_groups, G);
+    }
+    return check_launch("quant_dequant_roundtrip");
+}
+
+int launch_dequantize_groups(const uint8_t* packed, const float* scales, const float* zeros,
+                             float* out, int64_t n_groups, int32_t G, hipStream_t stream) {
+    int rc = check_common(packed, out, n_groups, G);
+    if (rc) return rc;
+    if (scales == nullptr || zeros == nullptr)
+        return set_error(kErrInvalidArgument, "null scales/zeros pointer");
+    const int bpg = G / 4;
+    const int64_t n_bytes = n_groups * bpg;
+    const unsigned grid = grid_for(n_bytes, kBlock * kUnroll);
+    const bool al = aligned16(out);
+    switch (bpg) {
+#define KIVI_D(L) case L: \
+        if (al) dequantize_kernel<L, true><<<grid, kBlock, 0, stream>>>(packed, scales, zeros, out, n_bytes, bpg); \
+        else dequantize_kernel<L, false><<<grid, kBlock, 0, stream>>>(packed, scales, zeros, out, n_bytes, bpg); \
+        break;
+        KIVI_D(1) KIVI_D(2) KIVI_D(4) KIVI_D(8) KIVI_D(16) KIVI_D(32) KIVI_D(64)
+#undef KIVI_D
+        default:
+            if (al) dequantize_kernel<0, true><<<grid, kBlock, 0, stream>>>(packed, scales, zeros, out, n_bytes, bpg);
+            else dequantize_kernel<0, false><<<grid, kBlock, 0, stream>>>(packed, scales, zeros, out, n_bytes, bpg);
+    }
+    return check_launch("dequantize");
+}
+
+}  // namespace kivi
+
+using namespace kivi;
+
+static int check_values(int64_t num_tokens, int32_t head_dim, int32_t G) {
+    if (G <= 0 || G % 4 != 0)
+        return set_error(kErrInvalidArgument,
+                         "group_size must be positive and divisible by 4, got %d", G);
+    if (head_dim <= 0 || head_dim % G != 0)
+        return set_error(kErrInvalidArgument,
+                         "head_dim must be positive and divisible by group_size");
+    if (num_tokens <= 0)
+        return set_error(kErrInvalidArgument, "input must be non-empty");
+    return kOk;
+}
+
+extern "C" {
+
+int kivi_quantize_keys_per_channel(const float* input, uint8_t* output, float* scales,
+                                   float* zeros, int64_t num_channels, int32_t group_size,
+                                   void* stream) {
+    return launch_quantize_groups(input, output, scales, zeros, num_channels, group_size,
+                                  (hipStream_t)stream);
+}
+
+int kivi_quantize_values_per_token(const float* input, uint8_t* output, float* scales,
+                                   float* zeros, int64_t num_tokens, int32_t head_dim,
+                                   int32_t group_size, void* stream) {
+    int rc = check_values(num_tokens, head_dim, group_size);
+    if (rc) return rc;
+    return launch_quantize_groups(input, output, scales, zeros,
+                                  num_tokens * (head_dim / group_size), group_size,
+                                  (hipStream_t)stream);
+}
+
+int kivi_dequantize_keys_per_channel(const uint8_t* input, const float* scales,
+                                     const float* zeros, float* output, int64_t num_channels,
+                                     int32_t group_size, void* stream) {
+    return launch_dequantize_groups(input, scales, zeros, output, num_channels, group_size,
+                                    (hipStream_t)stream);
+}
+
+int kivi_dequantize_values_per_token(const uint8_t* input, const float* scales,
+                                     const float* zeros, float* output, int64_t num_groups,
+                                     int32_t group_size, void* stream) {
+    return launch_dequantize_groups(input, scales, zeros, output, num_groups, group_size,
+                                    (hipStream_t)stream);
+}
+
+int kivi_quant_dequant_roundtrip_keys(const float* input, float* output,
+                                      int64_t num_channels, int32_t group_size,
+                                      void* stream) {
+    return launch_roundtrip_groups(input, output, num_channels, group_size,
+                                   (hipStream_t)stream);
+}
+
+int kivi_quant_dequant_roundtrip_values(const float* input, float* output,
+                                        int64_t num_tokens, int32_t head_dim,
+                                        int32_t group_size, void* stream) {
+    int rc = check_values(num_tokens, head_dim, group_size);
+    if (rc) return rc;
+    return launch_roundtrip_groups(input, output, num_tokens * (head_dim / group_size),
+                                   group_size, (hipStream_t)stream);
+}
+
+}  // extern "C"

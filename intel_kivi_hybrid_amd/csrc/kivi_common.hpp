@@ -1,0 +1,169 @@
+// Shared host/device helpers for the gfx950 KIVI kernels.
+//
+// Numerics contract (reference: src/csrc/kernels/internal/quant_tile.hpp:35-91,
+// src/csrc/kernels/quantize_kernels.cpp:46-48,
+// src/csrc/kernels/dequantize_kernels.cpp:17-28), read as IEEE fp32:
+//   min/max over a group, NaN ignored, -0.0 ordered below +0.0, folded with the
+//   reference's initial values 1e30f / -1e30f;
+//   scale = (max - min) / 3.0f + 1e-10f (correctly rounded divide), zero = min;
+//   code  = clamp(round_half_away((x - min) / scale), 0, 3), NaN -> 0;
+//   x_hat = fl(fl(code * scale) + zero) (never fused into an FMA).
+// The whole library is compiled with -ffp-contract=off and
+// -fhip-fp32-correctly-rounded-divide-sqrt; kernels that want FMAs call fmaf.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kivi {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Host-side status plumbing (defined in kivi_runtime.hip).
+// ---------------------------------------------------------------------------
+enum Status : int {
+    kOk = 0,
+    kErrInvalidArgument = 1,
+    kErrLaunch = 2,
+    kErrRuntime = 3,
+    kErrUnsupported = 4,
+};
+
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+int check_hip(hipError_t err, const char* what);
+
+// ---------------------------------------------------------------------------
+// Device helpers.
+// ---------------------------------------------------------------------------
+
+// fmin/fmax with NaN ignored.  v_min_f32 / v_max_f32 order -0.0 below +0.0.
+__device__ __forceinline__ float fmin_nan(float a, float b) { return fminf(a, b); }
+__device__ __forceinline__ float fmax_nan(float a, float b) { return fmaxf(a, b); }
+
+// Cross-lane exchange helpers within a wave64.  `seg_partner<M>` returns the value
+// held by lane (lane ^ M).  Masks 1 and 2 use DPP quad permutes, 4 and 8 use
+// the row half-mirror / mirror (valid for reductions once the smaller
+// sub-segments already hold their reduced value), 16 and 32 use ds_swizzle /
+// ds_bpermute.
+template <int M>
+__device__ __forceinline__ float seg_partner(float v) {
+    int x = __builtin_bit_cast(int, v);
+    int r;
+    if constexpr (M == 1) {
+        r = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+    } else if constexpr (M == 2) {
+        r = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+    } else if constexpr (M == 4) {
+        r = __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    } else if constexpr (M == 8) {
+        r = __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false);  // row_mirror
+    } else if constexpr (M == 16) {
+        r = __builtin_amdgcn_ds_swizzle(x, 0x401F);                      // bitmask xor 0x10
+    } else {
+        static_assert(M == 32, "segment partner mask");
+        r = __shfl_xor(x, 32);
+    }
+    return __builtin_bit_cast(float, r);
+}
+
+// Reduce min and max over aligned segments of LANES consecutive lanes
+// (LANES a power of two <= 64).  Every lane of a segment ends with the result.
+template <int LANES>
+__device__ __forceinline__ void seg_min_max(float& mn, float& mx) {
+    if constexpr (LANES >= 2) {
+        mn = fmin_nan(mn, seg_partner<1>(mn));
+        mx = fmax_nan(mx, seg_partner<1>(mx));
+    }
+    if constexpr (LANES >= 4) {
+        mn = fmin_nan(mn, seg_partner<2>(mn));
+        mx = fmax_nan(mx, seg_partner<2>(mx));
+    }
+    if constexpr (LANES >= 8) {
+        mn = fmin_nan(mn, seg_partner<4>(mn));
+        mx = fmax_nan(mx, seg_partner<4>(mx));
+    }
+    if constexpr (LANES >= 16) {
+        mn = fmin_nan(mn, seg_partner<8>(mn));
+        mx = fmax_nan(mx, seg_partner<8>(mx));
+    }
+    if constexpr (LANES >= 32) {
+        mn = fmin_nan(mn, seg_partner<16>(mn));
+        mx = fmax_nan(mx, seg_partner<16>(mx));
+    }
+    if constexpr (LANES >= 64) {
+        mn = fmin_nan(mn, seg_partner<32>(mn));
+        mx = fmax_nan(mx, seg_partner<32>(mx));
+    }
+}
+
+// Fold the reference's initial values (quant_tile.hpp:39-40) and form the
+// group's scale (quantize_kernels.cpp:46).
+__device__ __forceinline__ void finish_group(float& mn, float& mx, float& scale) {
+    mn = fmin_nan(mn, 1e30f);
+    mx = fmax_nan(mx, -1e30f);
+    scale = (mx - mn) / 3.0f + 1e-10f;
+}
+
+// Exact code of one element: clamp(round_half_away((x-min)/scale), 0, 3).
+__device__ __forceinline__ uint32_t code_exact(float x, float mn, float scale) {
+    float t = (x - mn) / scale;                  // correctly rounded
+    float r = roundf(t);                         // half away from zero
+    r = fminf(fmaxf(r, 0.0f), 3.0f);             // NaN -> 0
+    return (uint32_t)r;
+}
+
+// Codes of four elements of one group.  Fast path: the quotient from a 1-ulp
+// reciprocal differs from the correctly rounded one by < 1e-6 (t <= ~3), so
+// unless u = t + 0.5 lies within kTieGuard of an integer the rounding
+// decision is the same; any lane that is that close (or whose scale is outside
+// the range where v_rcp_f32 is accurate) recomputes with the exact divide.
+constexpr float kTieGuard = 4e-6f;
+
+__device__ __forceinline__ uint32_t encode4(float x0, float x1, float x2, float x3,
+                                            float mn, float scale) {
+    const float r = __builtin_amdgcn_rcpf(scale);
+    float u0 = fmaf(x0 - mn, r, 0.5f);
+    float u1 = fmaf(x1 - mn, r, 0.5f);
+    float u2 = fmaf(x2 - mn, r, 0.5f);
+    float u3 = fmaf(x3 - mn, r, 0.5f);
+    float d0 = fabsf(__builtin_amdgcn_fractf(u0) - 0.5f);
+    float d1 = fabsf(__builtin_amdgcn_fractf(u1) - 0.5f);
+    float d2 = fabsf(__builtin_amdgcn_fractf(u2) - 0.5f);
+    float d3 = fabsf(__builtin_amdgcn_fractf(u3) - 0.5f);
+    float dmax = fmaxf(fmaxf(d0, d1), fmaxf(d2, d3));
+    const bool ok_scale = (scale >= 1e-10f) && (scale <= 0x1.0p120f);
+    uint32_t q0, q1, q2, q3;
+    if (__builtin_expect(!(dmax < 0.5f - kTieGuard) || !ok_scale, 0)) {
+        // NaN dmax (a NaN quotient) also lands here; the exact path maps it to 0.
+        q0 = code_exact(x0, mn, scale);
+        q1 = code_exact(x1, mn, scale);
+        q2 = code_exact(x2, mn, scale);
+        q3 = code_exact(x3, mn, scale);
+    } else {
+        // fmaxf first so that a NaN element (whose NaN distance fmaxf dropped
+        // above) still yields code 0, as the exact path does.
+        q0 = (uint32_t)fminf(fmaxf(u0, 0.0f), 3.0f);
+        q1 = (uint32_t)fminf(fmaxf(u1, 0.0f), 3.0f);
+        q2 = (uint32_t)fminf(fmaxf(u2, 0.0f), 3.0f);
+        q3 = (uint32_t)fminf(fmaxf(u3, 0.0f), 3.0f);
+    }
+    return q0 | (q1 << 2) | (q2 << 4) | (q3 << 6);
+}
+
+// x_hat = fl(fl(q * scale) + zero) (dequantize_kernels.cpp:24).
+__device__ __forceinline__ float decode1(uint32_t q, float scale, float zero) {
+    return __fadd_rn(__fmul_rn((float)q, scale), zero);
+}
+
+__device__ __forceinline__ float4 decode4(uint32_t byte, float scale, float zero) {
+    float4 o;
+    o.x = decode1(byte & 3u, scale, zero);
+    o.y = decode1((byte >> 2) & 3u, scale, zero);
+    o.z = decode1((byte >> 4) & 3u, scale, zero);
+    o.w = decode1((byte >> 6) & 3u, scale, zero);
+    return o;
+}
+
+}  // namespace kivi

@@ -1,0 +1,47 @@
+"""Test infrastructure only: float64 decode attention over a KIVI cache.
+
+The reference has no attention kernel.  Its attention semantics are what its
+test states explicitly -- ``softmax(Q K^T * D^-0.5) V`` over the dequantised
+keys/values (tests/integration/test_attention_fix.py:40-43,91-93) -- and what
+the HF model computes over ``get_full_cache()`` (dequantised history followed
+by the fp32 residual window, src/kivi_sycl/cache/manager.py:263-288).  Query
+head ``h`` reads kv head ``h // (Hq // Hkv)`` (HF ``repeat_kv``).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def decode_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None):
+    """q: [B, Hq, D]; k_hist/v_hist: [B, Hkv, Tq, D] dequantised history;
+    k_res/v_res: [B, Hkv, Tr, D] fp32 residual.  Returns o [B, Hq, D] float64.
+
+    Works one (batch, kv-head) at a time so that long contexts fit in memory.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    B, Hq, D = q.shape
+    Hkv = k_hist.shape[1] if k_hist is not None else k_res.shape[1]
+    if Hq % Hkv:
+        raise ValueError("Hq must be a multiple of Hkv")
+    g = Hq // Hkv
+    scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
+    out = np.empty((B, Hq, D), dtype=np.float64)
+    for b in range(B):
+        for kh in range(Hkv):
+            parts_k, parts_v = [], []
+            if k_hist is not None and k_hist.shape[2]:
+                parts_k.append(np.asarray(k_hist[b, kh], dtype=np.float64))
+                parts_v.append(np.asarray(v_hist[b, kh], dtype=np.float64))
+            if k_res is not None and k_res.shape[2]:
+                parts_k.append(np.asarray(k_res[b, kh], dtype=np.float64))
+                parts_v.append(np.asarray(v_res[b, kh], dtype=np.float64))
+            K = np.concatenate(parts_k, axis=0)          # [T, D]
+            V = np.concatenate(parts_v, axis=0)
+            qh = q[b, kh * g:(kh + 1) * g]               # [g, D]
+            s = (qh @ K.T) * scale                       # [g, T]
+            s -= s.max(axis=1, keepdims=True)
+            p = np.exp(s)
+            p /= p.sum(axis=1, keepdims=True)
+            out[b, kh * g:(kh + 1) * g] = p @ V
+    return out

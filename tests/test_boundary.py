@@ -1,0 +1,165 @@
+"""CPU tests of the drop-in boundary: the C-ABI library loads and exports every
+symbol include/kivi_hip.h declares, and the Python ``_C`` facade validates
+arguments exactly like the reference (src/csrc/ops/kv_cache_ops.cpp:19-171,
+src/csrc/include/kivi/common.hpp:64-75) without touching a GPU.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from tests.conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "kivi_hip.h")
+
+
+def _declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kivi_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = _declared_symbols()
+    for required in ("kivi_quantize_keys_per_channel", "kivi_quantize_values_per_token",
+                     "kivi_dequantize_keys_per_channel", "kivi_dequantize_values_per_token",
+                     "kivi_quant_dequant_roundtrip_keys",
+                     "kivi_quant_dequant_roundtrip_values",
+                     "kivi_event_record", "kivi_event_wait", "kivi_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    from intel_kivi_hybrid_amd import _native
+    lib = ctypes.CDLL(_native.LIB_PATH)
+    missing = [n for n in _declared_symbols() if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+    # and the Python binding binds exactly the declared set
+    assert sorted(_native.SIGNATURES) == _declared_symbols()
+
+
+def test_abi_version_and_error_string():
+    from intel_kivi_hybrid_amd import _native
+    lib = _native.load()
+    assert lib.kivi_abi_version() == 1
+    # invalid arguments are rejected on the host, before any launch
+    rc = lib.kivi_quantize_keys_per_channel(None, None, None, None, 4, 32, None)
+    assert rc == 1 and "null" in _native.last_error()
+    buf = (ctypes.c_float * 8)()
+    rc = lib.kivi_quantize_keys_per_channel(ctypes.addressof(buf), ctypes.addressof(buf),
+                                            ctypes.addressof(buf), ctypes.addressof(buf),
+                                            1, 6, None)
+    assert rc == 1 and "divisible by 4, got 6" in _native.last_error()
+    rc = lib.kivi_quantize_values_per_token(ctypes.addressof(buf), ctypes.addressof(buf),
+                                            ctypes.addressof(buf), ctypes.addressof(buf),
+                                            2, 20, 8, None)
+    assert rc == 1 and "head_dim must be positive and divisible by group_size" in _native.last_error()
+
+
+# ----------------------------------------------------------------------------
+# Facade validation, message for message (CPU tensors: the device check is the
+# last check of check_tensor, so dtype/contiguity errors come first).
+# ----------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def C():
+    from intel_kivi_hybrid_amd import _C
+    return _C
+
+
+def _keys_args(dtype=torch.float32):
+    x = torch.zeros(1, 2, 4, 32, dtype=dtype)
+    packed = torch.empty(1, 2, 4, 8, dtype=torch.uint8)
+    scales = torch.empty(1, 2, 4)
+    zeros = torch.empty(1, 2, 4)
+    return x, packed, scales, zeros
+
+
+def test_device_check_message(C):
+    x, packed, scales, zeros = _keys_args()
+    with pytest.raises(RuntimeError, match=r"^input must be on cuda but got cpu$"):
+        C.quantize_keys(x, packed, scales, zeros, 32)
+
+
+def test_dtype_check_message(monkeypatch, C):
+    x, packed, scales, zeros = _keys_args(torch.float16)
+    with pytest.raises(RuntimeError, match=r"^input must be Float but got Half$"):
+        C.quantize_keys(x, packed, scales, zeros, 32)
+    # input passes check_tensor only on the expected device type
+    monkeypatch.setattr(C, "_DEVICE_TYPE", "cpu")
+    x, _, scales, zeros = _keys_args()
+    with pytest.raises(RuntimeError, match=r"^output must be Byte but got Float$"):
+        C.quantize_keys(x, torch.empty(1, 2, 4, 8), scales, zeros, 32)
+
+
+def test_contiguity_check_message(C):
+    x, packed, scales, zeros = _keys_args()
+    with pytest.raises(RuntimeError, match=r"^input must be contiguous$"):
+        C.quantize_keys(x.transpose(2, 3), packed, scales, zeros, 32)
+
+
+def test_all_twelve_ops_and_event_exist(C):
+    names = ["quantize_keys", "quantize_values", "dequantize_keys", "dequantize_values",
+             "quant_dequant_roundtrip_keys", "quant_dequant_roundtrip_values"]
+    for n in names:
+        assert callable(getattr(C, n)) and callable(getattr(C, n + "_async"))
+    assert hasattr(C.KiviEvent, "wait")
+
+
+def test_keyword_names_match_reference(C):
+    import inspect
+    sig = lambda f: list(inspect.signature(f).parameters)          # noqa: E731
+    assert sig(C.quantize_keys) == ["input", "output", "scales", "zeros", "group_size"]
+    assert sig(C.quantize_values) == ["input", "output", "scales", "zeros", "head_dim", "group_size"]
+    assert sig(C.dequantize_keys) == ["input", "scales", "zeros", "output", "group_size"]
+    assert sig(C.dequantize_values) == ["input", "scales", "zeros", "output", "head_dim", "group_size"]
+    assert sig(C.quant_dequant_roundtrip_keys) == ["input", "output", "group_size"]
+    assert sig(C.quant_dequant_roundtrip_values) == ["input", "output", "head_dim", "group_size"]
+    assert sig(C.quantize_keys_async) == sig(C.quantize_keys)
+
+
+def test_group_size_type_errors(C):
+    x, packed, scales, zeros = _keys_args()
+    with pytest.raises(TypeError):
+        C.quantize_keys(x, packed, scales, zeros, 32.0)
+
+
+# Size rules need device tensors to get past check_tensor; they are restated
+# here against the validators directly, with "meta"-free CPU tensors patched
+# through the private validators (same code path the ops call).
+def _on_fake_device(monkeypatch, C):
+    monkeypatch.setattr(C, "_DEVICE_TYPE", "cpu")
+
+
+def test_size_rule_messages(monkeypatch, C):
+    _on_fake_device(monkeypatch, C)
+    x, packed, scales, zeros = _keys_args()
+    with pytest.raises(RuntimeError, match=r"group_size must be positive and divisible by 4, got 6"):
+        C._validate_quant_keys(x, packed, scales, zeros, 6)
+    with pytest.raises(RuntimeError, match=r"zeros size \(3\) must match scales size \(8\)"):
+        C._validate_quant_keys(x, packed, scales, torch.empty(3), 32)
+    with pytest.raises(RuntimeError, match=r"input size \(256\) must equal num_channels\(8\) \* group_size\(16\) = 128"):
+        C._validate_quant_keys(x, packed, scales, zeros, 16)
+    with pytest.raises(RuntimeError, match=r"output size \(32\) must equal num_channels\(8\) \* \(group_size/4\) = 64"):
+        C._validate_quant_keys(x, torch.empty(32, dtype=torch.uint8), scales, zeros, 32)
+    with pytest.raises(RuntimeError, match=r"scales must be non-empty"):
+        C._validate_quant_keys(x, packed, torch.empty(0), torch.empty(0), 32)
+    v = torch.zeros(2, 3, 8, 64)
+    with pytest.raises(RuntimeError, match=r"head_dim must be positive and divisible by group_size"):
+        C._validate_quant_values(v, torch.empty(2, 3, 8, 16, dtype=torch.uint8),
+                                 torch.empty(96), torch.empty(96), 48, 32)
+    with pytest.raises(RuntimeError, match=r"refusing to silently truncate"):
+        C._validate_quant_values(torch.zeros(100), torch.empty(25, dtype=torch.uint8),
+                                 torch.empty(1), torch.empty(1), 64, 32)
+    with pytest.raises(RuntimeError, match=r"round-trip is shape-preserving"):
+        C._validate_roundtrip_keys(torch.zeros(64), torch.zeros(32), 32)
+    with pytest.raises(RuntimeError, match=r"input must be non-empty"):
+        C._validate_roundtrip_values(torch.zeros(0), torch.zeros(0), 64, 32)
+    # valid arguments return the launch count the kernels use
+    assert C._validate_quant_keys(x, packed, scales, zeros, 32) == 8
+    assert C._validate_quant_values(v, torch.empty(2, 3, 8, 16, dtype=torch.uint8),
+                                    torch.empty(96), torch.empty(96), 64, 32) == 48
+    assert C._validate_dequant_values(torch.empty(2, 3, 8, 16, dtype=torch.uint8),
+                                      torch.empty(96), torch.empty(96), v, 64, 32) == 96
