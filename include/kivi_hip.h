@@ -87,6 +87,60 @@ int kivi_quant_dequant_roundtrip_values(const float* input, float* output,
                                         int64_t num_tokens, int32_t head_dim,
                                         int32_t group_size, void* stream);
 
+/* ---- HBM-resident packed store --------------------------------------------
+ * Replaces KiviCache._flush_group (src/kivi_sycl/cache/manager.py:309-374):
+ * quantises the `group_size_k` oldest tokens of the fp32 residual ring of
+ * every (batch, kv-head) into chunk `chunk_index` of the packed store, on the
+ * device, without host copies.  Layout per (b, kv-head):
+ *   k_res, v_res    [res_capacity][head_dim] f32 ring; token t of the window
+ *                   sits at slot (res_start + t) % res_capacity
+ *   k_codes         [chunk_capacity][G][head_dim/4] u8 (byte (t,i) = channels
+ *                   4i..4i+3 of token t, channel 4i+k at bits 2k)
+ *   k_scale, k_zero [chunk_capacity][head_dim] f32 (per channel per chunk)
+ *   v_codes         [chunk_capacity][head_dim][G/4] u8 (byte (d,j) = tokens
+ *                   4j..4j+3 of channel d, token 4j+k at bits 2k)
+ *   v_scale, v_zero [chunk_capacity][G][head_dim/group_size_v] f32
+ * Codes, scales and zeros equal quantize_keys on the chunk's [D, G] transpose
+ * and quantize_values on its [G, D] rows.  If k_hist/v_hist are non-null
+ * ([hist_capacity][head_dim] f32 per (b, kv-head)) the dequantised tokens are
+ * also written at rows chunk_index*G .. +G-1 (bit-identical to the round-trip
+ * ops, manager.py:337-345).  Requires group_size_k * head_dim <= 65536. */
+int kivi_store_flush(const float* k_res, const float* v_res, uint8_t* k_codes,
+                     float* k_scale, float* k_zero, uint8_t* v_codes, float* v_scale,
+                     float* v_zero, float* k_hist, float* v_hist, int64_t hist_capacity,
+                     int32_t batch, int32_t kv_heads, int32_t head_dim,
+                     int32_t group_size_k, int32_t group_size_v, int32_t res_capacity,
+                     int32_t res_start, int32_t chunk_capacity, int32_t chunk_index,
+                     void* stream);
+
+/* ---- fused packed-KV decode attention -------------------------------------
+ * No reference counterpart (the reference runs HF attention on the CPU over
+ * the dequantised history, manager.py:251-290; its stated math is
+ * tests/integration/test_attention_fix.py:40-43).  For q [batch][q_heads]
+ * [head_dim] f32, computes out [batch][q_heads][head_dim] =
+ *   softmax(q . [K_hat ; K_res]^T * softmax_scale) . [V_hat ; V_res]
+ * over the first num_chunks chunks of the packed store (layout above) and the
+ * res_len residual tokens, query head h reading kv head h / (q_heads/kv_heads).
+ * num_splits <= 0 picks the split-K factor; workspace must hold
+ * kivi_packed_decode_attention_workspace_size(...) bytes (0 means none is
+ * needed and workspace may be NULL).  Supported: q_heads/kv_heads in
+ * {1,2,4,8}, head_dim % 16 == 0 and <= 256, group_size_k % 16 == 0 and <= 64. */
+size_t kivi_packed_decode_attention_workspace_size(int32_t batch, int32_t q_heads,
+                                                   int32_t kv_heads, int32_t head_dim,
+                                                   int32_t num_chunks, int32_t res_len,
+                                                   int32_t num_splits);
+
+int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const float* k_scale,
+                                 const float* k_zero, const uint8_t* v_codes,
+                                 const float* v_scale, const float* v_zero, const float* k_res,
+                                 const float* v_res, float* out, void* workspace,
+                                 size_t workspace_bytes, int32_t batch, int32_t q_heads,
+                                 int32_t kv_heads, int32_t head_dim, int32_t group_size_k,
+                                 int32_t group_size_v, int32_t chunk_capacity,
+                                 int32_t num_chunks, int32_t res_capacity, int32_t res_start,
+                                 int32_t res_len, float softmax_scale, int32_t num_splits,
+                                 void* stream);
+
 #ifdef __cplusplus
 }
 #endif

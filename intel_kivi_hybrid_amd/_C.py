@@ -386,3 +386,61 @@ def quant_dequant_roundtrip_keys_async(input, output, group_size):
 def quant_dequant_roundtrip_values_async(input, output, head_dim, group_size):
     """Non-blocking quant_dequant_roundtrip_values -- returns a KiviEvent."""
     return _roundtrip_values(input, output, head_dim, group_size, False)
+
+
+# --------------------------------------------------------------------------
+# Fused packed-KV decode attention (no reference counterpart; see
+# include/kivi_hip.h).  Not part of the reference's twelve ops.
+# --------------------------------------------------------------------------
+_ws_cache = {}
+
+
+def _workspace(device, nbytes: int):
+    if nbytes == 0:
+        return None
+    key = (str(device), torch.cuda.current_stream(device).cuda_stream)
+    buf = _ws_cache.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _ws_cache[key] = buf
+    return buf
+
+
+def packed_decode_attention(q, store, softmax_scale=None, out=None, num_splits=0,
+                            workspace=None):
+    """o = softmax(q . [K_hat; K_res]^T * scale) . [V_hat; V_res] for one query
+    token per sequence, straight from a :class:`PackedKVStore`.
+
+    q: [B, Hq, D] or [B, Hq, 1, D] fp32 on the store's device.  Returns
+    ``out`` ([B, Hq, D] fp32), launched on the current stream (asynchronous)."""
+    _check_tensor(q, "q", torch.float32)
+    B, Hq, D = store.B, q.shape[1], store.D
+    _check(q.dim() in (3, 4) and q.shape[0] == B and q.shape[-1] == D
+           and (q.dim() == 3 or q.shape[2] == 1),
+           "q must be [B, Hq, D] or [B, Hq, 1, D] matching the store, got ", tuple(q.shape))
+    _check(q.device == store.device, "q must be on the store's device")
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=torch.float32, device=q.device)
+    else:
+        _check_tensor(out, "out", torch.float32)
+        _check(out.numel() == B * Hq * D, "out must hold B*Hq*D elements")
+    scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
+    need = store.workspace_bytes(Hq, num_splits)
+    if workspace is None:
+        workspace = _workspace(q.device, need)
+    elif need:
+        _check(workspace.is_contiguous() and workspace.numel() * workspace.element_size() >= need,
+               "workspace must be contiguous and hold ", need, " bytes")
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    with torch.cuda.device(q.device):
+        _native.check(_lib.kivi_packed_decode_attention(
+            ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(store.k_codes.data_ptr()),
+            ctypes.c_void_p(store.k_scale.data_ptr()), ctypes.c_void_p(store.k_zero.data_ptr()),
+            ctypes.c_void_p(store.v_codes.data_ptr()), ctypes.c_void_p(store.v_scale.data_ptr()),
+            ctypes.c_void_p(store.v_zero.data_ptr()), ctypes.c_void_p(store.k_res.data_ptr()),
+            ctypes.c_void_p(store.v_res.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+            ctypes.c_void_p(workspace.data_ptr() if workspace is not None else 0), ws_bytes,
+            B, Hq, store.H, D, store.G, store.Gv, store.capacity, store.n_chunks, store.R,
+            store.res_start, store.res_len, scale, int(num_splits),
+            ctypes.c_void_p(_stream_of(q.device))), "packed_decode_attention")
+    return out

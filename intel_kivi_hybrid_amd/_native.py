@@ -36,11 +36,18 @@ SIGNATURES = {
     "kivi_dequantize_values_per_token": [_vp, _vp, _vp, _vp, _i64, _i32, _vp],
     "kivi_quant_dequant_roundtrip_keys": [_vp, _vp, _i64, _i32, _vp],
     "kivi_quant_dequant_roundtrip_values": [_vp, _vp, _i64, _i32, _i32, _vp],
+    "kivi_store_flush": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+                         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+    "kivi_packed_decode_attention_workspace_size": [_i32, _i32, _i32, _i32, _i32, _i32, _i32],
+    "kivi_packed_decode_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                     _vp, ctypes.c_size_t, _i32, _i32, _i32, _i32, _i32,
+                                     _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp],
 }
 
 _RESTYPES = {
     "kivi_last_error": ctypes.c_char_p,
     "kivi_clear_error": None,
+    "kivi_packed_decode_attention_workspace_size": ctypes.c_size_t,
 }
 
 _lib = None

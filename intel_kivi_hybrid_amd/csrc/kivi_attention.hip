@@ -1,0 +1,423 @@
+// Fused packed-KV decode attention for gfx950.
+//
+// No reference counterpart: the reference dequantises every flushed chunk back
+// to an fp32 CPU history (src/kivi_sycl/cache/manager.py:362-374) and lets the
+// HF model run ordinary attention over [history || residual]
+// (manager.py:251-290; the math it relies on is stated in
+// tests/integration/test_attention_fix.py:40-43,91-93).  This kernel computes
+//   o[h] = softmax(q[h] . [K_hat ; K_res]^T * scale) . [V_hat ; V_res]
+// for one query token per sequence directly from the packed store
+// (kivi_store.hip layout) and the fp32 residual ring, without materialising
+// K_hat / V_hat.  Query head h reads kv head h / (Hq / Hkv) (HF repeat_kv).
+//
+// Dequantisation is factored out of the inner loops:
+//   q . k_hat(t) = sum_d (q_d * ks_d) * code_dt + sum_d q_d * kz_d
+//   p . v_hat(d) = sum_t p_t * (code_td * vs_t,g(d) + vz_t,g(d))
+// Work split: the context is cut into units (a quantised chunk of G tokens, or
+// up to 64 residual tokens); a workgroup takes a contiguous range of units
+// (split-K), each of its 4 waves keeps its own online-softmax state over its
+// units, the waves merge through LDS, and a second kernel merges the splits
+// with log-sum-exp weights when there is more than one.  Scores are kept in the
+// log2 domain (q is pre-scaled by scale * log2(e)) so exp is a single v_exp_f32.
+#include <math.h>
+
+#include "kivi_common.hpp"
+#include "../../include/kivi_hip.h"
+
+namespace kivi {
+namespace {
+
+constexpr int kAttnWaves = 4;
+constexpr int kAttnBlock = kAttnWaves * kWave;
+constexpr int kMaxD = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct AttnArgs {
+    const float* q;
+    const uint8_t* k_codes;
+    const float* k_scale;
+    const float* k_zero;
+    const uint8_t* v_codes;
+    const float* v_scale;
+    const float* v_zero;
+    const float* k_res;
+    const float* v_res;
+    float* out;
+    float* part_o;     // [B, Hq, S, D]
+    float* part_ml;    // [B, Hq, S, 2]
+    int Hq, Hkv, D, G, Gv, Cmax, n_chunks, Rcap, res_start, res_len;
+    int n_units, n_splits, units_per_split;
+    float qscale;      // softmax scale * log2(e)
+};
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+
+__device__ __forceinline__ int ring_slot(int start, int t, int cap) {
+    int s = start + t;
+    return s >= cap ? s - cap : s;
+}
+
+template <int HG>
+__global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
+    extern __shared__ float smem[];
+    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int D = a.D, G = a.G;
+    const int wave_floats = HG * D + HG * kWave;
+    float* sq = smem;                                      // [HG][D]
+    float* sqs = smem + HG * D + wave * wave_floats;       // [HG][D]  q * k_scale
+    float* sp = sqs + HG * D;                              // [HG][64] probabilities
+    const int64_t bh = (int64_t)b * a.Hkv + kvh;
+
+    for (int e = threadIdx.x; e < HG * D; e += kAttnBlock) {
+        const int h = e / D, d = e % D;
+        sq[e] = a.q[((int64_t)b * a.Hq + kvh * HG + h) * D + d] * a.qscale;
+    }
+    __syncthreads();
+
+    float m[HG], l[HG], o[HG][kMaxD / kWave];
+#pragma unroll
+    for (int h = 0; h < HG; ++h) {
+        m[h] = -INFINITY;
+        l[h] = 0.f;
+#pragma unroll
+        for (int j = 0; j < kMaxD / kWave; ++j) o[h][j] = 0.f;
+    }
+
+    const int u_begin = split * a.units_per_split;
+    const int u_end = min(u_begin + a.units_per_split, a.n_units);
+    for (int u = u_begin + wave; u < u_end; u += kAttnWaves) {
+        float s[HG];
+        bool valid;
+        const bool quant = u < a.n_chunks;
+        const int64_t cid = bh * a.Cmax + u;
+        int rbase = 0, rcount = 0;
+        if (quant) {
+            // q * k_scale for this chunk, and the zero-point term per head.
+            float bpart[HG];
+#pragma unroll
+            for (int h = 0; h < HG; ++h) bpart[h] = 0.f;
+            for (int d = lane; d < D; d += kWave) {
+                const float ks = a.k_scale[cid * D + d], kz = a.k_zero[cid * D + d];
+#pragma unroll
+                for (int h = 0; h < HG; ++h) {
+                    const float qv = sq[h * D + d];
+                    sqs[h * D + d] = qv * ks;
+                    bpart[h] = fmaf(qv, kz, bpart[h]);
+                }
+            }
+            float bias[HG];
+#pragma unroll
+            for (int h = 0; h < HG; ++h) bias[h] = wave_sum(bpart[h]);
+            wave_sync();
+            const int t = lane;
+            valid = t < G;
+            float acc[HG];
+#pragma unroll
+            for (int h = 0; h < HG; ++h) acc[h] = 0.f;
+            if (valid) {
+                const uint32_t* kc =
+                    reinterpret_cast<const uint32_t*>(a.k_codes + (cid * G + t) * (D / 4));
+                for (int w4 = 0; w4 < D / 16; ++w4) {
+                    const uint32_t w = kc[w4];
+                    // dword w4 holds channels 16*w4 .. 16*w4+15; byte j bits 2k
+                    // hold channel 16*w4 + 4j + k.
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const uint32_t mk = (w >> (2 * k)) & 0x03030303u;
+                        const float c0 = (float)(mk & 0xff), c1 = (float)((mk >> 8) & 0xff);
+                        const float c2 = (float)((mk >> 16) & 0xff), c3 = (float)(mk >> 24);
+                        const int ch = 16 * w4 + k;
+#pragma unroll
+                        for (int h = 0; h < HG; ++h) {
+                            const float* qs = sqs + h * D + ch;
+                            acc[h] = fmaf(qs[0], c0, acc[h]);
+                            acc[h] = fmaf(qs[4], c1, acc[h]);
+                            acc[h] = fmaf(qs[8], c2, acc[h]);
+                            acc[h] = fmaf(qs[12], c3, acc[h]);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < HG; ++h) s[h] = valid ? acc[h] + bias[h] : -INFINITY;
+        } else {
+            rbase = (u - a.n_chunks) * kWave;
+            rcount = min(kWave, a.res_len - rbase);
+            const int t = rbase + lane;
+            valid = lane < rcount;
+            float acc[HG];
+#pragma unroll
+            for (int h = 0; h < HG; ++h) acc[h] = 0.f;
+            if (valid) {
+                const float4* kr = reinterpret_cast<const float4*>(
+                    a.k_res + (bh * a.Rcap + ring_slot(a.res_start, t, a.Rcap)) * D);
+                for (int d4 = 0; d4 < D / 4; ++d4) {
+                    const float4 kv = kr[d4];
+#pragma unroll
+                    for (int h = 0; h < HG; ++h) {
+                        const float* qh = sq + h * D + 4 * d4;
+                        acc[h] = fmaf(qh[0], kv.x, acc[h]);
+                        acc[h] = fmaf(qh[1], kv.y, acc[h]);
+                        acc[h] = fmaf(qh[2], kv.z, acc[h]);
+                        acc[h] = fmaf(qh[3], kv.w, acc[h]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < HG; ++h) s[h] = valid ? acc[h] : -INFINITY;
+        }
+
+        // Online softmax (log2 domain).
+#pragma unroll
+        for (int h = 0; h < HG; ++h) {
+            const float mnew = fmaxf(m[h], wave_max(s[h]));
+            const float alpha = exp2f(m[h] - mnew);
+            const float p = valid ? exp2f(s[h] - mnew) : 0.f;
+            l[h] = l[h] * alpha + wave_sum(p);
+            m[h] = mnew;
+#pragma unroll
+            for (int j = 0; j < kMaxD / kWave; ++j) o[h][j] *= alpha;
+            sp[h * kWave + lane] = p;
+        }
+        wave_sync();
+
+        if (quant) {
+            const int gpt = D / a.Gv;
+#pragma unroll
+            for (int j = 0; j < kMaxD / kWave; ++j) {
+                const int d = lane + kWave * j;
+                if (d >= D) break;
+                const int gd = d / a.Gv;
+                const uint32_t* vc =
+                    reinterpret_cast<const uint32_t*>(a.v_codes + (cid * D + d) * (G / 4));
+                const float* vs = a.v_scale + cid * G * gpt + gd;
+                const float* vz = a.v_zero + cid * G * gpt + gd;
+                for (int w4 = 0; w4 < G / 16; ++w4) {
+                    const uint32_t w = vc[w4];
+#pragma unroll
+                    for (int byte = 0; byte < 4; ++byte) {
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            const int tok = 16 * w4 + 4 * byte + k;
+                            const uint32_t c = (w >> (8 * byte + 2 * k)) & 3u;
+                            const float vh = decode1(c, vs[tok * gpt], vz[tok * gpt]);
+#pragma unroll
+                            for (int h = 0; h < HG; ++h)
+                                o[h][j] = fmaf(sp[h * kWave + tok], vh, o[h][j]);
+                        }
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kMaxD / kWave; ++j) {
+                const int d = lane + kWave * j;
+                if (d >= D) break;
+                for (int tt = 0; tt < rcount; ++tt) {
+                    const float vv =
+                        a.v_res[(bh * a.Rcap + ring_slot(a.res_start, rbase + tt, a.Rcap)) * D + d];
+#pragma unroll
+                    for (int h = 0; h < HG; ++h)
+                        o[h][j] = fmaf(sp[h * kWave + tt], vv, o[h][j]);
+                }
+            }
+        }
+        wave_sync();
+    }
+
+    // ---- merge the waves' states through LDS -------------------------------
+    __syncthreads();
+    float* mine = smem + HG * D + wave * wave_floats;      // [HG][D] o, then [HG] m, [HG] l
+#pragma unroll
+    for (int h = 0; h < HG; ++h) {
+#pragma unroll
+        for (int j = 0; j < kMaxD / kWave; ++j) {
+            const int d = lane + kWave * j;
+            if (d < D) mine[h * D + d] = o[h][j];
+        }
+        if (lane == 0) {
+            mine[HG * D + h] = m[h];
+            mine[HG * D + HG + h] = l[h];
+        }
+    }
+    __syncthreads();
+    const int64_t hq0 = (int64_t)b * a.Hq + kvh * HG;
+    for (int e = threadIdx.x; e < HG * D; e += kAttnBlock) {
+        const int h = e / D, d = e % D;
+        float M = -INFINITY;
+        for (int w = 0; w < kAttnWaves; ++w)
+            M = fmaxf(M, smem[HG * D + w * wave_floats + HG * D + h]);
+        float acc = 0.f, L = 0.f;
+        for (int w = 0; w < kAttnWaves; ++w) {
+            const float* reg = smem + HG * D + w * wave_floats;
+            const float mw = reg[HG * D + h];
+            const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
+            acc = fmaf(f, reg[h * D + d], acc);
+            L = fmaf(f, reg[HG * D + HG + h], L);
+        }
+        if (a.n_splits == 1) {
+            a.out[(hq0 + h) * D + d] = acc / L;
+        } else {
+            const int64_t row = (hq0 + h) * a.n_splits + split;
+            a.part_o[row * D + d] = acc;
+            if (d == 0) {
+                a.part_ml[row * 2] = M;
+                a.part_ml[row * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+// Merge split partials: grid (Hq, B), one thread per channel.
+__global__ __launch_bounds__(kMaxD) void attn_merge_kernel(const float* __restrict__ part_o,
+                                                           const float* __restrict__ part_ml,
+                                                           float* __restrict__ out, int Hq,
+                                                           int D, int S) {
+    const int64_t row = (int64_t)blockIdx.y * Hq + blockIdx.x;
+    const float* ml = part_ml + row * S * 2;
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s) M = fmaxf(M, ml[2 * s]);
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        float acc = 0.f, L = 0.f;
+        for (int s = 0; s < S; ++s) {
+            const float ms = ml[2 * s];
+            const float f = ms == -INFINITY ? 0.f : exp2f(ms - M);
+            acc = fmaf(f, part_o[(row * S + s) * D + d], acc);
+            L = fmaf(f, ml[2 * s + 1], L);
+        }
+        out[row * D + d] = acc / L;
+    }
+}
+
+struct Plan {
+    int n_units, n_splits, units_per_split;
+};
+
+Plan make_plan(int B, int Hkv, int n_chunks, int res_len, int splits_hint) {
+    Plan p;
+    p.n_units = n_chunks + (res_len + kWave - 1) / kWave;
+    int S = splits_hint;
+    if (S <= 0) {
+        const int target_groups = 2048;
+        S = (target_groups + B * Hkv - 1) / (B * Hkv);
+    }
+    S = max(1, min(S, (p.n_units + kAttnWaves - 1) / kAttnWaves));
+    p.units_per_split = (p.n_units + S - 1) / S;
+    p.n_splits = (p.n_units + p.units_per_split - 1) / p.units_per_split;
+    return p;
+}
+
+}  // namespace
+}  // namespace kivi
+
+using namespace kivi;
+
+extern "C" {
+
+size_t kivi_packed_decode_attention_workspace_size(int32_t batch, int32_t q_heads,
+                                                   int32_t kv_heads, int32_t head_dim,
+                                                   int32_t num_chunks, int32_t res_len,
+                                                   int32_t num_splits) {
+    if (batch <= 0 || kv_heads <= 0 || q_heads <= 0 || head_dim <= 0) return 0;
+    Plan p = make_plan(batch, kv_heads, num_chunks, res_len, num_splits);
+    if (p.n_splits <= 1) return 0;
+    return (size_t)batch * q_heads * p.n_splits * (head_dim + 2) * sizeof(float);
+}
+
+int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const float* k_scale,
+                                 const float* k_zero, const uint8_t* v_codes,
+                                 const float* v_scale, const float* v_zero, const float* k_res,
+                                 const float* v_res, float* out, void* workspace,
+                                 size_t workspace_bytes, int32_t batch, int32_t q_heads,
+                                 int32_t kv_heads, int32_t head_dim, int32_t group_size_k,
+                                 int32_t group_size_v, int32_t chunk_capacity,
+                                 int32_t num_chunks, int32_t res_capacity, int32_t res_start,
+                                 int32_t res_len, float softmax_scale, int32_t num_splits,
+                                 void* stream) {
+    if (!q || !out)
+        return set_error(kErrInvalidArgument, "null q/out pointer");
+    if (batch <= 0 || kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads)
+        return set_error(kErrInvalidArgument,
+                         "q_heads (%d) must be a positive multiple of kv_heads (%d)",
+                         q_heads, kv_heads);
+    const int hg = q_heads / kv_heads;
+    if (hg != 1 && hg != 2 && hg != 4 && hg != 8)
+        return set_error(kErrUnsupported, "q_heads / kv_heads = %d (supported: 1, 2, 4, 8)", hg);
+    if (head_dim <= 0 || head_dim % 16 || head_dim > kMaxD)
+        return set_error(kErrUnsupported, "head_dim %d (supported: multiple of 16, <= %d)",
+                         head_dim, kMaxD);
+    if (num_chunks < 0 || res_len < 0 || num_chunks + res_len == 0)
+        return set_error(kErrInvalidArgument, "empty context (num_chunks=%d, res_len=%d)",
+                         num_chunks, res_len);
+    if (num_chunks > 0) {
+        if (!k_codes || !k_scale || !k_zero || !v_codes || !v_scale || !v_zero)
+            return set_error(kErrInvalidArgument, "null packed-store pointer");
+        if (group_size_k <= 0 || group_size_k % 16 || group_size_k > kWave)
+            return set_error(kErrUnsupported,
+                             "group_size_k %d (supported: multiple of 16, <= 64)", group_size_k);
+        if (group_size_v <= 0 || group_size_v % 4 || head_dim % group_size_v)
+            return set_error(kErrInvalidArgument,
+                             "head_dim must be positive and divisible by group_size_v");
+        if (num_chunks > chunk_capacity)
+            return set_error(kErrInvalidArgument, "num_chunks %d exceeds capacity %d",
+                             num_chunks, chunk_capacity);
+    }
+    if (res_len > 0) {
+        if (!k_res || !v_res)
+            return set_error(kErrInvalidArgument, "null residual pointer");
+        if (res_len > res_capacity || res_start < 0 || res_start >= res_capacity)
+            return set_error(kErrInvalidArgument,
+                             "residual window (start %d, len %d) outside capacity %d",
+                             res_start, res_len, res_capacity);
+    }
+    Plan p = make_plan(batch, kv_heads, num_chunks, res_len, num_splits);
+    float* part_o = nullptr;
+    float* part_ml = nullptr;
+    if (p.n_splits > 1) {
+        const size_t need = (size_t)batch * q_heads * p.n_splits * (head_dim + 2) * sizeof(float);
+        if (workspace == nullptr || workspace_bytes < need)
+            return set_error(kErrInvalidArgument, "workspace of %zu bytes needed, got %zu",
+                             need, workspace_bytes);
+        part_o = (float*)workspace;
+        part_ml = part_o + (size_t)batch * q_heads * p.n_splits * head_dim;
+    }
+    AttnArgs a{q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res, v_res, out,
+               part_o, part_ml, q_heads, kv_heads, head_dim, group_size_k, group_size_v,
+               chunk_capacity, num_chunks, res_capacity, res_start, res_len, p.n_units,
+               p.n_splits, p.units_per_split, softmax_scale * kLog2e};
+    const dim3 grid(p.n_splits, kv_heads, batch);
+    const size_t lds = (size_t)(hg * head_dim + kAttnWaves * (hg * head_dim + hg * kWave)) *
+                       sizeof(float);
+    hipStream_t st = (hipStream_t)stream;
+    switch (hg) {
+        case 1: attn_generic_kernel<1><<<grid, kAttnBlock, lds, st>>>(a); break;
+        case 2: attn_generic_kernel<2><<<grid, kAttnBlock, lds, st>>>(a); break;
+        case 4: attn_generic_kernel<4><<<grid, kAttnBlock, lds, st>>>(a); break;
+        case 8: attn_generic_kernel<8><<<grid, kAttnBlock, lds, st>>>(a); break;
+    }
+    int rc = check_launch("packed_decode_attention");
+    if (rc || p.n_splits == 1) return rc;
+    attn_merge_kernel<<<dim3(q_heads, batch), head_dim, 0, st>>>(part_o, part_ml, out,
+                                                                  q_heads, head_dim,
+                                                                  p.n_splits);
+    return check_launch("packed_decode_attention_merge");
+}
+
+}  // extern "C"

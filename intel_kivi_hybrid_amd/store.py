@@ -1,0 +1,158 @@
+"""HBM-resident packed KV store for one attention layer.
+
+The reference keeps the fp32 residual and a dequantised fp32 history on the
+CPU and sends one G-token chunk to the device per flush
+(src/kivi_sycl/cache/manager.py:100-118,309-374).  Here everything stays in
+device memory:
+
+* an fp32 residual ring ``[B, Hkv, R, D]`` (``res_start``/``res_len`` track
+  the window; a flush advances ``res_start`` by G instead of moving data);
+* the packed store (codes, scales, zeros per chunk of G tokens, layout in
+  include/kivi_hip.h), grown geometrically;
+* optionally the dequantised history ``[B, Hkv, T, D]`` that
+  ``KiviCache.get_full_cache()`` serves (written by the flush kernel itself).
+
+Flushes and attention launch the HIP kernels of ``libkivi_hip.so`` on the
+current stream; the only torch work is allocation and plain copies.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _native
+
+_lib = _native.load()
+
+
+def _vp(t: Optional[torch.Tensor]):
+    return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
+
+
+def _stream(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+class PackedKVStore:
+    """Residual ring + packed chunks for one layer (all on ``device``)."""
+
+    def __init__(self, batch: int, kv_heads: int, head_dim: int, group_size: int,
+                 residual_capacity: int, device, group_size_v: Optional[int] = None,
+                 chunk_capacity: int = 0, keep_history: bool = False):
+        if group_size <= 0 or group_size % 4:
+            raise ValueError(f"group_size ({group_size}) must be >= 4 and divisible by 4")
+        gv = group_size if group_size_v is None else group_size_v
+        if gv <= 0 or gv % 4 or head_dim % gv:
+            raise ValueError(f"head_dim ({head_dim}) must be divisible by group_size_v ({gv})")
+        if residual_capacity < group_size:
+            raise ValueError("residual capacity must hold at least one group")
+        self.B, self.H, self.D = batch, kv_heads, head_dim
+        self.G, self.Gv, self.R = group_size, gv, residual_capacity
+        self.device = torch.device(device)
+        self.keep_history = keep_history
+        f32 = dict(dtype=torch.float32, device=self.device)
+        self.k_res = torch.zeros(batch, kv_heads, residual_capacity, head_dim, **f32)
+        self.v_res = torch.zeros_like(self.k_res)
+        self.res_start = 0
+        self.res_len = 0
+        self.n_chunks = 0
+        self.capacity = 0
+        self._alloc(max(int(chunk_capacity), 1))
+
+    # ------------------------------------------------------------------ alloc
+    def _alloc(self, cap: int) -> None:
+        B, H, D, G, gpt = self.B, self.H, self.D, self.G, self.D // self.Gv
+        u8 = dict(dtype=torch.uint8, device=self.device)
+        f32 = dict(dtype=torch.float32, device=self.device)
+        new = {
+            "k_codes": torch.empty(B, H, cap, G, D // 4, **u8),
+            "k_scale": torch.empty(B, H, cap, D, **f32),
+            "k_zero": torch.empty(B, H, cap, D, **f32),
+            "v_codes": torch.empty(B, H, cap, D, G // 4, **u8),
+            "v_scale": torch.empty(B, H, cap, G, gpt, **f32),
+            "v_zero": torch.empty(B, H, cap, G, gpt, **f32),
+        }
+        if self.keep_history:
+            new["k_hist"] = torch.empty(B, H, cap * G, D, **f32)
+            new["v_hist"] = torch.empty(B, H, cap * G, D, **f32)
+        n = self.n_chunks
+        for name, t in new.items():
+            if n and hasattr(self, name):
+                old = getattr(self, name)
+                if name.endswith("hist"):
+                    t[:, :, :n * G].copy_(old[:, :, :n * G])
+                else:
+                    t[:, :, :n].copy_(old[:, :, :n])
+            setattr(self, name, t)
+        if not self.keep_history:
+            self.k_hist = self.v_hist = None
+        self.capacity = cap
+
+    def reserve(self, n_chunks: int) -> None:
+        if n_chunks > self.capacity:
+            self._alloc(max(n_chunks, 2 * self.capacity))
+
+    # --------------------------------------------------------------- tokens
+    @property
+    def quantized_tokens(self) -> int:
+        return self.n_chunks * self.G
+
+    def append(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Copy new tokens ``[B, Hkv, n, D]`` into the residual window.  The
+        window must have room (callers flush first)."""
+        n = k.shape[2]
+        if self.res_len + n > self.R:
+            raise RuntimeError(f"residual window overflow ({self.res_len} + {n} > {self.R})")
+        pos = (self.res_start + self.res_len) % self.R
+        first = min(n, self.R - pos)
+        self.k_res[:, :, pos:pos + first].copy_(k[:, :, :first])
+        self.v_res[:, :, pos:pos + first].copy_(v[:, :, :first])
+        if first < n:
+            self.k_res[:, :, :n - first].copy_(k[:, :, first:])
+            self.v_res[:, :, :n - first].copy_(v[:, :, first:])
+        self.res_len += n
+
+    def residual(self):
+        """The residual window in token order (a copy when it wraps)."""
+        s, n = self.res_start, self.res_len
+        if s + n <= self.R:
+            return self.k_res[:, :, s:s + n], self.v_res[:, :, s:s + n]
+        return (torch.cat([self.k_res[:, :, s:], self.k_res[:, :, :s + n - self.R]], dim=2),
+                torch.cat([self.v_res[:, :, s:], self.v_res[:, :, :s + n - self.R]], dim=2))
+
+    def flush(self) -> None:
+        """Quantise the G oldest residual tokens into the next chunk."""
+        if self.res_len < self.G:
+            raise RuntimeError(f"Cannot flush {self.G} tokens: residual only has {self.res_len}")
+        self.reserve(self.n_chunks + 1)
+        hist_cap = self.capacity * self.G if self.keep_history else 0
+        with torch.cuda.device(self.device):
+            _native.check(_lib.kivi_store_flush(
+                _vp(self.k_res), _vp(self.v_res), _vp(self.k_codes), _vp(self.k_scale),
+                _vp(self.k_zero), _vp(self.v_codes), _vp(self.v_scale), _vp(self.v_zero),
+                _vp(self.k_hist), _vp(self.v_hist), hist_cap, self.B, self.H, self.D,
+                self.G, self.Gv, self.R, self.res_start, self.capacity, self.n_chunks,
+                _stream(self.device)), "kivi_store_flush")
+        self.n_chunks += 1
+        self.res_start = (self.res_start + self.G) % self.R
+        self.res_len -= self.G
+
+    def reset(self) -> None:
+        self.res_start = self.res_len = self.n_chunks = 0
+
+    # ------------------------------------------------------------ attention
+    def workspace_bytes(self, q_heads: int, num_splits: int = 0) -> int:
+        return int(_lib.kivi_packed_decode_attention_workspace_size(
+            self.B, q_heads, self.H, self.D, self.n_chunks, self.res_len, num_splits))
+
+    def attention(self, q: torch.Tensor, softmax_scale: Optional[float] = None,
+                  out: Optional[torch.Tensor] = None, num_splits: int = 0,
+                  workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Fused decode attention of ``q [B, Hq, D]`` (or ``[B, Hq, 1, D]``)
+        over [packed history ; residual]; returns ``[B, Hq, D]`` fp32."""
+        from . import _C
+        return _C.packed_decode_attention(q, self, softmax_scale=softmax_scale, out=out,
+                                          num_splits=num_splits, workspace=workspace)

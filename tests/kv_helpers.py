@@ -1,0 +1,87 @@
+"""Test-side helpers: build packed stores from seeded K/V and the matching
+oracle views (dequantised history, expected store bytes)."""
+
+import numpy as np
+import torch
+
+from oracle import codec
+from tests.conftest import seeded_kv
+
+
+def make_kv(B, H, T, D, seed):
+    k = seeded_kv((B, H, T, D), seed=seed, kind="key")
+    v = seeded_kv((B, H, T, D), seed=seed + 1, kind="value")
+    return k, v
+
+
+def oracle_chunk(k_chunk, v_chunk, G, Gv):
+    """Oracle quantisation of one chunk [B,H,G,D] in the store's byte order.
+
+    Keys: quantize_keys on the [B,H,D,G] transpose (per channel along tokens),
+    then codes re-packed token-major ([G][D/4], channel 4i+k at bits 2k).
+    Values: quantize_values on [B,H,G,D] rows, codes re-packed channel-major
+    ([D][G/4], token 4j+k at bits 2k)."""
+    B, H, _, D = k_chunk.shape
+    kt = k_chunk.transpose(2, 3).contiguous().numpy()             # [B,H,D,G]
+    kp, ks, kz = codec.quantize_groups(kt, G)
+    kcodes = codec.unpack_codes(kp, G).reshape(B, H, D, G).transpose(0, 1, 3, 2)   # [B,H,G,D]
+    k_bytes = pack_last(kcodes)                                    # [B,H,G,D/4]
+    vp, vs, vz = codec.quantize_groups(v_chunk.contiguous().numpy(), Gv)
+    vcodes = codec.unpack_codes(vp, Gv).reshape(B, H, G, D).transpose(0, 1, 3, 2)  # [B,H,D,G]
+    v_bytes = pack_last(vcodes)                                    # [B,H,D,G/4]
+    k_deq = codec.dequantize_groups(kp, ks, kz, G).reshape(B, H, D, G).transpose(0, 1, 3, 2)
+    v_deq = codec.dequantize_groups(vp, vs, vz, Gv).reshape(B, H, G, D)
+    return {
+        "k_codes": k_bytes, "k_scale": ks.reshape(B, H, D), "k_zero": kz.reshape(B, H, D),
+        "v_codes": v_bytes, "v_scale": vs.reshape(B, H, G, D // Gv),
+        "v_zero": vz.reshape(B, H, G, D // Gv),
+        "k_deq": np.ascontiguousarray(k_deq), "v_deq": v_deq,
+    }
+
+
+def pack_last(codes):
+    """codes [..., N] (N % 4 == 0) -> bytes [..., N/4], element 4j+k at bits 2k."""
+    c = codes.astype(np.uint8).reshape(*codes.shape[:-1], codes.shape[-1] // 4, 4)
+    return (c[..., 0] | (c[..., 1] << 2) | (c[..., 2] << 4) | (c[..., 3] << 6)).astype(np.uint8)
+
+
+def fill_store(store, k, v, R):
+    """Feed tokens [B,H,T,D] one group at a time as KiviCache would (flush
+    while residual >= R)."""
+    T = k.shape[2]
+    dev = store.device
+    t = 0
+    step = store.G
+    while t < T:
+        n = min(step, T - t, store.R - store.res_len)
+        store.append(k[:, :, t:t + n].to(dev), v[:, :, t:t + n].to(dev))
+        t += n
+        while store.res_len >= R:
+            store.flush()
+
+
+def oracle_history(k, v, n_chunks, G, Gv):
+    """Dequantised history [B,H,n_chunks*G,D] for keys and values."""
+    ks, vs = [], []
+    for c in range(n_chunks):
+        o = oracle_chunk(k[:, :, c * G:(c + 1) * G], v[:, :, c * G:(c + 1) * G], G, Gv)
+        ks.append(o["k_deq"])
+        vs.append(o["v_deq"])
+    B, H, _, D = k.shape
+    if not ks:
+        return np.zeros((B, H, 0, D), np.float32), np.zeros((B, H, 0, D), np.float32)
+    return np.concatenate(ks, axis=2), np.concatenate(vs, axis=2)
+
+
+def rel_err(out, ref):
+    """max |out - ref| / max |ref| per (b, head) row, worst row."""
+    out = np.asarray(out, np.float64)
+    ref = np.asarray(ref, np.float64)
+    num = np.abs(out - ref).max(axis=-1)
+    den = np.abs(ref).max(axis=-1)
+    return float((num / den).max())
+
+
+def seeded_q(B, Hq, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(B, Hq, D, generator=g) * (D ** -0.5)

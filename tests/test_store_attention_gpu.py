@@ -1,0 +1,120 @@
+"""GPU parity of the HBM-resident store (flush) and the fused packed decode
+attention, against the CPU oracle.
+
+Flush bar: codes (through the documented byte transposes), scales, zeros and
+the served dequantised history bit-exact.  Attention bar: within 1e-3
+relative (max |o - o_ref| / max |o_ref| per (batch, head)) of float64 SDPA
+over the oracle-dequantised history plus the fp32 residual.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention import decode_attention
+from tests.kv_helpers import (fill_store, make_kv, oracle_chunk, oracle_history, rel_err,
+                              seeded_q)
+
+pytestmark = pytest.mark.gpu
+
+ATTN_TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def store_cls(hip_device):
+    from intel_kivi_hybrid_amd.store import PackedKVStore
+    return PackedKVStore
+
+
+def _u32(t):
+    return t.detach().cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.parametrize("B,H,D,G,Gv,R,T", [
+    (1, 2, 8, 4, 4, 8, 30),          # the reference unit-test geometry (G=4, R=8, D=8)
+    (1, 12, 64, 32, 32, 32, 200),    # BASELINE config 1 geometry
+    (2, 3, 128, 32, 128, 48, 170),   # Gv != G, ring wrap (R not a multiple of G)
+    (2, 2, 64, 16, 16, 40, 133),
+])
+def test_flush_bit_exact(store_cls, B, H, D, G, Gv, R, T):
+    print(f"[flush] B={B} H={H} D={D} G={G} Gv={Gv} R={R} T={T}", flush=True)
+    k, v = make_kv(B, H, T, D, seed=T + D)
+    st = store_cls(B, H, D, G, R, "cuda:0", group_size_v=Gv, keep_history=True)
+    fill_store(st, k, v, R)
+    n_flush = 0 if T < R else (T - R) // G + 1
+    assert st.n_chunks == n_flush and st.res_len == T - n_flush * G
+    for c in range(st.n_chunks):
+        o = oracle_chunk(k[:, :, c * G:(c + 1) * G], v[:, :, c * G:(c + 1) * G], G, Gv)
+        assert np.array_equal(st.k_codes[:, :, c].cpu().numpy(), o["k_codes"]), f"k codes chunk {c}"
+        assert np.array_equal(_u32(st.k_scale[:, :, c]), o["k_scale"].view(np.uint32))
+        assert np.array_equal(_u32(st.k_zero[:, :, c]), o["k_zero"].view(np.uint32))
+        assert np.array_equal(st.v_codes[:, :, c].cpu().numpy(), o["v_codes"]), f"v codes chunk {c}"
+        assert np.array_equal(_u32(st.v_scale[:, :, c]), o["v_scale"].view(np.uint32))
+        assert np.array_equal(_u32(st.v_zero[:, :, c]), o["v_zero"].view(np.uint32))
+        kh = st.k_hist[:, :, c * G:(c + 1) * G]
+        vh = st.v_hist[:, :, c * G:(c + 1) * G]
+        assert np.array_equal(_u32(kh), o["k_deq"].view(np.uint32)), f"k history chunk {c}"
+        assert np.array_equal(_u32(vh), o["v_deq"].view(np.uint32)), f"v history chunk {c}"
+    rk, rv = st.residual()
+    q0 = st.n_chunks * G
+    assert torch.equal(rk.cpu(), k[:, :, q0:]) and torch.equal(rv.cpu(), v[:, :, q0:])
+
+
+def _attention_case(store_cls, B, Hq, Hkv, D, G, Gv, R, T, splits=0, seed=0):
+    print(f"[attn] B={B} Hq={Hq} Hkv={Hkv} D={D} G={G} Gv={Gv} R={R} T={T} splits={splits}",
+          flush=True)
+    k, v = make_kv(B, Hkv, T, D, seed=seed + T)
+    st = store_cls(B, Hkv, D, G, R, "cuda:0", group_size_v=Gv)
+    fill_store(st, k, v, R)
+    q = seeded_q(B, Hq, D, seed=seed + 99)
+    out = st.attention(q.cuda(), num_splits=splits)
+    torch.cuda.synchronize()
+    kh, vh = oracle_history(k, v, st.n_chunks, G, Gv)
+    q0 = st.n_chunks * G
+    ref = decode_attention(q.numpy(), kh, vh, k[:, :, q0:].numpy(), v[:, :, q0:].numpy())
+    err = rel_err(out.cpu().numpy(), ref)
+    print(f"[attn]   chunks={st.n_chunks} res={st.res_len} rel_err={err:.3e}", flush=True)
+    assert err <= ATTN_TOL
+    return err
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(4, 4), (8, 4), (16, 4), (32, 4)])
+@pytest.mark.parametrize("D", [64, 128])
+def test_attention_gqa_ratios(store_cls, Hq, Hkv, D):
+    _attention_case(store_cls, 2, Hq, Hkv, D, 32, 32, 64, 300)
+
+
+@pytest.mark.parametrize("G,Gv,R,T", [
+    (16, 16, 32, 100), (32, 128, 128, 400), (64, 64, 64, 400), (32, 32, 32, 32),
+    (32, 32, 128, 127),   # residual only, no chunk yet
+    (32, 32, 32, 64),     # residual empty right after a flush
+    (32, 32, 48, 77),     # ring wrap
+])
+def test_attention_group_shapes(store_cls, G, Gv, R, T):
+    _attention_case(store_cls, 2, 8, 2, 128, G, Gv, R, T)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 7, 64])
+def test_attention_split_counts_agree(store_cls, splits):
+    _attention_case(store_cls, 1, 8, 2, 128, 32, 32, 128, 2000, splits=splits, seed=3)
+
+
+def test_attention_reference_cosine_gate(store_cls, kat):
+    """The reference's only attention check (test_attention_fix.py:33-115):
+    KIVI attention vs fp32 attention cosine > 0.85 at B=1, H=2, cache 32,
+    D=64, G=32 (one token per query here; the reference used 3)."""
+    g = kat["attention_cosine_gate"]
+    torch.manual_seed(42)
+    B, H, T, D, G = g["B"], g["H"], g["cache_len"], g["D"], g["G"]
+    q = torch.randn(B, H, D)
+    k = torch.randn(B, H, T, D)
+    v = torch.randn(B, H, T, D)
+    st = store_cls(B, H, D, G, G, "cuda:0")
+    fill_store(st, k, v, G)
+    assert st.n_chunks == 1 and st.res_len == 0
+    out = st.attention(q.cuda()).cpu().double()
+    ref = decode_attention(q.numpy(), k.numpy(), v.numpy(), None, None)
+    cos = torch.nn.functional.cosine_similarity(out.reshape(1, -1),
+                                                torch.from_numpy(ref).reshape(1, -1)).item()
+    print(f"[attn] cosine vs fp32 = {cos:.4f}", flush=True)
+    assert cos > g["min_cosine"]
