@@ -115,6 +115,24 @@ class PackedKVStore:
             self.v_res[:, :, :n - first].copy_(v[:, :, first:])
         self.res_len += n
 
+    def extend(self, k: torch.Tensor, v: torch.Tensor, flush_at: Optional[int] = None) -> int:
+        """Append ``[B, Hkv, n, D]`` tokens, flushing the G oldest whenever the
+        residual reaches ``flush_at`` (default: the ring capacity), exactly as
+        KiviCache.add_tokens does (manager.py:226-249).  Returns the number of
+        flushes."""
+        R = self.R if flush_at is None else int(flush_at)
+        if not self.G <= R <= self.R:
+            raise ValueError(f"flush threshold {R} must lie in [{self.G}, {self.R}]")
+        n, t, flushes = k.shape[2], 0, 0
+        while t < n:
+            take = min(n - t, R - self.res_len)
+            self.append(k[:, :, t:t + take], v[:, :, t:t + take])
+            t += take
+            while self.res_len >= R:
+                self.flush()
+                flushes += 1
+        return flushes
+
     def residual(self):
         """The residual window in token order (a copy when it wraps)."""
         s, n = self.res_start, self.res_len
