@@ -161,6 +161,17 @@ class PackedKVStore:
     def reset(self) -> None:
         self.res_start = self.res_len = self.n_chunks = 0
 
+    # ---------------------------------------------------------- inspection
+    def unpermuted_k_codes(self, chunk: int) -> torch.Tensor:
+        """Key codes of one chunk as ``[B, Hkv, G, D/4]`` bytes: byte (t, i)
+        holds channels 4i..4i+3 of token t, channel 4i+k at bits 2k."""
+        return self.k_codes[:, :, chunk]
+
+    def unpermuted_v_codes(self, chunk: int) -> torch.Tensor:
+        """Value codes of one chunk as ``[B, Hkv, D, G/4]`` bytes: byte (d, j)
+        holds tokens 4j..4j+3 of channel d, token 4j+k at bits 2k."""
+        return self.v_codes[:, :, chunk]
+
     # ------------------------------------------------------------ attention
     def workspace_bytes(self, q_heads: int, num_splits: int = 0) -> int:
         return int(_lib.kivi_packed_decode_attention_workspace_size(

@@ -51,7 +51,11 @@ class KiviCacheOracle:
     """manager.py:52-423, state kept on the CPU as the reference keeps it."""
 
     def __init__(self, num_layers, head_dim, num_kv_heads=None, group_size=32,
-                 residual_length=128):
+                 residual_length=128, roundtrip_fn=None):
+        """``roundtrip_fn(t, group_size)`` replaces the device round-trip
+        (default: the C oracle codec); the reference's unit tests also run
+        with an identity round-trip (tests/unit/test_manager_bookkeeping.py:56-69)."""
+        self._roundtrip = roundtrip if roundtrip_fn is None else roundtrip_fn
         # manager.py:82-90
         assert head_dim % group_size == 0
         assert group_size >= 4 and group_size % 4 == 0
@@ -135,7 +139,8 @@ class KiviCacheOracle:
 
     def reset(self):
         """manager.py:292-303."""
-        self.__init__(self.num_layers, self.head_dim, None, self.G, self.R)
+        heads = self.num_kv_heads      # reset() keeps it (manager.py:292-303)
+        self.__init__(self.num_layers, self.head_dim, heads, self.G, self.R, self._roundtrip)
 
     def _flush_group(self, i: int):
         """manager.py:309-374."""
@@ -143,9 +148,9 @@ class KiviCacheOracle:
         assert self.res_keys[i].shape[2] >= G
         k_trans = self.res_keys[i][:, :, :G, :].transpose(2, 3).contiguous()  # [B,H,D,G]
         batch, heads, dim, seq = k_trans.shape
-        deq_k = roundtrip(k_trans, G)
+        deq_k = self._roundtrip(k_trans, G)
         v_chunk = self.res_values[i][:, :, :G, :].contiguous()                 # [B,H,G,D]
-        deq_v = roundtrip(v_chunk, G)
+        deq_v = self._roundtrip(v_chunk, G)
         groups_per_token = self.head_dim // G
         self._quant_token_count[i] += G
         self._quant_bytes[i] += (
