@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define KIVI_HIP_ABI_VERSION 1
+#define KIVI_HIP_ABI_VERSION 2
 
 #define KIVI_OK 0
 #define KIVI_ERR_INVALID_ARGUMENT 1
@@ -91,20 +91,29 @@ int kivi_quant_dequant_roundtrip_values(const float* input, float* output,
  * Replaces KiviCache._flush_group (src/kivi_sycl/cache/manager.py:309-374):
  * quantises the `group_size_k` oldest tokens of the fp32 residual ring of
  * every (batch, kv-head) into chunk `chunk_index` of the packed store, on the
- * device, without host copies.  Layout per (b, kv-head):
+ * device, without host copies.  Per (b, kv-head):
  *   k_res, v_res    [res_capacity][head_dim] f32 ring; token t of the window
  *                   sits at slot (res_start + t) % res_capacity
- *   k_codes         [chunk_capacity][G][head_dim/4] u8 (byte (t,i) = channels
- *                   4i..4i+3 of token t, channel 4i+k at bits 2k)
+ *   k_codes, v_codes [chunk_capacity][G*head_dim/4] u8 per chunk, in the code
+ *                   layout kivi_store_code_layout() reports:
+ *                   0 (plain): keys [G][D/4] (byte (t,i) = channels 4i..4i+3 of
+ *                     token t, channel 4i+k at bits 2k), values [D][G/4] (byte
+ *                     (d,j) = tokens 4j..4j+3 of channel d, token 4j+k at bits 2k);
+ *                   1 (matrix-core operand order): [64 lanes][G*D/1024 dwords]
+ *                     holding v_mfma_f32_16x16x32_bf16 B operands -- key tile
+ *                     ks*(G/16)+nb: lane l element j = token 16nb+l%16, channel
+ *                     32ks+8(l/16)+j; value tile kt*(D/16)+nb: lane l element j
+ *                     = token 32kt+8(l/16)+j, channel 16nb+l%16; tiles 2w and
+ *                     2w+1 share dword w, element j of tile 2w+m at bit
+ *                     8m+2(j/2)+16(j%2).
  *   k_scale, k_zero [chunk_capacity][head_dim] f32 (per channel per chunk)
- *   v_codes         [chunk_capacity][head_dim][G/4] u8 (byte (d,j) = tokens
- *                   4j..4j+3 of channel d, token 4j+k at bits 2k)
- *   v_scale, v_zero [chunk_capacity][G][head_dim/group_size_v] f32
+ *   v_scale, v_zero [chunk_capacity][head_dim/group_size_v][G] f32
  * Codes, scales and zeros equal quantize_keys on the chunk's [D, G] transpose
- * and quantize_values on its [G, D] rows.  If k_hist/v_hist are non-null
- * ([hist_capacity][head_dim] f32 per (b, kv-head)) the dequantised tokens are
- * also written at rows chunk_index*G .. +G-1 (bit-identical to the round-trip
- * ops, manager.py:337-345).  Requires group_size_k * head_dim <= 65536. */
+ * and quantize_values on its [G, D] rows; only their order differs.  If
+ * k_hist/v_hist are non-null ([hist_capacity][head_dim] f32 per (b, kv-head))
+ * the dequantised tokens are also written at rows chunk_index*G .. +G-1
+ * (bit-identical to the round-trip ops, manager.py:337-345).  Requires
+ * group_size_k * head_dim <= 65536. */
 int kivi_store_flush(const float* k_res, const float* v_res, uint8_t* k_codes,
                      float* k_scale, float* k_zero, uint8_t* v_codes, float* v_scale,
                      float* v_zero, float* k_hist, float* v_hist, int64_t hist_capacity,
@@ -112,6 +121,12 @@ int kivi_store_flush(const float* k_res, const float* v_res, uint8_t* k_codes,
                      int32_t group_size_k, int32_t group_size_v, int32_t res_capacity,
                      int32_t res_start, int32_t chunk_capacity, int32_t chunk_index,
                      void* stream);
+
+/* Code layout of a store with these shapes: 1 (matrix-core operand order)
+ * when head_dim is 64, 128 or 256, group_size_k is 32 or 64 and
+ * group_size_v is a multiple of 32 dividing head_dim; 0 (plain) otherwise.
+ * No reference counterpart (the reference keeps no packed store). */
+int kivi_store_code_layout(int32_t head_dim, int32_t group_size_k, int32_t group_size_v);
 
 /* ---- fused packed-KV decode attention -------------------------------------
  * No reference counterpart (the reference runs HF attention on the CPU over
@@ -124,9 +139,12 @@ int kivi_store_flush(const float* k_res, const float* v_res, uint8_t* k_codes,
  * num_splits <= 0 picks the split-K factor; workspace must hold
  * kivi_packed_decode_attention_workspace_size(...) bytes (0 means none is
  * needed and workspace may be NULL).  Supported: q_heads/kv_heads in
- * {1,2,4,8}, head_dim % 16 == 0 and <= 256, group_size_k % 16 == 0 and <= 64. */
+ * {1,2,4,8}, head_dim % 16 == 0 and <= 256; plain-layout stores also need
+ * group_size_k % 16 == 0 and <= 64.  Matrix-core-layout stores run on the
+ * bf16 MFMA units with fp32 accumulation (relative error ~1e-5). */
 size_t kivi_packed_decode_attention_workspace_size(int32_t batch, int32_t q_heads,
                                                    int32_t kv_heads, int32_t head_dim,
+                                                   int32_t group_size_k, int32_t group_size_v,
                                                    int32_t num_chunks, int32_t res_len,
                                                    int32_t num_splits);
 

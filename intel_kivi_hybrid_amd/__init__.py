@@ -3,12 +3,23 @@
 Drop-in for the ``kivi_sycl`` API surface (src/kivi_sycl/__init__.py:24-28 in
 the reference): ``KiviCache``, ``generate`` and the compiled-op module ``_C``.
 All device work runs in hand-written HIP kernels in ``libkivi_hip.so``,
-reached through its C ABI (include/kivi_hip.h); importing the package fails
-with ImportError when that library is missing.
+reached through its C ABI (include/kivi_hip.h); using ``KiviCache``,
+``generate`` or ``_C`` fails with ImportError when that library is missing.
+
+The public names resolve on first access, so that the build module
+(``python -m intel_kivi_hybrid_amd.build``) imports without the library.
 """
 
 from ._version import __version__
-from .cache.manager import KiviCache
-from .generation.generate import generate
 
 __all__ = ["KiviCache", "generate", "__version__"]
+
+
+def __getattr__(name):
+    if name == "KiviCache":
+        from .cache.manager import KiviCache
+        return KiviCache
+    if name == "generate":
+        from .generation.generate import generate
+        return generate
+    raise AttributeError(f"module {__name__!r} has no attribute {name!r}")

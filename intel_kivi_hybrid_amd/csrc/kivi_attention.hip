@@ -21,6 +21,7 @@
 // log2 domain (q is pre-scaled by scale * log2(e)) so exp is a single v_exp_f32.
 #include <math.h>
 
+#include "kivi_attention.hpp"
 #include "kivi_common.hpp"
 #include "../../include/kivi_hip.h"
 
@@ -207,8 +208,8 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
                 const int gd = d / a.Gv;
                 const uint32_t* vc =
                     reinterpret_cast<const uint32_t*>(a.v_codes + (cid * D + d) * (G / 4));
-                const float* vs = a.v_scale + cid * G * gpt + gd;
-                const float* vz = a.v_zero + cid * G * gpt + gd;
+                const float* vs = a.v_scale + (cid * gpt + gd) * G;   // [D/Gv][G]
+                const float* vz = a.v_zero + (cid * gpt + gd) * G;
                 for (int w4 = 0; w4 < G / 16; ++w4) {
                     const uint32_t w = vc[w4];
 #pragma unroll
@@ -217,7 +218,7 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
                         for (int k = 0; k < 4; ++k) {
                             const int tok = 16 * w4 + 4 * byte + k;
                             const uint32_t c = (w >> (8 * byte + 2 * k)) & 3u;
-                            const float vh = decode1(c, vs[tok * gpt], vz[tok * gpt]);
+                            const float vh = decode1(c, vs[tok], vz[tok]);
 #pragma unroll
                             for (int h = 0; h < HG; ++h)
                                 o[h][j] = fmaf(sp[h * kWave + tok], vh, o[h][j]);
@@ -307,11 +308,42 @@ __global__ __launch_bounds__(kMaxD) void attn_merge_kernel(const float* __restri
 }
 
 struct Plan {
-    int n_units, n_splits, units_per_split;
+    int layout;
+    int n_units, n_splits, units_per_split;   // generic kernel
+    int n_qsplits, chunks_per_wave, res_per_wave;   // matrix-core kernel
 };
 
-Plan make_plan(int B, int Hkv, int n_chunks, int res_len, int splits_hint) {
-    Plan p;
+Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
+               int splits_hint) {
+    Plan p{};
+    p.layout = code_layout_for(D, G, Gv);
+    if (p.layout == kLayoutMfma) {
+        // Aim for ~2048 chunk waves in flight (8 per CU) with >= 8 chunks per
+        // wave; the residual window gets its own workgroups.
+        constexpr int kWavesPerGroup = 4, kTargetWaves = 2048, kMinChunksPerWave = 8;
+        int S = splits_hint;
+        if (S <= 0) {
+            S = (kTargetWaves + kWavesPerGroup * B * Hkv - 1) / (kWavesPerGroup * B * Hkv);
+            const int cap = (n_chunks + kWavesPerGroup * kMinChunksPerWave - 1) /
+                            (kWavesPerGroup * kMinChunksPerWave);
+            S = min(S, max(cap, 1));
+        }
+        // Every wave also takes an even slice of the residual window.
+        if (n_chunks > 0) {
+            S = max(1, min(S, (n_chunks + kWavesPerGroup - 1) / kWavesPerGroup));
+            p.chunks_per_wave = (n_chunks + kWavesPerGroup * S - 1) / (kWavesPerGroup * S);
+            p.n_qsplits = (n_chunks + kWavesPerGroup * p.chunks_per_wave - 1) /
+                          (kWavesPerGroup * p.chunks_per_wave);
+        } else {
+            p.chunks_per_wave = 0;
+            p.n_qsplits = max(1, min(splits_hint > 0 ? splits_hint : 1,
+                                     (res_len + 16 * kWavesPerGroup - 1) / (16 * kWavesPerGroup)));
+        }
+        const int waves = kWavesPerGroup * p.n_qsplits;
+        p.res_per_wave = (res_len + waves - 1) / waves;
+        p.n_splits = p.n_qsplits;
+        return p;
+    }
     p.n_units = n_chunks + (res_len + kWave - 1) / kWave;
     int S = splits_hint;
     if (S <= 0) {
@@ -324,6 +356,10 @@ Plan make_plan(int B, int Hkv, int n_chunks, int res_len, int splits_hint) {
     return p;
 }
 
+// Partials are needed whenever more than one workgroup covers a row; the
+// matrix-core kernel always writes partials.
+bool needs_workspace(const Plan& p) { return p.layout == kLayoutMfma || p.n_splits > 1; }
+
 }  // namespace
 }  // namespace kivi
 
@@ -333,11 +369,15 @@ extern "C" {
 
 size_t kivi_packed_decode_attention_workspace_size(int32_t batch, int32_t q_heads,
                                                    int32_t kv_heads, int32_t head_dim,
+                                                   int32_t group_size_k, int32_t group_size_v,
                                                    int32_t num_chunks, int32_t res_len,
                                                    int32_t num_splits) {
-    if (batch <= 0 || kv_heads <= 0 || q_heads <= 0 || head_dim <= 0) return 0;
-    Plan p = make_plan(batch, kv_heads, num_chunks, res_len, num_splits);
-    if (p.n_splits <= 1) return 0;
+    if (batch <= 0 || kv_heads <= 0 || q_heads <= 0 || head_dim <= 0 || group_size_k <= 0 ||
+        group_size_v <= 0)
+        return 0;
+    Plan p = make_plan(batch, kv_heads, head_dim, group_size_k, group_size_v, num_chunks,
+                       res_len, num_splits);
+    if (!needs_workspace(p)) return 0;
     return (size_t)batch * q_heads * p.n_splits * (head_dim + 2) * sizeof(float);
 }
 
@@ -363,18 +403,22 @@ int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const f
     if (head_dim <= 0 || head_dim % 16 || head_dim > kMaxD)
         return set_error(kErrUnsupported, "head_dim %d (supported: multiple of 16, <= %d)",
                          head_dim, kMaxD);
+    if (group_size_k <= 0 || group_size_k % 4 || group_size_v <= 0 || group_size_v % 4 ||
+        head_dim % group_size_v)
+        return set_error(kErrInvalidArgument,
+                         "group sizes must be positive multiples of 4 and group_size_v must "
+                         "divide head_dim (got %d, %d, head_dim %d)", group_size_k,
+                         group_size_v, head_dim);
     if (num_chunks < 0 || res_len < 0 || num_chunks + res_len == 0)
         return set_error(kErrInvalidArgument, "empty context (num_chunks=%d, res_len=%d)",
                          num_chunks, res_len);
+    const int layout = code_layout_for(head_dim, group_size_k, group_size_v);
     if (num_chunks > 0) {
         if (!k_codes || !k_scale || !k_zero || !v_codes || !v_scale || !v_zero)
             return set_error(kErrInvalidArgument, "null packed-store pointer");
-        if (group_size_k <= 0 || group_size_k % 16 || group_size_k > kWave)
+        if (layout == kLayoutPlain && (group_size_k % 16 || group_size_k > kWave))
             return set_error(kErrUnsupported,
                              "group_size_k %d (supported: multiple of 16, <= 64)", group_size_k);
-        if (group_size_v <= 0 || group_size_v % 4 || head_dim % group_size_v)
-            return set_error(kErrInvalidArgument,
-                             "head_dim must be positive and divisible by group_size_v");
         if (num_chunks > chunk_capacity)
             return set_error(kErrInvalidArgument, "num_chunks %d exceeds capacity %d",
                              num_chunks, chunk_capacity);
@@ -387,10 +431,11 @@ int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const f
                              "residual window (start %d, len %d) outside capacity %d",
                              res_start, res_len, res_capacity);
     }
-    Plan p = make_plan(batch, kv_heads, num_chunks, res_len, num_splits);
+    Plan p = make_plan(batch, kv_heads, head_dim, group_size_k, group_size_v, num_chunks,
+                       res_len, num_splits);
     float* part_o = nullptr;
     float* part_ml = nullptr;
-    if (p.n_splits > 1) {
+    if (needs_workspace(p)) {
         const size_t need = (size_t)batch * q_heads * p.n_splits * (head_dim + 2) * sizeof(float);
         if (workspace == nullptr || workspace_bytes < need)
             return set_error(kErrInvalidArgument, "workspace of %zu bytes needed, got %zu",
@@ -398,22 +443,32 @@ int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const f
         part_o = (float*)workspace;
         part_ml = part_o + (size_t)batch * q_heads * p.n_splits * head_dim;
     }
-    AttnArgs a{q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res, v_res, out,
-               part_o, part_ml, q_heads, kv_heads, head_dim, group_size_k, group_size_v,
-               chunk_capacity, num_chunks, res_capacity, res_start, res_len, p.n_units,
-               p.n_splits, p.units_per_split, softmax_scale * kLog2e};
-    const dim3 grid(p.n_splits, kv_heads, batch);
-    const size_t lds = (size_t)(hg * head_dim + kAttnWaves * (hg * head_dim + hg * kWave)) *
-                       sizeof(float);
     hipStream_t st = (hipStream_t)stream;
-    switch (hg) {
-        case 1: attn_generic_kernel<1><<<grid, kAttnBlock, lds, st>>>(a); break;
-        case 2: attn_generic_kernel<2><<<grid, kAttnBlock, lds, st>>>(a); break;
-        case 4: attn_generic_kernel<4><<<grid, kAttnBlock, lds, st>>>(a); break;
-        case 8: attn_generic_kernel<8><<<grid, kAttnBlock, lds, st>>>(a); break;
+    if (layout == kLayoutMfma) {
+        AttnLaunch L{q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res, v_res, out,
+                     part_o, part_ml, batch, q_heads, kv_heads, head_dim, group_size_k,
+                     group_size_v, chunk_capacity, num_chunks, res_capacity, res_start, res_len,
+                     p.n_qsplits, p.chunks_per_wave, p.res_per_wave, p.n_splits,
+                     softmax_scale * kLog2e};
+        int rc = launch_attention_mfma(L, st);
+        if (rc) return rc;
+    } else {
+        AttnArgs a{q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res, v_res, out,
+                   part_o, part_ml, q_heads, kv_heads, head_dim, group_size_k, group_size_v,
+                   chunk_capacity, num_chunks, res_capacity, res_start, res_len, p.n_units,
+                   p.n_splits, p.units_per_split, softmax_scale * kLog2e};
+        const dim3 grid(p.n_splits, kv_heads, batch);
+        const size_t lds = (size_t)(hg * head_dim + kAttnWaves * (hg * head_dim + hg * kWave)) *
+                           sizeof(float);
+        switch (hg) {
+            case 1: attn_generic_kernel<1><<<grid, kAttnBlock, lds, st>>>(a); break;
+            case 2: attn_generic_kernel<2><<<grid, kAttnBlock, lds, st>>>(a); break;
+            case 4: attn_generic_kernel<4><<<grid, kAttnBlock, lds, st>>>(a); break;
+            case 8: attn_generic_kernel<8><<<grid, kAttnBlock, lds, st>>>(a); break;
+        }
+        int rc = check_launch("packed_decode_attention");
+        if (rc || !needs_workspace(p)) return rc;
     }
-    int rc = check_launch("packed_decode_attention");
-    if (rc || p.n_splits == 1) return rc;
     attn_merge_kernel<<<dim3(q_heads, batch), head_dim, 0, st>>>(part_o, part_ml, out,
                                                                   q_heads, head_dim,
                                                                   p.n_splits);

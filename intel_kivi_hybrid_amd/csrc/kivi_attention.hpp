@@ -1,0 +1,35 @@
+// Internal interface between the decode-attention entry point
+// (kivi_attention.hip) and its matrix-core kernel (kivi_attention_mfma.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kivi {
+
+struct AttnLaunch {
+    const float* q;          // [B, Hq, D]
+    const uint8_t* k_codes;  // [B, Hkv, Cmax, G*D/4]
+    const float* k_scale;    // [B, Hkv, Cmax, D]
+    const float* k_zero;
+    const uint8_t* v_codes;  // [B, Hkv, Cmax, G*D/4]
+    const float* v_scale;    // [B, Hkv, Cmax, D/Gv, G]
+    const float* v_zero;
+    const float* k_res;      // [B, Hkv, Rcap, D] ring
+    const float* v_res;
+    float* out;              // [B, Hq, D]
+    float* part_o;           // [B, Hq, n_splits, D]
+    float* part_ml;          // [B, Hq, n_splits, 2]
+    int B, Hq, Hkv, D, G, Gv, Cmax, n_chunks, Rcap, res_start, res_len;
+    int n_qsplits;           // workgroups per (b, kv-head)
+    int chunks_per_wave;     // packed chunks per wave
+    int res_per_wave;        // residual tokens per wave
+    int n_splits;            // partial states per row (= n_qsplits)
+    float qscale;            // softmax scale * log2(e)
+};
+
+// Launches the matrix-core kernel (kLayoutMfma stores, Hq/Hkv in {1,2,4,8}).
+// Always writes partials; the caller runs the merge.
+int launch_attention_mfma(const AttnLaunch& a, hipStream_t stream);
+
+}  // namespace kivi

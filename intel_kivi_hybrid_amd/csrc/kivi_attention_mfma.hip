@@ -1,0 +1,856 @@
+// Fused packed-KV decode attention on the gfx950 matrix cores.
+//
+// No reference counterpart (the reference dequantises flushed chunks into an
+// fp32 CPU history and runs HF attention over it, src/kivi_sycl/cache/
+// manager.py:251-290; the math is stated in tests/integration/
+// test_attention_fix.py:40-43).  For one query token per sequence and the
+// Hq/Hkv = HG query heads that share a kv head:
+//
+//   s[h,t] = sum_d q[h,d] * k_hat[t,d],  k_hat[t,d] = c[t,d]*ks[d] + kz[d]
+//   o[h,d] = sum_t softmax(s)[h,t] * v_hat[t,d],
+//            v_hat[t,d] = c'[t,d]*vs[t,g(d)] + vz[t,g(d)]
+//
+// over the packed chunks of the store, and the same over the fp32 residual
+// window.  Decode at GQA ratio HG needs ~4*HG multiply-adds per 2-bit code;
+// at fp32 VALU rates that, not HBM, would bound the kernel, so the two
+// contractions run as bf16 MFMAs (v_mfma_f32_16x16x32_bf16) with fp32
+// accumulation:
+//
+// * B operands are the codes themselves.  The store keeps each lane's codes
+//   in MFMA operand order (kLayoutMfma), and a code c becomes the bf16 value
+//   8 + c (exponent of 8, c in mantissa bits 5:4) with one shift and one
+//   and-or per two codes.  Integers 8..11 are exact in bf16.
+// * A operands carry the fp32 factors split into bf16 hi + lo rows
+//   (x ~ hi + lo to 2^-17 relative): rows 2h/2h+1 of the key A matrix are
+//   q[h,d]*ks[d], rows of the value A matrix are p[h,t]*vs[t,g].
+// * The constant parts fold into corrections that are linear in the data:
+//     s[h,t] = sum_d (q ks)[h,d] (8 + c) + sum_d q[h,d] (kz[d] - 8 ks[d])
+//     o[h,d] = sum_t (p vs)[h,t] (8 + c') + sum_t p[h,t] (vz[t] - 8 vs[t])
+//   The key correction enters the MFMA as extra k-steps against a B of ones
+//   (so it is summed across lanes by the matrix core); the value correction
+//   is accumulated per lane and added once at the end.
+//
+// Work split: each wave owns a contiguous range of chunks of one
+// (batch, kv-head) and keeps an online softmax over it in the log2 domain
+// (q is pre-scaled by softmax_scale * log2(e)).  The running maximum is only
+// moved when a chunk exceeds it by more than 8 (probabilities stay <= 256),
+// so rescaling the accumulators is rare.  Workgroups of 4 waves merge their
+// states in LDS; workgroups past the chunk splits take the fp32 residual
+// window with plain fp32 FMAs.  Each workgroup writes a partial (o, m, l)
+// that kivi_attention.hip's merge kernel combines with log-sum-exp weights.
+#include <math.h>
+
+#include "kivi_common.hpp"
+#include "kivi_attention.hpp"
+
+namespace kivi {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 4;
+
+template <int V>
+struct Int {
+    static constexpr int value = V;
+};
+
+// f(Int<K>{}), ..., f(Int<N-1>{}): a loop whose index is a constant expression.
+template <int K, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (K < N) {
+        f(Int<K>{});
+        static_for<K + 1, N>(f);
+    }
+}
+constexpr int kBlock = kWaves * kWave;
+constexpr int kResPass = 16;              // residual tokens per pass of a wave
+constexpr float kRescaleThreshold = 8.0f;   // log2 units
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    bf16x2_t v = {(__bf16)a, (__bf16)b};   // round to nearest even
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// (a, b) -> hi and lo bf16 pairs with a ~ hi.x + lo.x, b ~ hi.y + lo.y.
+__device__ __forceinline__ void split_pair(float a, float b, uint32_t& hi, uint32_t& lo) {
+    hi = pack_bf16x2(a, b);
+    const float ha = __builtin_bit_cast(float, hi << 16);
+    const float hb = __builtin_bit_cast(float, hi & 0xffff0000u);
+    lo = pack_bf16x2(a - ha, b - hb);
+}
+
+// (x & mask) | base in one VALU op.  LLVM splits it into two VOP2 ops with
+// literal operands; VOP3 v_and_or_b32 (one SGPR operand allowed on gfx950,
+// the other constant kept in a VGPR) is half the cost, and this is the inner
+// loop's most frequent operation.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t base) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(base));
+    return r;
+}
+
+// Code word -> B operand (four dwords of two bf16 "8 + c" each) for tile
+// 2w + M of the word (element j at bit mfma_code_bit(M, j)).
+template <int M>
+__device__ __forceinline__ bf16x8_t unpack_codes(uint32_t x) {
+    const uint32_t kMask = __builtin_amdgcn_readfirstlane(0x00300030u);
+    const uint32_t kBase = 0x41004100u;
+    u32x4_t o;
+    if constexpr (M == 0) {
+        o[0] = and_or(x << 4, kMask, kBase);
+        o[1] = and_or(x << 2, kMask, kBase);
+        o[2] = and_or(x, kMask, kBase);
+        o[3] = and_or(x >> 2, kMask, kBase);
+    } else {
+        o[0] = and_or(x >> 4, kMask, kBase);
+        o[1] = and_or(x >> 6, kMask, kBase);
+        o[2] = and_or(x >> 8, kMask, kBase);
+        o[3] = and_or(x >> 10, kMask, kBase);
+    }
+    return __builtin_bit_cast(bf16x8_t, o);
+}
+
+__device__ __forceinline__ f32x4_t mfma(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+        0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Reductions across the 16 lanes of a DPP row (row_ror 8, 4, 2, 1).
+__device__ __forceinline__ float row_max16(float v) {
+    v = fmaxf(v, dpp<0x128>(v));
+    v = fmaxf(v, dpp<0x124>(v));
+    v = fmaxf(v, dpp<0x122>(v));
+    return fmaxf(v, dpp<0x121>(v));
+}
+
+__device__ __forceinline__ float row_sum16(float v) {
+    v += dpp<0x128>(v);
+    v += dpp<0x124>(v);
+    v += dpp<0x122>(v);
+    return v + dpp<0x121>(v);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Compile-time shape of one instantiation.
+template <int HG_, int D_, int G_>
+struct Shape {
+    static constexpr int HG = HG_, D = D_, G = G_;
+    static constexpr int NSUB = G / 32;              // 32-token sub-chunks
+    static constexpr int NP = G * D / 1024;          // code dwords per lane
+    static constexpr int KS = D / 32;                // key k-steps
+    static constexpr int NBV = D / 16;               // value n-blocks
+    static constexpr int LPH = (64 / HG < D / 2) ? 64 / HG : D / 2;   // W-prep lanes per head
+    static constexpr int CPL = D / LPH;              // channels per W-prep lane
+    static constexpr int NBB = (LPH + 31) / 32;      // bias k-steps
+    static constexpr int NGMAX = D / 32;             // value groups (Gv >= 32)
+    static constexpr int NEV = (HG * (G / 8) * NGMAX + 63) / 64;   // P-prep items per lane
+    // chunk metadata: ks [D], kz [D], vs [NG][G], vz [NG][G] as float4s
+    static constexpr int META4_MAX = (2 * D + 2 * NGMAX * G) / 4;
+    static constexpr int NMETA = (META4_MAX + 63) / 64;      // float4 loads per lane
+    // chunks kept in flight per wave: ~64 VGPRs of prefetch ring, and at
+    // least 2 (the pipelined loop holds chunks i and i+1 at once)
+    static constexpr int REGS_PER_CHUNK = 2 * NP + 4 * NMETA;
+    static constexpr int PF = (64 / REGS_PER_CHUNK) < 2 ? 2
+                              : (64 / REGS_PER_CHUNK) > 4 ? 4 : 64 / REGS_PER_CHUNK;
+    // per-wave LDS (bytes).  A-operand rows are padded by 16 bytes so that
+    // the 8 lanes of a ds_read_b128 phase (8 consecutive rows) hit distinct
+    // LDS banks.
+    static constexpr int WA_ROW = D + 8;             // bf16 per key A row
+    static constexpr int BA_ROW = 32 * NBB + 8;      // bf16 per correction A row
+    static constexpr int PA_ROW = G + 8;             // bf16 per value A row
+    static constexpr int PA_MAT = 16 * PA_ROW + 8;   // bf16 per value A matrix (one group)
+    static constexpr int OFF_WA = 0;
+    static constexpr int OFF_BA = OFF_WA + 16 * WA_ROW * 2;
+    static constexpr int OFF_PA = OFF_BA + 16 * BA_ROW * 2;
+    // The rest depends on the number of value groups NG = D / Gv.
+    __host__ __device__ static constexpr int off_pl(int NG) { return OFF_PA + NG * PA_MAT * 2; }
+    __host__ __device__ static constexpr int off_al(int NG) { return off_pl(NG) + 2 * HG * G * 4; }
+    __host__ __device__ static constexpr int off_vb(int NG) { return off_al(NG) + 2 * 16 * 4; }
+    __host__ __device__ static constexpr int off_mt(int NG) {
+        return off_vb(NG) + HG * NG * (G / 8) * 4;
+    }
+    __host__ __device__ static constexpr int meta_floats(int NG) { return 2 * D + 2 * NG * G; }
+    __host__ __device__ static constexpr int wave_lds(int NG) {
+        return off_mt(NG) + 2 * meta_floats(NG) * 4;
+    }
+    // merge region: per wave o [HG][D], m [HG], l [HG] fp32
+    // merge region: one chunk state per wave
+    static constexpr int MERGE_LDS = kWaves * (HG * D + 2 * HG) * 4;
+    // residual region: scaled q [HG][D], per-wave probabilities [HG][16] and
+    // per-wave residual states (o [HG][D], m [HG], l [HG])
+    static constexpr int RSTATE = HG * D + 2 * HG;
+    static constexpr int RES_LDS = HG * D * 4 + kWaves * HG * kResPass * 4 + kWaves * RSTATE * 4;
+    __host__ __device__ static constexpr int lds(int NG) {
+        return (kWaves * wave_lds(NG) > MERGE_LDS ? kWaves * wave_lds(NG) : MERGE_LDS) + RES_LDS;
+    }
+    static_assert(NP >= 1 && LPH * CPL == D && CPL % 2 == 0, "shape");
+};
+
+// Writes this wave's state (o unnormalised over D channels, m, l) to the
+// merge region; `o_of(h, d)` supplies o.
+__device__ __forceinline__ float* merge_slot(unsigned char* smem, int HG, int D, int wave) {
+    return reinterpret_cast<float*>(smem) + wave * (HG * D + 2 * HG);
+}
+
+// Combines the 4 chunk states (merge slots) and the 4 residual-slice states
+// of the workgroup and writes one partial (o, m, l) row per query head.
+template <int HG, int D>
+__device__ void merge_and_store(unsigned char* smem, const float* rstates, const AttnLaunch& a,
+                                int split, int kvh, int b) {
+    __syncthreads();
+    constexpr int ST = HG * D + 2 * HG;
+    const int64_t hq0 = (int64_t)b * a.Hq + kvh * HG;
+    for (int e = threadIdx.x; e < HG * D; e += kBlock) {
+        const int h = e / D, d = e % D;
+        float M = -INFINITY;
+        for (int w = 0; w < 2 * kWaves; ++w) {
+            const float* s = w < kWaves ? merge_slot(smem, HG, D, w) : rstates + (w - kWaves) * ST;
+            M = fmaxf(M, s[HG * D + h]);
+        }
+        float acc = 0.f, L = 0.f;
+        for (int w = 0; w < 2 * kWaves; ++w) {
+            const float* s = w < kWaves ? merge_slot(smem, HG, D, w) : rstates + (w - kWaves) * ST;
+            const float mw = s[HG * D + h];
+            const float f = mw == -INFINITY ? 0.f : exp2_fast(mw - M);
+            acc = fmaf(f, s[h * D + d], acc);
+            L = fmaf(f, s[HG * D + HG + h], L);
+        }
+        const int64_t row = (hq0 + h) * a.n_splits + split;
+        a.part_o[row * D + d] = acc;
+        if (d == 0) {
+            a.part_ml[row * 2] = M;
+            a.part_ml[row * 2 + 1] = L;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Quantised chunks (matrix cores).
+// ---------------------------------------------------------------------------
+template <class S>
+struct ChunkRegs {
+    uint32_t kc[S::NP];      // this lane's key code words
+    uint32_t vc[S::NP];      // this lane's value code words
+    float4 meta[S::NMETA];   // slice of [ks | kz | vs | vz]
+};
+
+// Per-lane sources of a chunk's loads, computed once per wave: the lane's code
+// words, and for each float4 of the metadata sweep [ks | kz | vs | vz] the
+// address at chunk 0 of this (b, kv-head) and the per-chunk stride.
+template <class S>
+struct ChunkSrc {
+    const uint32_t* kc;
+    const uint32_t* vc;
+    const float4* meta[S::NMETA];
+    int meta_stride[S::NMETA];    // float4s per chunk
+};
+
+template <class S>
+__device__ __forceinline__ ChunkSrc<S> chunk_src(const AttnLaunch& a, int64_t cid0, int lane,
+                                                 int NG) {
+    ChunkSrc<S> c;
+    c.kc = reinterpret_cast<const uint32_t*>(a.k_codes) + cid0 * (64 * S::NP) + lane * S::NP;
+    c.vc = reinterpret_cast<const uint32_t*>(a.v_codes) + cid0 * (64 * S::NP) + lane * S::NP;
+    const int kq = S::D / 4, vq = NG * S::G / 4;
+#pragma unroll
+    for (int i = 0; i < S::NMETA; ++i) {
+        // Lanes past the end reload the last float4 (never stored), so every
+        // load is unconditional.
+        const int e = min(lane + 64 * i, 2 * kq + 2 * vq - 1);
+        if (e < kq) {
+            c.meta[i] = reinterpret_cast<const float4*>(a.k_scale + cid0 * S::D) + e;
+            c.meta_stride[i] = kq;
+        } else if (e < 2 * kq) {
+            c.meta[i] = reinterpret_cast<const float4*>(a.k_zero + cid0 * S::D) + (e - kq);
+            c.meta_stride[i] = kq;
+        } else if (e < 2 * kq + vq) {
+            c.meta[i] = reinterpret_cast<const float4*>(a.v_scale + cid0 * NG * S::G) + (e - 2 * kq);
+            c.meta_stride[i] = vq;
+        } else {
+            c.meta[i] = reinterpret_cast<const float4*>(a.v_zero + cid0 * NG * S::G) +
+                        (e - 2 * kq - vq);
+            c.meta_stride[i] = vq;
+        }
+    }
+    return c;
+}
+
+// Issues the loads of chunk c (relative to the wave's (b, kv-head)).
+template <class S>
+__device__ __forceinline__ void load_chunk(ChunkRegs<S>& r, const ChunkSrc<S>& src, int c) {
+    const uint32_t* kc = src.kc + (int64_t)c * (64 * S::NP);
+    const uint32_t* vc = src.vc + (int64_t)c * (64 * S::NP);
+#pragma unroll
+    for (int i = 0; i < S::NP; ++i) {
+        r.kc[i] = kc[i];
+        r.vc[i] = vc[i];
+    }
+#pragma unroll
+    for (int i = 0; i < S::NMETA; ++i) r.meta[i] = src.meta[i][(int64_t)c * src.meta_stride[i]];
+}
+
+template <class S>
+__device__ __forceinline__ void stage_meta(const ChunkRegs<S>& r, float* MT, int lane, int NG,
+                                           int meta_floats) {
+    const int n4 = meta_floats / 4;
+#pragma unroll
+    for (int i = 0; i < S::NMETA; ++i) {
+        const int e = lane + 64 * i;
+        if (e < n4) reinterpret_cast<float4*>(MT)[e] = r.meta[i];
+    }
+}
+
+template <class S>
+__device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, int kvh, int b) {
+    constexpr int HG = S::HG, D = S::D, G = S::G, NSUB = S::NSUB, NB = G / 16, NSEG = G / 8;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int NG = D / a.Gv;
+    const int64_t bh = (int64_t)b * a.Hkv + kvh;
+
+    unsigned char* wl = smem + wave * S::wave_lds(NG);
+    uint16_t* WA = reinterpret_cast<uint16_t*>(wl + S::OFF_WA);
+    uint16_t* BA = reinterpret_cast<uint16_t*>(wl + S::OFF_BA);
+    uint16_t* PA = reinterpret_cast<uint16_t*>(wl + S::OFF_PA);
+    float* PL = reinterpret_cast<float*>(wl + S::off_pl(NG));      // [2][HG][G]
+    float* AL = reinterpret_cast<float*>(wl + S::off_al(NG));      // [2][16]
+    float* VB = reinterpret_cast<float*>(wl + S::off_vb(NG));
+    float* MT = reinterpret_cast<float*>(wl + S::off_mt(NG));      // [2][meta]
+    const int meta_floats = S::meta_floats(NG);
+
+    // Zero the A operands once: rows >= 2*HG and correction columns >= LPH
+    // are never written and must read as 0.
+    for (int e = lane; e < S::off_pl(NG) / 4; e += kWave) reinterpret_cast<uint32_t*>(wl)[e] = 0u;
+
+    // Residual region: scaled q of the group, per-wave probabilities and the
+    // per-wave residual-slice states.
+    float* qres = reinterpret_cast<float*>(smem + S::lds(NG) - S::RES_LDS);   // [HG][D]
+    float* rstates = qres + HG * D + kWaves * HG * kResPass;
+    for (int e = threadIdx.x; e < HG * D; e += kBlock)
+        qres[e] = a.q[((int64_t)b * a.Hq + kvh * HG) * D + e] * a.qscale;
+    __syncthreads();
+
+    // W-prep lane: head wh, channels [wseg*CPL, +CPL).
+    const bool wlane = lane < HG * S::LPH;
+    const int wh = lane / S::LPH, wseg = lane % S::LPH;
+    float qv[S::CPL];
+#pragma unroll
+    for (int i = 0; i < S::CPL; ++i)
+        qv[i] = wlane ? a.q[((int64_t)b * a.Hq + kvh * HG + wh) * D + wseg * S::CPL + i] * a.qscale
+                      : 0.f;
+
+    const int c_begin = (split * kWaves + wave) * a.chunks_per_wave;
+    const int c_end = min(c_begin + a.chunks_per_wave, a.n_chunks);
+
+    f32x4_t O[S::NBV];
+#pragma unroll
+    for (int i = 0; i < S::NBV; ++i) O[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int gq = lane / 16, col = lane % 16;
+    float m_run[2] = {-INFINITY, -INFINITY}, l_part[2] = {0.f, 0.f};
+    const bool hvalid[2] = {2 * gq < HG, 2 * gq + 1 < HG};
+    float vb[S::NEV];
+#pragma unroll
+    for (int it = 0; it < S::NEV; ++it) vb[it] = 0.f;
+    const int n_items = HG * NSEG * NG;
+
+    const bf16x8_t ones = __builtin_bit_cast(
+        bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+
+    // ---- phases of one chunk --------------------------------------------------
+    // Key A operand: rows 2h / 2h+1 = hi / lo of q[h,d]*ks[d]; correction
+    // column: hi / lo of sum_d q[h,d]*(kz[d] - 8 ks[d]) over the lane's channels.
+    auto wprep = [&](auto slot_c) {
+        constexpr int slot = decltype(slot_c)::value;
+        if (!wlane) return;
+        const float* mks = MT + slot * meta_floats + wseg * S::CPL;
+        const float* mkz = mks + D;
+        float ks[S::CPL], kz[S::CPL];
+        if constexpr (S::CPL % 4 == 0) {
+#pragma unroll
+            for (int i = 0; i < S::CPL; i += 4) {
+                const float4 a4 = *reinterpret_cast<const float4*>(mks + i);
+                const float4 z4 = *reinterpret_cast<const float4*>(mkz + i);
+                ks[i] = a4.x; ks[i + 1] = a4.y; ks[i + 2] = a4.z; ks[i + 3] = a4.w;
+                kz[i] = z4.x; kz[i + 1] = z4.y; kz[i + 2] = z4.z; kz[i + 3] = z4.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < S::CPL; i += 2) {
+                const float2 a2 = *reinterpret_cast<const float2*>(mks + i);
+                const float2 z2 = *reinterpret_cast<const float2*>(mkz + i);
+                ks[i] = a2.x; ks[i + 1] = a2.y;
+                kz[i] = z2.x; kz[i + 1] = z2.y;
+            }
+        }
+        uint32_t hi[S::CPL / 2], lo[S::CPL / 2];
+        float corr = 0.f;
+#pragma unroll
+        for (int j = 0; j < S::CPL / 2; ++j) {
+            split_pair(qv[2 * j] * ks[2 * j], qv[2 * j + 1] * ks[2 * j + 1], hi[j], lo[j]);
+            corr = fmaf(qv[2 * j], fmaf(-8.f, ks[2 * j], kz[2 * j]), corr);
+            corr = fmaf(qv[2 * j + 1], fmaf(-8.f, ks[2 * j + 1], kz[2 * j + 1]), corr);
+        }
+        uint32_t* rhi = reinterpret_cast<uint32_t*>(WA + (2 * wh) * S::WA_ROW + wseg * S::CPL);
+        uint32_t* rlo = reinterpret_cast<uint32_t*>(WA + (2 * wh + 1) * S::WA_ROW + wseg * S::CPL);
+#pragma unroll
+        for (int j = 0; j < S::CPL / 2; ++j) {
+            rhi[j] = hi[j];
+            rlo[j] = lo[j];
+        }
+        uint32_t chi, clo;
+        split_pair(corr, 0.f, chi, clo);
+        BA[(2 * wh) * S::BA_ROW + wseg] = (uint16_t)chi;
+        BA[(2 * wh + 1) * S::BA_ROW + wseg] = (uint16_t)clo;
+    };
+
+    // Scores of the chunk's G tokens (matrix cores), then the online softmax:
+    // lane group gq holds heads 2gq, 2gq+1.  Returns whether any running max
+    // moved (then O and l are already rescaled and AL[slot] holds the factors).
+    auto kside = [&](const ChunkRegs<S>& r, auto slot_c) -> bool {
+        constexpr int slot = decltype(slot_c)::value;
+        bf16x8_t Aw[S::KS], Ab[S::NBB];
+#pragma unroll
+        for (int ks = 0; ks < S::KS; ++ks)
+            Aw[ks] = *reinterpret_cast<const bf16x8_t*>(WA + col * S::WA_ROW + 32 * ks + 8 * gq);
+#pragma unroll
+        for (int kb = 0; kb < S::NBB; ++kb)
+            Ab[kb] = *reinterpret_cast<const bf16x8_t*>(BA + col * S::BA_ROW + 32 * kb + 8 * gq);
+        f32x4_t Sc[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < S::KS; ++ks) {
+                const uint32_t word = r.kc[ks * NSUB + nb / 2];
+                acc = mfma(Aw[ks], (nb % 2) == 0 ? unpack_codes<0>(word) : unpack_codes<1>(word),
+                           acc);
+            }
+#pragma unroll
+            for (int kb = 0; kb < S::NBB; ++kb) acc = mfma(Ab[kb], ones, acc);
+            Sc[nb] = acc;
+        }
+        float sc[2][NB], alpha[2] = {1.f, 1.f};
+        bool need[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            float cm = -INFINITY;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                sc[e][nb] = Sc[nb][2 * e] + Sc[nb][2 * e + 1];
+                cm = fmaxf(cm, sc[e][nb]);
+            }
+            cm = row_max16(cm);
+            need[e] = hvalid[e] && cm > m_run[e] + kRescaleThreshold;
+            if (need[e]) {
+                alpha[e] = exp2_fast(m_run[e] - cm);
+                m_run[e] = cm;
+            }
+        }
+        const bool any = __builtin_amdgcn_ballot_w64(need[0] || need[1]) != 0;
+        if (any) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                l_part[e] *= alpha[e];
+#pragma unroll
+                for (int nb = 0; nb < S::NBV; ++nb) {
+                    O[nb][2 * e] *= alpha[e];
+                    O[nb][2 * e + 1] *= alpha[e];
+                }
+                if (col == 0 && hvalid[e]) AL[slot * 16 + 2 * gq + e] = alpha[e];
+            }
+        }
+        float* pl = PL + slot * (HG * G);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            float lsum = 0.f;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const float p = exp2_fast(sc[e][nb] - m_run[e]);
+                lsum += p;
+                if (hvalid[e]) pl[(2 * gq + e) * G + 16 * nb + col] = p;
+            }
+            l_part[e] += lsum;
+        }
+        return any;
+    };
+
+    // Value A operands: rows 2h / 2h+1 = hi / lo of p[h,t]*vs[t,g] for each
+    // group g, one item = (head, group, 8 tokens); value corrections p*(vz-8vs).
+    // Item geometry is fixed per lane: LDS offsets are computed once here.
+    int it_valid[S::NEV], it_h[S::NEV], it_pl[S::NEV], it_mv[S::NEV], it_pa[S::NEV];
+#pragma unroll
+    for (int it = 0; it < S::NEV; ++it) {
+        const int e = lane + 64 * it;
+        const int h = e / (NSEG * NG), rem = e % (NSEG * NG);
+        const int g = rem / NSEG, seg = rem % NSEG;
+        it_valid[it] = e < n_items;
+        it_h[it] = h;
+        it_pl[it] = h * G + 8 * seg;                       // into PL[slot]
+        it_mv[it] = g * G + 8 * seg;                       // into vs / vz of MT[slot]
+        it_pa[it] = g * S::PA_MAT + 8 * seg + 2 * h * S::PA_ROW;
+    }
+    auto pprep = [&](auto slot_c, bool any) {
+        constexpr int slot = decltype(slot_c)::value;
+        const float* pl = PL + slot * (HG * G);
+        const float* mvs = MT + slot * meta_floats + 2 * D;
+        const float* mvz = mvs + NG * G;
+#pragma unroll
+        for (int it = 0; it < S::NEV; ++it) {
+            if (it_valid[it]) {
+                if (any) vb[it] *= AL[slot * 16 + it_h[it]];
+                const float4 pa = *reinterpret_cast<const float4*>(pl + it_pl[it]);
+                const float4 pb = *reinterpret_cast<const float4*>(pl + it_pl[it] + 4);
+                const float4 sa = *reinterpret_cast<const float4*>(mvs + it_mv[it]);
+                const float4 sb = *reinterpret_cast<const float4*>(mvs + it_mv[it] + 4);
+                const float4 za = *reinterpret_cast<const float4*>(mvz + it_mv[it]);
+                const float4 zb = *reinterpret_cast<const float4*>(mvz + it_mv[it] + 4);
+                const float p[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+                const float vs[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
+                const float vz[8] = {za.x, za.y, za.z, za.w, zb.x, zb.y, zb.z, zb.w};
+                u32x4_t hi, lo;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t h2, l2;
+                    split_pair(p[2 * j] * vs[2 * j], p[2 * j + 1] * vs[2 * j + 1], h2, l2);
+                    hi[j] = h2;
+                    lo[j] = l2;
+                }
+                float acc = vb[it];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc = fmaf(p[j], fmaf(-8.f, vs[j], vz[j]), acc);
+                vb[it] = acc;
+                uint16_t* base = PA + it_pa[it];
+                *reinterpret_cast<u32x4_t*>(base) = hi;
+                *reinterpret_cast<u32x4_t*>(base + S::PA_ROW) = lo;
+            }
+        }
+    };
+
+    // o += P' . V-codes over the chunk's G tokens.
+    auto vside = [&](const ChunkRegs<S>& r) {
+#pragma unroll
+        for (int kt = 0; kt < NSUB; ++kt) {
+            int g_loaded = -1;
+            bf16x8_t Ap;
+#pragma unroll
+            for (int nb = 0; nb < S::NBV; ++nb) {
+                const int g = (16 * nb) / a.Gv;
+                if (g != g_loaded) {
+                    Ap = *reinterpret_cast<const bf16x8_t*>(PA + g * S::PA_MAT + col * S::PA_ROW +
+                                                            32 * kt + 8 * gq);
+                    g_loaded = g;
+                }
+                const uint32_t word = r.vc[kt * (D / 32) + nb / 2];
+                O[nb] = mfma(Ap, (nb % 2) == 0 ? unpack_codes<0>(word) : unpack_codes<1>(word),
+                             O[nb]);
+            }
+        }
+    };
+
+    // ---- software-pipelined chunk loop ----------------------------------------
+    // Step i finishes chunk i (value operands and o update) while it starts
+    // chunk i+1 (metadata, key operands, scores, softmax): the two halves are
+    // independent, so their latencies overlap, and each chunk costs two
+    // wave-level LDS syncs.  Chunk data come from a ring of PF register
+    // buffers filled PF chunks ahead (clamped indices, so no load is inside a
+    // branch and the compiler waits only for the chunk about to be used).
+    constexpr int PF = S::PF;
+    ChunkRegs<S> buf[PF];
+    const int n_mine = max(0, c_end - c_begin);
+    const int n_full = n_mine / PF * PF;
+    const ChunkSrc<S> src = chunk_src<S>(a, bh * a.Cmax, lane, NG);
+    bool any_cur = false;
+    if (n_mine > 0) {
+#pragma unroll
+        for (int k = 0; k < PF; ++k)
+            load_chunk<S>(buf[k], src, min(c_begin + k, c_end - 1));
+    }
+
+    // ---- this wave's slice of the fp32 residual window ------------------------
+    // Its own online-softmax state (mr, lr, orr), merged with the chunk state
+    // in LDS.  Passes of 16 tokens; scores with 4 lanes per token (a quarter
+    // of the channels each), the weighted sum with one float4 of channels per
+    // lane and 64/(D/4) token slots; every load of a pass is issued up front.
+    constexpr int F4 = D / 4;                 // float4 per token row
+    constexpr int TS = 64 / F4;               // token slots in the value pass
+    constexpr int KQ = D / 16;                // float4 per lane in the score pass
+    {
+        float mr[HG], lr[HG], orr[HG][4];
+#pragma unroll
+        for (int h = 0; h < HG; ++h) {
+            mr[h] = -INFINITY;
+            lr[h] = 0.f;
+            orr[h][0] = orr[h][1] = orr[h][2] = orr[h][3] = 0.f;
+        }
+        float* pres = qres + HG * D + wave * HG * kResPass;                      // [HG][16]
+        const int wave_idx = split * kWaves + wave;
+        const int r0 = min(wave_idx * a.res_per_wave, a.res_len);
+        const int r1 = min(r0 + a.res_per_wave, a.res_len);
+        const int tk = lane / 4, qq = lane % 4;
+        const int c4 = lane % F4, ts = lane / F4;
+        for (int t0 = r0; t0 < r1; t0 += kResPass) {
+            const int n = min(kResPass, r1 - t0);
+            // scores
+            int slot = a.res_start + t0 + min(tk, n - 1);
+            slot = slot >= a.Rcap ? slot - a.Rcap : slot;
+            const float4* krow = reinterpret_cast<const float4*>(
+                a.k_res + (bh * a.Rcap + slot) * D) + qq * KQ;
+            float4 kv[KQ];
+#pragma unroll
+            for (int j = 0; j < KQ; ++j) kv[j] = krow[j];
+            float sres[HG];
+#pragma unroll
+            for (int h = 0; h < HG; ++h) {
+                const float4* qh = reinterpret_cast<const float4*>(qres + h * D) + qq * KQ;
+                float acc = 0.f;
+#pragma unroll
+                for (int j = 0; j < KQ; ++j) {
+                    const float4 qv4 = qh[j];
+                    acc = fmaf(qv4.x, kv[j].x, acc);
+                    acc = fmaf(qv4.y, kv[j].y, acc);
+                    acc = fmaf(qv4.z, kv[j].z, acc);
+                    acc = fmaf(qv4.w, kv[j].w, acc);
+                }
+                acc += dpp<0xB1>(acc);        // quad_perm [1,0,3,2]
+                acc += dpp<0x4E>(acc);        // quad_perm [2,3,0,1]
+                sres[h] = tk < n ? acc : -INFINITY;
+            }
+#pragma unroll
+            for (int h = 0; h < HG; ++h) {
+                const float mnew = fmaxf(mr[h], wave_max(sres[h]));
+                const float alpha = mr[h] == -INFINITY ? 0.f : exp2_fast(mr[h] - mnew);
+                mr[h] = mnew;
+                const float p = tk < n ? exp2_fast(sres[h] - mnew) : 0.f;
+                lr[h] = lr[h] * alpha + 0.25f * wave_sum(p);    // each token sits in 4 lanes
+                orr[h][0] *= alpha;
+                orr[h][1] *= alpha;
+                orr[h][2] *= alpha;
+                orr[h][3] *= alpha;
+                if (qq == 0) pres[h * kResPass + tk] = p;
+            }
+            wave_sync();
+            // weighted sum of the values
+            float4 vv[kResPass / TS];
+#pragma unroll
+            for (int j = 0; j < kResPass / TS; ++j) {
+                int vs = a.res_start + t0 + min(ts + TS * j, n - 1);
+                vs = vs >= a.Rcap ? vs - a.Rcap : vs;
+                vv[j] = reinterpret_cast<const float4*>(a.v_res + (bh * a.Rcap + vs) * D)[c4];
+            }
+#pragma unroll
+            for (int j = 0; j < kResPass / TS; ++j) {
+                const int tt = ts + TS * j;
+#pragma unroll
+                for (int h = 0; h < HG; ++h) {
+                    const float p = tt < n ? pres[h * kResPass + tt] : 0.f;
+                    orr[h][0] = fmaf(p, vv[j].x, orr[h][0]);
+                    orr[h][1] = fmaf(p, vv[j].y, orr[h][1]);
+                    orr[h][2] = fmaf(p, vv[j].z, orr[h][2]);
+                    orr[h][3] = fmaf(p, vv[j].w, orr[h][3]);
+                }
+            }
+            wave_sync();
+        }
+        // fold the token slots (lanes c4, c4 + F4, ... hold the same channels)
+        // and park the slice's state in LDS until the merge
+#pragma unroll
+        for (int sh = F4; sh < 64; sh <<= 1) {
+#pragma unroll
+            for (int h = 0; h < HG; ++h) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) orr[h][i] += __shfl_xor(orr[h][i], sh);
+            }
+        }
+        float* rst = rstates + wave * S::RSTATE;
+        if (lane < F4) {
+#pragma unroll
+            for (int h = 0; h < HG; ++h) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) rst[h * D + 4 * lane + i] = orr[h][i];
+            }
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int h = 0; h < HG; ++h) {
+                rst[HG * D + h] = mr[h];
+                rst[HG * D + HG + h] = lr[h];
+            }
+        }
+    }
+
+
+    if (n_mine > 0) {
+        stage_meta<S>(buf[0], MT, lane, NG, meta_floats);
+        wave_sync();
+        wprep(Int<0>{});
+        wave_sync();
+        any_cur = kside(buf[0], Int<0>{});
+    }
+    // Step i (of the wave's chunks, counted from c_begin) uses double-buffer
+    // slot i & 1; PF is even, so within the unrolled ring the slot of step k
+    // is k & 1, a compile-time constant.
+    auto step = [&](const ChunkRegs<S>& cur, const ChunkRegs<S>& nxt, int i, auto slot_c) {
+        constexpr int slot = decltype(slot_c)::value, nslot = slot ^ 1;
+        const bool has_next = i + 1 < c_end;
+        if (has_next) stage_meta<S>(nxt, MT + nslot * meta_floats, lane, NG, meta_floats);
+        wave_sync();
+        if (has_next) wprep(Int<nslot>{});
+        pprep(Int<slot>{}, any_cur);
+        wave_sync();
+        vside(cur);
+        if (has_next) any_cur = kside(nxt, Int<nslot>{});
+    };
+    static_assert(PF % 2 == 0, "the slot parity of a ring step must be static");
+    for (int c0 = c_begin; c0 < c_begin + n_full; c0 += PF) {
+        static_for<0, PF>([&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            step(buf[k], buf[(k + 1) % PF], c0 + k, Int<k & 1>{});
+            load_chunk<S>(buf[k], src, min(c0 + k + PF, c_end - 1));
+        });
+    }
+    static_for<0, PF>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        if (k < n_mine - n_full) step(buf[k], buf[(k + 1) % PF], c_begin + n_full + k, Int<k & 1>{});
+    });
+
+    // ---- wave state -> merge slot --------------------------------------------
+    wave_sync();
+#pragma unroll
+    for (int it = 0; it < S::NEV; ++it) {
+        const int e = lane + 64 * it;
+        if (e < n_items) VB[e] = vb[it];          // [h][g][seg]
+    }
+    float l_tot[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) l_tot[e] = row_sum16(l_part[e]);
+    wave_sync();
+    // Gather this wave's value corrections before the merge slot (which
+    // overlaps the per-wave LDS) is written.
+    float vcorr[2][S::NBV];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int h = 2 * gq + e;
+#pragma unroll
+        for (int nb = 0; nb < S::NBV; ++nb) {
+            float v = 0.f;
+            if (h < HG) {
+                const int g = (16 * nb + col) / a.Gv;
+                const float* pv = VB + (h * NG + g) * NSEG;
+#pragma unroll
+                for (int sg = 0; sg < NSEG; ++sg) v += pv[sg];
+            }
+            vcorr[e][nb] = v;
+        }
+    }
+    __syncthreads();
+    float* slot = merge_slot(smem, HG, D, wave);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int h = 2 * gq + e;
+        if (h < HG) {
+#pragma unroll
+            for (int nb = 0; nb < S::NBV; ++nb)
+                slot[h * D + 16 * nb + col] = O[nb][2 * e] + O[nb][2 * e + 1] + vcorr[e][nb];
+            if (col == 0) {
+                slot[HG * D + h] = m_run[e];
+                slot[HG * D + HG + h] = l_tot[e];
+            }
+        }
+    }
+    merge_and_store<HG, D>(smem, rstates, a, split, kvh, b);
+}
+
+// Occupancy target: two waves per SIMD where the 4-deep prefetch ring fits
+// that register budget without spilling (head_dim 64, or head_dim 128 with
+// up to 4 query heads per kv head); that measured faster than three waves
+// with a 2-deep ring.  Larger shapes keep the full register file (one wave
+// per SIMD).
+template <int HG, int D>
+constexpr int attn_waves_per_eu() { return (D <= 64 || (D <= 128 && HG <= 4)) ? 2 : 1; }
+
+template <int HG, int D, int G>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<HG, D>())))
+void attn_mfma_kernel(AttnLaunch a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    using S = Shape<HG, D, G>;
+    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    wave_path<S>(smem, a, split, kvh, b);
+}
+
+int max_lds_per_block() {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+        return 64 * 1024;
+    return v;
+}
+
+template <int HG, int D, int G>
+int launch_shape(const AttnLaunch& a, hipStream_t st) {
+    using S = Shape<HG, D, G>;
+    static const int lds_limit = max_lds_per_block();
+    const int lds = S::lds(D / a.Gv);
+    if (lds > lds_limit)
+        return set_error(kErrUnsupported,
+                         "decode attention with q_heads/kv_heads=%d, head_dim=%d, G=%d, "
+                         "group_size_v=%d needs %d bytes of LDS per workgroup; the device "
+                         "allows %d", HG, D, G, a.Gv, lds, lds_limit);
+    const dim3 grid(a.n_splits, a.Hkv, a.B);
+    attn_mfma_kernel<HG, D, G><<<grid, kBlock, lds, st>>>(a);
+    return check_launch("packed_decode_attention (mfma)");
+}
+
+template <int HG, int D>
+int launch_g(const AttnLaunch& a, hipStream_t st) {
+    return a.G == 32 ? launch_shape<HG, D, 32>(a, st) : launch_shape<HG, D, 64>(a, st);
+}
+
+template <int HG>
+int launch_d(const AttnLaunch& a, hipStream_t st) {
+    switch (a.D) {
+        case 64: return launch_g<HG, 64>(a, st);
+        case 128: return launch_g<HG, 128>(a, st);
+        default: return launch_g<HG, 256>(a, st);
+    }
+}
+
+}  // namespace
+
+int launch_attention_mfma(const AttnLaunch& a, hipStream_t st) {
+    switch (a.Hq / a.Hkv) {
+        case 1: return launch_d<1>(a, st);
+        case 2: return launch_d<2>(a, st);
+        case 4: return launch_d<4>(a, st);
+        default: return launch_d<8>(a, st);
+    }
+}
+
+
+}  // namespace kivi

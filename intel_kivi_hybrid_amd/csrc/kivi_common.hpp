@@ -35,6 +35,38 @@ int check_launch(const char* what);
 int check_hip(hipError_t err, const char* what);
 
 // ---------------------------------------------------------------------------
+// Packed-store code layouts (shared by the flush and attention kernels).
+//
+// kLayoutPlain: per chunk of G tokens, key codes [G][D/4] bytes (byte (t, i)
+//   holds channels 4i..4i+3 of token t, channel 4i+k at bits 2k) and value
+//   codes [D][G/4] bytes (byte (d, j) holds tokens 4j..4j+3 of channel d).
+// kLayoutMfma: the chunk's codes are the B operands of
+//   v_mfma_f32_16x16x32_bf16, stored lane-major: [64 lanes][NP dwords] per
+//   chunk for keys and for values, NP = G*D/1024.  A "tile" is one MFMA B
+//   operand: 64 lanes x 8 codes.  Tiles are numbered
+//     keys:   tile = ks*(G/16) + nb   (nb: 16-token block, ks: 32-channel step)
+//             lane l, element j -> token 16*nb + l%16, channel 32*ks + 8*(l/16) + j
+//     values: tile = kt*(D/16) + nb  (kt: 32-token step, nb: 16-channel block)
+//             lane l, element j -> token 32*kt + 8*(l/16) + j, channel 16*nb + l%16
+//   and tiles 2w and 2w+1 share dword w of each lane: element j of tile
+//   2w+m sits at bits  8*m + 2*(j/2) + 16*(j%2).
+// Scales/zeros are the same in both layouts: keys [D] per chunk, values
+// [D/Gv][G] per chunk (group-major).
+// ---------------------------------------------------------------------------
+enum CodeLayout : int { kLayoutPlain = 0, kLayoutMfma = 1 };
+
+inline int code_layout_for(int D, int G, int Gv) {
+    const bool d_ok = D == 64 || D == 128 || D == 256;
+    const bool g_ok = G == 32 || G == 64;
+    const bool gv_ok = Gv > 0 && Gv % 32 == 0 && D % Gv == 0;
+    return (d_ok && g_ok && gv_ok) ? kLayoutMfma : kLayoutPlain;
+}
+
+__host__ __device__ constexpr int mfma_code_bit(int m, int j) {
+    return 8 * m + 2 * (j / 2) + 16 * (j % 2);
+}
+
+// ---------------------------------------------------------------------------
 // Device helpers.
 // ---------------------------------------------------------------------------
 

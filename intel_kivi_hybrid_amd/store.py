@@ -36,6 +36,43 @@ def _stream(device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+def _pack_last(codes: torch.Tensor) -> torch.Tensor:
+    """[..., N] codes (one per byte) -> [..., N/4] bytes, element 4j+k at bits 2k."""
+    c = codes.to(torch.int32).reshape(*codes.shape[:-1], codes.shape[-1] // 4, 4)
+    return (c[..., 0] | (c[..., 1] << 2) | (c[..., 2] << 4) | (c[..., 3] << 6)).to(torch.uint8)
+
+
+_MAPS = {}
+
+
+def _mfma_maps(G: int, D: int, key: bool):
+    """For the matrix-core code layout: the flat [G][D] index of every
+    (lane, word, tile-in-word, element) and the bit shift of each of the 16
+    codes of a word (include/kivi_hip.h documents the layout)."""
+    cache_key = (G, D, key)
+    if cache_key not in _MAPS:
+        np_ = G * D // 1024
+        flat = torch.empty(64, np_, 16, dtype=torch.long)
+        shifts = torch.empty(16, dtype=torch.int32)
+        for m in range(2):
+            for j in range(8):
+                shifts[8 * m + j] = 8 * m + 2 * (j // 2) + 16 * (j % 2)
+        for lane in range(64):
+            for w in range(np_):
+                for m in range(2):
+                    tile = 2 * w + m
+                    for j in range(8):
+                        if key:
+                            ks, nb = divmod(tile, G // 16)
+                            t, d = 16 * nb + lane % 16, 32 * ks + 8 * (lane // 16) + j
+                        else:
+                            kt, nb = divmod(tile, D // 16)
+                            t, d = 32 * kt + 8 * (lane // 16) + j, 16 * nb + lane % 16
+                        flat[lane, w, 8 * m + j] = t * D + d
+        _MAPS[cache_key] = (flat.reshape(-1), shifts)
+    return _MAPS[cache_key]
+
+
 class PackedKVStore:
     """Residual ring + packed chunks for one layer (all on ``device``)."""
 
@@ -51,6 +88,8 @@ class PackedKVStore:
             raise ValueError("residual capacity must hold at least one group")
         self.B, self.H, self.D = batch, kv_heads, head_dim
         self.G, self.Gv, self.R = group_size, gv, residual_capacity
+        # 1: codes stored in matrix-core operand order, 0: plain byte order
+        self.code_layout = int(_lib.kivi_store_code_layout(head_dim, group_size, gv))
         self.device = torch.device(device)
         self.keep_history = keep_history
         f32 = dict(dtype=torch.float32, device=self.device)
@@ -64,16 +103,16 @@ class PackedKVStore:
 
     # ------------------------------------------------------------------ alloc
     def _alloc(self, cap: int) -> None:
-        B, H, D, G, gpt = self.B, self.H, self.D, self.G, self.D // self.Gv
+        B, H, D, G, ng = self.B, self.H, self.D, self.G, self.D // self.Gv
         u8 = dict(dtype=torch.uint8, device=self.device)
         f32 = dict(dtype=torch.float32, device=self.device)
         new = {
-            "k_codes": torch.empty(B, H, cap, G, D // 4, **u8),
+            "k_codes": torch.empty(B, H, cap, G * D // 4, **u8),
             "k_scale": torch.empty(B, H, cap, D, **f32),
             "k_zero": torch.empty(B, H, cap, D, **f32),
-            "v_codes": torch.empty(B, H, cap, D, G // 4, **u8),
-            "v_scale": torch.empty(B, H, cap, G, gpt, **f32),
-            "v_zero": torch.empty(B, H, cap, G, gpt, **f32),
+            "v_codes": torch.empty(B, H, cap, G * D // 4, **u8),
+            "v_scale": torch.empty(B, H, cap, ng, G, **f32),
+            "v_zero": torch.empty(B, H, cap, ng, G, **f32),
         }
         if self.keep_history:
             new["k_hist"] = torch.empty(B, H, cap * G, D, **f32)
@@ -162,20 +201,45 @@ class PackedKVStore:
         self.res_start = self.res_len = self.n_chunks = 0
 
     # ---------------------------------------------------------- inspection
+    def _codes(self, which: str, chunk: int) -> torch.Tensor:
+        """One chunk's 2-bit codes, one byte per element, as [B, Hkv, G, D]."""
+        B, H, G, D = self.B, self.H, self.G, self.D
+        raw = getattr(self, which)[:, :, chunk]
+        if self.code_layout == 0:
+            b = raw.reshape(B, H, -1).to(torch.int32)
+            c = torch.stack([(b >> (2 * k)) & 3 for k in range(4)], dim=-1).reshape(B, H, -1)
+            if which == "k_codes":
+                return c.reshape(B, H, G, D).to(torch.uint8)
+            return c.reshape(B, H, D, G).transpose(2, 3).contiguous().to(torch.uint8)
+        words = raw.contiguous().view(torch.int32).reshape(B, H, -1)     # [B, H, 64*NP]
+        flat, shifts = _mfma_maps(G, D, which == "k_codes")
+        vals = (words[..., :, None] >> shifts.to(raw.device)) & 3        # [B, H, 64*NP, 16]
+        out = torch.empty(B, H, G * D, dtype=torch.int32, device=raw.device)
+        out[..., flat.to(raw.device)] = vals.reshape(B, H, -1)
+        return out.reshape(B, H, G, D).to(torch.uint8)
+
     def unpermuted_k_codes(self, chunk: int) -> torch.Tensor:
         """Key codes of one chunk as ``[B, Hkv, G, D/4]`` bytes: byte (t, i)
         holds channels 4i..4i+3 of token t, channel 4i+k at bits 2k."""
-        return self.k_codes[:, :, chunk]
+        return _pack_last(self._codes("k_codes", chunk))
 
     def unpermuted_v_codes(self, chunk: int) -> torch.Tensor:
         """Value codes of one chunk as ``[B, Hkv, D, G/4]`` bytes: byte (d, j)
         holds tokens 4j..4j+3 of channel d, token 4j+k at bits 2k."""
-        return self.v_codes[:, :, chunk]
+        return _pack_last(self._codes("v_codes", chunk).transpose(2, 3))
+
+    def chunk_v_scale(self, chunk: int) -> torch.Tensor:
+        """Value scales of one chunk as ``[B, Hkv, G, D/Gv]`` (token-major)."""
+        return self.v_scale[:, :, chunk].transpose(2, 3)
+
+    def chunk_v_zero(self, chunk: int) -> torch.Tensor:
+        return self.v_zero[:, :, chunk].transpose(2, 3)
 
     # ------------------------------------------------------------ attention
     def workspace_bytes(self, q_heads: int, num_splits: int = 0) -> int:
         return int(_lib.kivi_packed_decode_attention_workspace_size(
-            self.B, q_heads, self.H, self.D, self.n_chunks, self.res_len, num_splits))
+            self.B, q_heads, self.H, self.D, self.G, self.Gv, self.n_chunks, self.res_len,
+            num_splits))
 
     def attention(self, q: torch.Tensor, softmax_scale: Optional[float] = None,
                   out: Optional[torch.Tensor] = None, num_splits: int = 0,

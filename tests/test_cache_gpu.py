@@ -142,9 +142,11 @@ def test_config1_cache_full_size(KiviCache):
         o = oracle_chunk(k_all[:, :, c * G:(c + 1) * G], v_all[:, :, c * G:(c + 1) * G], G, G)
         assert np.array_equal(st.unpermuted_k_codes(c).cpu().numpy(), o["k_codes"])
         assert np.array_equal(st.unpermuted_v_codes(c).cpu().numpy(), o["v_codes"])
-        for name in ("k_scale", "k_zero", "v_scale", "v_zero"):
-            got = getattr(st, name)[:, :, c].cpu().numpy().view(np.uint32)
-            assert np.array_equal(got, o[name].view(np.uint32)), f"{name} chunk {c}"
+        got = {"k_scale": st.k_scale[:, :, c], "k_zero": st.k_zero[:, :, c],
+               "v_scale": st.chunk_v_scale(c), "v_zero": st.chunk_v_zero(c)}
+        for name, t in got.items():
+            bits = t.contiguous().cpu().numpy().view(np.uint32)
+            assert np.array_equal(bits, o[name].view(np.uint32)), f"{name} chunk {c}"
 
 
 @pytest.mark.parametrize("Hq", [12, 24])

@@ -45,12 +45,14 @@ def test_flush_bit_exact(store_cls, B, H, D, G, Gv, R, T):
     assert st.n_chunks == n_flush and st.res_len == T - n_flush * G
     for c in range(st.n_chunks):
         o = oracle_chunk(k[:, :, c * G:(c + 1) * G], v[:, :, c * G:(c + 1) * G], G, Gv)
-        assert np.array_equal(st.k_codes[:, :, c].cpu().numpy(), o["k_codes"]), f"k codes chunk {c}"
+        assert np.array_equal(st.unpermuted_k_codes(c).cpu().numpy(), o["k_codes"]), \
+            f"k codes chunk {c}"
         assert np.array_equal(_u32(st.k_scale[:, :, c]), o["k_scale"].view(np.uint32))
         assert np.array_equal(_u32(st.k_zero[:, :, c]), o["k_zero"].view(np.uint32))
-        assert np.array_equal(st.v_codes[:, :, c].cpu().numpy(), o["v_codes"]), f"v codes chunk {c}"
-        assert np.array_equal(_u32(st.v_scale[:, :, c]), o["v_scale"].view(np.uint32))
-        assert np.array_equal(_u32(st.v_zero[:, :, c]), o["v_zero"].view(np.uint32))
+        assert np.array_equal(st.unpermuted_v_codes(c).cpu().numpy(), o["v_codes"]), \
+            f"v codes chunk {c}"
+        assert np.array_equal(_u32(st.chunk_v_scale(c).contiguous()), o["v_scale"].view(np.uint32))
+        assert np.array_equal(_u32(st.chunk_v_zero(c).contiguous()), o["v_zero"].view(np.uint32))
         kh = st.k_hist[:, :, c * G:(c + 1) * G]
         vh = st.v_hist[:, :, c * G:(c + 1) * G]
         assert np.array_equal(_u32(kh), o["k_deq"].view(np.uint32)), f"k history chunk {c}"
@@ -118,3 +120,36 @@ def test_attention_reference_cosine_gate(store_cls, kat):
                                                 torch.from_numpy(ref).reshape(1, -1)).item()
     print(f"[attn] cosine vs fp32 = {cos:.4f}", flush=True)
     assert cos > g["min_cosine"]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,G,Gv,R,T", [
+    (2, 32, 8, 128, 32, 32, 128, 4196),     # config-4 head geometry, 2 sequences
+    (1, 16, 2, 256, 32, 64, 64, 1000),      # D=256, Gv=64
+    (1, 16, 2, 128, 64, 64, 128, 2000),     # GQA 8, G=64
+    (2, 4, 4, 256, 64, 256, 64, 700),       # MHA, D=256, one value group per token
+    (3, 8, 4, 64, 32, 64, 96, 1500),        # D=64, Gv=64
+])
+def test_attention_matrix_core_shapes(store_cls, B, Hq, Hkv, D, G, Gv, R, T):
+    """Every matrix-core instantiation family against float64 attention."""
+    st_layout = store_cls(1, 1, D, G, R, "cuda:0", group_size_v=Gv).code_layout
+    assert st_layout == 1
+    _attention_case(store_cls, B, Hq, Hkv, D, G, Gv, R, T, seed=7)
+
+
+def test_attention_outlier_heavy_scores(store_cls):
+    """Large query norms make the softmax nearly one-hot and exercise the
+    running-maximum rescale path (scores jump by far more than 8 in log2)."""
+    B, Hq, Hkv, D, G, R, T = 1, 8, 2, 128, 32, 64, 900
+    k, v = make_kv(B, Hkv, T, D, seed=41)
+    k[:, :, 700] *= 6.0                       # a late, dominant key
+    st = store_cls(B, Hkv, D, G, R, "cuda:0")
+    fill_store(st, k, v, R)
+    q = seeded_q(B, Hq, D, seed=43) * 40.0
+    out = st.attention(q.cuda())
+    torch.cuda.synchronize()
+    kh, vh = oracle_history(k, v, st.n_chunks, G, G)
+    q0 = st.n_chunks * G
+    ref = decode_attention(q.numpy(), kh, vh, k[:, :, q0:].numpy(), v[:, :, q0:].numpy())
+    err = rel_err(out.cpu().numpy(), ref)
+    print(f"[attn] outlier-heavy rel_err={err:.3e}", flush=True)
+    assert err <= ATTN_TOL
