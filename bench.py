@@ -1,6 +1,6 @@
 """KIVI hot-path benchmark on one MI355X.
 
-Headline (``value``): packed-KV decode throughput at BASELINE config 4
+Headline (``value``): packed-KV decode throughput at benchmark config 4
 (Llama-3-8B GQA shape: B=64, 32 q heads / 8 kv heads, D=128, 8K context,
 R=128, G=32).  One step = append the new token's K/V to the HBM residual
 ring, flush 32 tokens into the packed store whenever the residual reaches R,
@@ -261,8 +261,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--attn-iters", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["config4", "attention", "quantize"], default=None,
-                    help="run one workload (for profiling)")
+    ap.add_argument("--only", choices=["config4", "attention", "quantize", "copy"], default=None,
+                    help="run one workload (for profiling); 'copy' is a plain 512 MiB device "
+                         "copy used to calibrate the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the KIVI hot path here is built and "
@@ -274,6 +275,16 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     dev = torch.device("cuda:0")
     log = lambda *a: print(*a, file=sys.stderr, flush=True)      # noqa: E731
+
+    if args.only == "copy":
+        n = 512 << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(7)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copy: {n} bytes read and {n} bytes written per launch, 5 launches")
+        return
 
     # ---- config 4: the headline decode loop -------------------------------
     B, Hq, Hkv, D, T, R, G = 64, 32, 8, 128, 8192, 128, 32

@@ -356,9 +356,9 @@ Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
     return p;
 }
 
-// Partials are needed whenever more than one workgroup covers a row; the
-// matrix-core kernel always writes partials.
-bool needs_workspace(const Plan& p) { return p.layout == kLayoutMfma || p.n_splits > 1; }
+// Partials (and the merge kernel) are needed whenever more than one
+// workgroup covers a row.
+bool needs_workspace(const Plan& p) { return p.n_splits > 1; }
 
 }  // namespace
 }  // namespace kivi
@@ -451,7 +451,7 @@ int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const f
                      p.n_qsplits, p.chunks_per_wave, p.res_per_wave, p.n_splits,
                      softmax_scale * kLog2e};
         int rc = launch_attention_mfma(L, st);
-        if (rc) return rc;
+        if (rc || !needs_workspace(p)) return rc;
     } else {
         AttnArgs a{q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res, v_res, out,
                    part_o, part_ml, q_heads, kv_heads, head_dim, group_size_k, group_size_v,

@@ -18,7 +18,7 @@ struct AttnLaunch {
     const float* k_res;      // [B, Hkv, Rcap, D] ring
     const float* v_res;
     float* out;              // [B, Hq, D]
-    float* part_o;           // [B, Hq, n_splits, D]
+    float* part_o;           // [B, Hq, n_splits, D] (n_splits > 1 only)
     float* part_ml;          // [B, Hq, n_splits, 2]
     int B, Hq, Hkv, D, G, Gv, Cmax, n_chunks, Rcap, res_start, res_len;
     int n_qsplits;           // workgroups per (b, kv-head)
@@ -29,7 +29,8 @@ struct AttnLaunch {
 };
 
 // Launches the matrix-core kernel (kLayoutMfma stores, Hq/Hkv in {1,2,4,8}).
-// Always writes partials; the caller runs the merge.
+// With n_splits == 1 it writes `out`; otherwise partials, which the caller
+// merges.
 int launch_attention_mfma(const AttnLaunch& a, hipStream_t stream);
 
 }  // namespace kivi

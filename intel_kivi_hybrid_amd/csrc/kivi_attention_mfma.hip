@@ -221,7 +221,8 @@ __device__ __forceinline__ float* merge_slot(unsigned char* smem, int HG, int D,
 }
 
 // Combines the 4 chunk states (merge slots) and the 4 residual-slice states
-// of the workgroup and writes one partial (o, m, l) row per query head.
+// of the workgroup and writes one partial (o, m, l) row per query head, or the
+// normalised output when the workgroup is the row's only split.
 template <int HG, int D>
 __device__ void merge_and_store(unsigned char* smem, const float* rstates, const AttnLaunch& a,
                                 int split, int kvh, int b) {
@@ -242,6 +243,10 @@ __device__ void merge_and_store(unsigned char* smem, const float* rstates, const
             const float f = mw == -INFINITY ? 0.f : exp2_fast(mw - M);
             acc = fmaf(f, s[h * D + d], acc);
             L = fmaf(f, s[HG * D + HG + h], L);
+        }
+        if (a.n_splits == 1) {          // the only partial of its row: finish here
+            a.out[(hq0 + h) * D + d] = acc / L;
+            continue;
         }
         const int64_t row = (hq0 + h) * a.n_splits + split;
         a.part_o[row * D + d] = acc;

@@ -30,7 +30,7 @@ def hip_device():
 
 
 def seeded_kv(shape, seed, kind, outlier_axis=-1):
-    """Seeded synthetic K/V with the BASELINE outlier pattern, made on the CPU.
+    """Seeded synthetic K/V with the benchmark outlier pattern, made on the CPU.
 
     kind="key":   N(0,1), 4 fixed channels (last axis) scaled x10.
     kind="value": N(0,1), round(2% of the token axis) scaled x8.

@@ -118,7 +118,7 @@ def test_explicit_flush_group(KiviCache):
 
 
 def test_config1_cache_full_size(KiviCache):
-    """GPT-2-small-shaped cache, 12 layers, B=1, H=12,
+    """Benchmark config 1: GPT-2-small-shaped cache, 12 layers, B=1, H=12,
     D=64, R=G=32, 200 decode steps of seeded K/V with channel/token
     outliers.  Served K/V, packed bytes, scales/zeros and accounting."""
     layers, B, H, D, G, R, T = 12, 1, 12, 64, 32, 32, 200

@@ -106,7 +106,7 @@ def test_readme_accounting_replayed():
 
 
 def test_config1_accounting_and_history():
-    """12 layers, B=1, H=12, D=64, R=G=32, 200 steps."""
+    """Benchmark config 1: 12 layers, B=1, H=12, D=64, R=G=32, 200 steps."""
     layers, B, H, D, G = 12, 1, 12, 64, 32
     cache = KiviCacheOracle(layers, D, None, G, G)
     k_all, v_all = _feed_seeded(cache, layers, B, H, D, 200, seed=1235)

@@ -172,7 +172,7 @@ def test_tie_heavy_inputs_take_exact_path(C):
     _assert_codec_parity(C, x, 32)
 
 
-# ---- BASELINE config 2 at full size ----------------------------------------
+# ---- benchmark config 2 at full size ---------------------------------------
 def test_config2_full_size_bit_exact(C):
     """keys [8,32,128,4096] G=32 along tokens, values [8,32,4096,128] G=32."""
     k = seeded_kv((8, 32, 4096, 128), seed=1236, kind="key").transpose(2, 3).contiguous()

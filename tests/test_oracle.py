@@ -175,7 +175,7 @@ def test_stats_closed_form_matches_readme(kat):
 
 
 def test_config1_expected_accounting():
-    # 12 layers, B=1, H=12, D=64, R=G=32, 200 tokens.
+    # Benchmark config 1: 12 layers, B=1, H=12, D=64, R=G=32, 200 tokens.
     s = closed_form_stats(1, 12, 64, 32, 32, 200)
     assert s["quantized_tokens"] == 192 and s["residual_tokens"] == 8
     assert s["kivi_bytes"] == 196608 and s["fp32_bytes"] == 1228800

@@ -32,7 +32,7 @@ def _u32(t):
 
 @pytest.mark.parametrize("B,H,D,G,Gv,R,T", [
     (1, 2, 8, 4, 4, 8, 30),          # the reference unit-test geometry (G=4, R=8, D=8)
-    (1, 12, 64, 32, 32, 32, 200),    # BASELINE config 1 geometry
+    (1, 12, 64, 32, 32, 32, 200),    # benchmark config 1 geometry
     (2, 3, 128, 32, 128, 48, 170),   # Gv != G, ring wrap (R not a multiple of G)
     (2, 2, 64, 16, 16, 40, 133),
 ])
