@@ -78,6 +78,21 @@ def build_store(B, Hkv, D, G, Gv, R, T, seed, device, extra_chunks=16):
     return st
 
 
+def settle_clocks(fn, seconds=0.05, min_calls=20):
+    """Runs fn back to back for ~`seconds` of GPU time (untimed).  From idle,
+    MI355X clocks take tens of milliseconds to ramp up: timing without this
+    reports the first calls ~20% slow."""
+    import torch
+    t0 = time.perf_counter()
+    n = 0
+    while n < min_calls or time.perf_counter() - t0 < seconds:
+        fn()
+        n += 1
+        if n % 10 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+
+
 def time_attention(st, Hq, iters, seed, device):
     """Average duration of one fused-attention call (HIP events on the launch
     stream), and its algorithmic bytes."""
@@ -85,9 +100,7 @@ def time_attention(st, Hq, iters, seed, device):
     g = torch.Generator(device=device).manual_seed(seed)
     q = torch.randn(st.B, Hq, st.D, generator=g, device=device) * st.D ** -0.5
     out = torch.empty_like(q)
-    for _ in range(3):
-        st.attention(q, out=out)
-    torch.cuda.synchronize()
+    settle_clocks(lambda: st.attention(q, out=out))
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
     for i in range(iters):
@@ -119,6 +132,7 @@ def decode_loop(st, Hq, steps, warmup, R, seed, device):
         st.attention(q_all[i], out=out)
         return nb, flushes
 
+    settle_clocks(lambda: st.attention(q_all[0], out=out))
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()

@@ -361,6 +361,15 @@ Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
 bool needs_workspace(const Plan& p) { return p.n_splits > 1; }
 
 }  // namespace
+
+int launch_attention_mfma(const AttnLaunch& a, hipStream_t st) {
+    switch (a.Hq / a.Hkv) {
+        case 1: return launch_attention_mfma_hg1(a, st);
+        case 2: return launch_attention_mfma_hg2(a, st);
+        case 4: return launch_attention_mfma_hg4(a, st);
+        default: return launch_attention_mfma_hg8(a, st);
+    }
+}
 }  // namespace kivi
 
 using namespace kivi;

@@ -1,5 +1,5 @@
 // Internal interface between the decode-attention entry point
-// (kivi_attention.hip) and its matrix-core kernel (kivi_attention_mfma.hip).
+// (kivi_attention.hip) and its matrix-core kernel (kivi_attention_mfma.hpp).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -30,7 +30,13 @@ struct AttnLaunch {
 
 // Launches the matrix-core kernel (kLayoutMfma stores, Hq/Hkv in {1,2,4,8}).
 // With n_splits == 1 it writes `out`; otherwise partials, which the caller
-// merges.
+// merges.  The kernel templates live in kivi_attention_mfma.hpp; each
+// Hq/Hkv ratio is instantiated in its own translation unit
+// (kivi_attention_mfma_hg<N>.hip) so that the build compiles them in parallel.
 int launch_attention_mfma(const AttnLaunch& a, hipStream_t stream);
+int launch_attention_mfma_hg1(const AttnLaunch& a, hipStream_t stream);
+int launch_attention_mfma_hg2(const AttnLaunch& a, hipStream_t stream);
+int launch_attention_mfma_hg4(const AttnLaunch& a, hipStream_t stream);
+int launch_attention_mfma_hg8(const AttnLaunch& a, hipStream_t stream);
 
 }  // namespace kivi

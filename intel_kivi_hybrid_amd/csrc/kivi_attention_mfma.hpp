@@ -38,6 +38,8 @@
 // states in LDS; workgroups past the chunk splits take the fp32 residual
 // window with plain fp32 FMAs.  Each workgroup writes a partial (o, m, l)
 // that kivi_attention.hip's merge kernel combines with log-sum-exp weights.
+#pragma once
+
 #include <math.h>
 
 #include "kivi_common.hpp"
@@ -117,20 +119,25 @@ __device__ __forceinline__ UnpackConsts unpack_consts() {
     return c;
 }
 
+// Code word -> B operand of tile M (four dwords of two bf16 "8 + c" each).
+// Element j of the tile sits at bit 8M + 2(j/2) of the low (j even) or high
+// (j odd) half of the word and is moved to mantissa bits 5:4.  (Reading some
+// codes at lower mantissa bits saves shifts but needs an MFMA against -8 per
+// operand to keep the precision; at ~8 VALU ops per MFMA of issue time that
+// measured slower.)
 template <int M>
 __device__ __forceinline__ bf16x8_t unpack_codes(uint32_t x, UnpackConsts k) {
-    const uint32_t kMask = k.mask, kBase = k.base;
     u32x4_t o;
     if constexpr (M == 0) {
-        o[0] = and_or(x << 4, kMask, kBase);
-        o[1] = and_or(x << 2, kMask, kBase);
-        o[2] = and_or(x, kMask, kBase);
-        o[3] = and_or(x >> 2, kMask, kBase);
+        o[0] = and_or(x << 4, k.mask, k.base);
+        o[1] = and_or(x << 2, k.mask, k.base);
+        o[2] = and_or(x, k.mask, k.base);
+        o[3] = and_or(x >> 2, k.mask, k.base);
     } else {
-        o[0] = and_or(x >> 4, kMask, kBase);
-        o[1] = and_or(x >> 6, kMask, kBase);
-        o[2] = and_or(x >> 8, kMask, kBase);
-        o[3] = and_or(x >> 10, kMask, kBase);
+        o[0] = and_or(x >> 4, k.mask, k.base);
+        o[1] = and_or(x >> 6, k.mask, k.base);
+        o[2] = and_or(x >> 8, k.mask, k.base);
+        o[3] = and_or(x >> 10, k.mask, k.base);
     }
     return __builtin_bit_cast(bf16x8_t, o);
 }
@@ -160,16 +167,19 @@ __device__ __forceinline__ float row_sum16(float v) {
     return v + dpp<0x121>(v);
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
-    return v;
+// Across the wave: DPP within each 16-lane row, then the four row results
+// through readlane.  (__shfl_xor compiles to ds_bpermute, a chain of six LDS
+// round trips.)
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
-
+__device__ __forceinline__ float wave_max(float v) {
+    v = row_max16(v);
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-    return v;
+    v = row_sum16(v);
+    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -398,14 +408,18 @@ __device__ __forceinline__ void stage_meta(const ChunkRegs<S>& r, float* MT, int
     }
 }
 
-template <class S>
+// NGC > 0: the number of value groups per token (D / Gv) is NGC at compile
+// time, so the value operand of every n-block is known statically and its
+// LDS reads can be issued ahead; NGC == 0 reads it from the launch.
+template <class S, int NGC>
 __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, int kvh, int b) {
     constexpr int HG = S::HG, D = S::D, G = S::G, NSUB = S::NSUB, NB = G / 16, NSEG = G / 8;
     // wave-uniform in an SGPR: chunk ranges, ring indices and branches on
     // them stay scalar
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x % kWave;
-    const int NG = D / a.Gv;
+    const int NG = NGC > 0 ? NGC : D / a.Gv;
+    const int Gv = NGC > 0 ? D / NGC : a.Gv;
     const int64_t bh = (int64_t)b * a.Hkv + kvh;
 
     unsigned char* wl = smem + wave * S::wave_lds(NG);
@@ -436,8 +450,14 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         qv[i] = wlane ? a.q[((int64_t)b * a.Hq + kvh * HG + wh) * D + wseg * S::CPL + i] * a.qscale
                       : 0.f;
 
-    const int c_begin = (split * kWaves + wave) * a.chunks_per_wave;
-    const int c_end = min(c_begin + a.chunks_per_wave, a.n_chunks);
+    // The workgroup's chunks [g_begin, g_end) are dealt to its waves in turn
+    // (wave w takes g_begin + w + kWaves*j): the four waves of a workgroup
+    // then read neighbouring chunks, which streams from HBM measurably faster
+    // than four separate contiguous ranges.
+    const int g_begin = split * kWaves * a.chunks_per_wave;
+    const int g_end = min(g_begin + kWaves * a.chunks_per_wave, a.n_chunks);
+    const int n_mine = max(0, (g_end - g_begin - wave + kWaves - 1) / kWaves);
+    auto chunk_of = [&](int j) { return g_begin + wave + kWaves * min(j, n_mine - 1); };
 
     f32x4_t O[S::NBV];
 #pragma unroll
@@ -528,18 +548,21 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
 #pragma unroll
         for (int kb = 0; kb < S::NBB; ++kb)
             Ab[kb] = *reinterpret_cast<const bf16x8_t*>(BA + col * S::BA_ROW + 32 * kb + 8 * gq);
+        // The correction is the same for every token: one accumulator, shared
+        // as the starting value of every n-block's chain.
+        f32x4_t s0 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < S::NBB; ++kb) s0 = mfma(Ab[kb], ones, s0);
         f32x4_t Sc[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+            f32x4_t acc = s0;
 #pragma unroll
             for (int ks = 0; ks < S::KS; ++ks) {
                 const uint32_t word = r.kc[ks * NSUB + nb / 2];
                 acc = mfma(Aw[ks], (nb % 2) == 0 ? unpack_codes<0>(word, uc) : unpack_codes<1>(word, uc),
                            acc);
             }
-#pragma unroll
-            for (int kb = 0; kb < S::NBB; ++kb) acc = mfma(Ab[kb], ones, acc);
             Sc[nb] = acc;
         }
         // A head's running max moves only when its chunk max exceeds it by
@@ -556,7 +579,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             }
         }
         const bool any = __builtin_amdgcn_ballot_w64(over) != 0;
-        if (any) {
+        if (__builtin_expect(any, 0)) {
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
                 float cm = sc[e][0];
@@ -663,7 +686,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             bf16x8_t Ap;
 #pragma unroll
             for (int nb = 0; nb < S::NBV; ++nb) {
-                const int g = (16 * nb) / a.Gv;
+                const int g = (16 * nb) / Gv;
                 if (g != g_loaded) {
                     Ap = *reinterpret_cast<const bf16x8_t*>(PA + g * S::PA_MAT + col * S::PA_ROW +
                                                             32 * kt + 8 * gq);
@@ -685,14 +708,13 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // branch and the compiler waits only for the chunk about to be used).
     constexpr int PF = S::PF;
     ChunkRegs<S> buf[PF];
-    const int n_mine = max(0, c_end - c_begin);
     const int n_full = n_mine / PF * PF;
     const ChunkSrc<S> src = chunk_src<S>(a, bh * a.Cmax, lane, NG);
     bool any_cur = false;
     if (n_mine > 0) {
 #pragma unroll
         for (int k = 0; k < PF; ++k)
-            load_chunk<S>(buf[k], src, min(c_begin + k, c_end - 1));
+            load_chunk<S>(buf[k], src, chunk_of(k));
     }
 
     // ---- this wave's slice of the fp32 residual window ------------------------
@@ -722,19 +744,29 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             // scores
             int slot = a.res_start + t0 + min(tk, n - 1);
             slot = slot >= a.Rcap ? slot - a.Rcap : slot;
+            // lane (tk, qq) takes float4s qq, qq+4, ... of token tk's row
             const float4* krow = reinterpret_cast<const float4*>(
-                a.k_res + (bh * a.Rcap + slot) * D) + qq * KQ;
+                a.k_res + (bh * a.Rcap + slot) * D) + qq;
             float4 kv[KQ];
 #pragma unroll
-            for (int j = 0; j < KQ; ++j) kv[j] = krow[j];
+            for (int j = 0; j < KQ; ++j) kv[j] = krow[4 * j];
+            // the pass's value rows are independent of the scores: load them
+            // now so that a pass waits for HBM once
+            float4 vv[kResPass / TS];
+#pragma unroll
+            for (int j = 0; j < kResPass / TS; ++j) {
+                int vs = a.res_start + t0 + min(ts + TS * j, n - 1);
+                vs = vs >= a.Rcap ? vs - a.Rcap : vs;
+                vv[j] = reinterpret_cast<const float4*>(a.v_res + (bh * a.Rcap + vs) * D)[c4];
+            }
             float sres[HG];
 #pragma unroll
             for (int h = 0; h < HG; ++h) {
-                const float4* qh = reinterpret_cast<const float4*>(qres + h * D) + qq * KQ;
+                const float4* qh = reinterpret_cast<const float4*>(qres + h * D) + qq;
                 float acc = 0.f;
 #pragma unroll
                 for (int j = 0; j < KQ; ++j) {
-                    const float4 qv4 = qh[j];
+                    const float4 qv4 = qh[4 * j];
                     acc = fmaf(qv4.x, kv[j].x, acc);
                     acc = fmaf(qv4.y, kv[j].y, acc);
                     acc = fmaf(qv4.z, kv[j].z, acc);
@@ -759,13 +791,6 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             }
             wave_sync();
             // weighted sum of the values
-            float4 vv[kResPass / TS];
-#pragma unroll
-            for (int j = 0; j < kResPass / TS; ++j) {
-                int vs = a.res_start + t0 + min(ts + TS * j, n - 1);
-                vs = vs >= a.Rcap ? vs - a.Rcap : vs;
-                vv[j] = reinterpret_cast<const float4*>(a.v_res + (bh * a.Rcap + vs) * D)[c4];
-            }
 #pragma unroll
             for (int j = 0; j < kResPass / TS; ++j) {
                 const int tt = ts + TS * j;
@@ -819,12 +844,12 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         wave_sync();
         any_cur = kside(buf[0], Int<0>{});
     }
-    // Step i (of the wave's chunks, counted from c_begin) uses double-buffer
+    // Step i (of the wave's chunks, counted from 0) uses double-buffer
     // slot i & 1; PF is even, so within the unrolled ring the slot of step k
     // is k & 1, a compile-time constant.
     auto step = [&](const ChunkRegs<S>& cur, const ChunkRegs<S>& nxt, int i, auto slot_c) {
         constexpr int slot = decltype(slot_c)::value, nslot = slot ^ 1;
-        const bool has_next = i + 1 < c_end;
+        const bool has_next = i + 1 < n_mine;
         if (has_next) stage_meta<S>(nxt, MT + nslot * meta_stride, lane, NG, meta_floats);
         wave_sync();
         if (has_next) wprep(Int<nslot>{});
@@ -834,16 +859,16 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         if (has_next) any_cur = kside(nxt, Int<nslot>{});
     };
     static_assert(PF % 2 == 0, "the slot parity of a ring step must be static");
-    for (int c0 = c_begin; c0 < c_begin + n_full; c0 += PF) {
+    for (int c0 = 0; c0 < n_full; c0 += PF) {
         static_for<0, PF>([&](auto kc) {
             constexpr int k = decltype(kc)::value;
             step(buf[k], buf[(k + 1) % PF], c0 + k, Int<k & 1>{});
-            load_chunk<S>(buf[k], src, min(c0 + k + PF, c_end - 1));
+            load_chunk<S>(buf[k], src, chunk_of(c0 + k + PF));
         });
     }
     static_for<0, PF>([&](auto kc) {
         constexpr int k = decltype(kc)::value;
-        if (k < n_mine - n_full) step(buf[k], buf[(k + 1) % PF], c_begin + n_full + k, Int<k & 1>{});
+        if (k < n_mine - n_full) step(buf[k], buf[(k + 1) % PF], n_full + k, Int<k & 1>{});
     });
 
     // ---- wave state -> merge slot --------------------------------------------
@@ -867,7 +892,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         for (int nb = 0; nb < S::NBV; ++nb) {
             float v = 0.f;
             if (h < HG) {
-                const int g = (16 * nb + col) / a.Gv;
+                const int g = (16 * nb + col) / Gv;
                 const float* pv = VB + (h * NG + g) * NSEG;
 #pragma unroll
                 for (int sg = 0; sg < NSEG; ++sg) v += pv[sg];
@@ -901,13 +926,13 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
 template <int HG, int D>
 constexpr int attn_waves_per_eu() { return (D <= 64 || (D <= 128 && HG <= 4)) ? 2 : 1; }
 
-template <int HG, int D, int G>
+template <int HG, int D, int G, int NGC>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<HG, D>())))
 void attn_mfma_kernel(AttnLaunch a) {
     extern __shared__ __align__(16) unsigned char smem[];
     using S = Shape<HG, D, G>;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    wave_path<S>(smem, a, split, kvh, b);
+    wave_path<S, NGC>(smem, a, split, kvh, b);
 }
 
 int max_lds_per_block() {
@@ -918,7 +943,7 @@ int max_lds_per_block() {
     return v;
 }
 
-template <int HG, int D, int G>
+template <int HG, int D, int G, int NGC>
 int launch_shape(const AttnLaunch& a, hipStream_t st) {
     using S = Shape<HG, D, G>;
     static const int lds_limit = max_lds_per_block();
@@ -929,13 +954,23 @@ int launch_shape(const AttnLaunch& a, hipStream_t st) {
                          "group_size_v=%d needs %d bytes of LDS per workgroup; the device "
                          "allows %d", HG, D, G, a.Gv, lds, lds_limit);
     const dim3 grid(a.n_splits, a.Hkv, a.B);
-    attn_mfma_kernel<HG, D, G><<<grid, kBlock, lds, st>>>(a);
+    attn_mfma_kernel<HG, D, G, NGC><<<grid, kBlock, lds, st>>>(a);
     return check_launch("packed_decode_attention (mfma)");
+}
+
+// Value groups of 32 channels, one group per token, or (head_dim 128/256
+// with 64- or 128-channel groups) the runtime count.
+template <int HG, int D, int G>
+int launch_ng(const AttnLaunch& a, hipStream_t st) {
+    if (a.Gv == 32) return launch_shape<HG, D, G, D / 32>(a, st);
+    if (a.Gv == D) return launch_shape<HG, D, G, 1>(a, st);
+    if constexpr (D > 64) return launch_shape<HG, D, G, 0>(a, st);
+    return set_error(kErrUnsupported, "group_size_v=%d with head_dim=%d", a.Gv, D);
 }
 
 template <int HG, int D>
 int launch_g(const AttnLaunch& a, hipStream_t st) {
-    return a.G == 32 ? launch_shape<HG, D, 32>(a, st) : launch_shape<HG, D, 64>(a, st);
+    return a.G == 32 ? launch_ng<HG, D, 32>(a, st) : launch_ng<HG, D, 64>(a, st);
 }
 
 template <int HG>
@@ -948,15 +983,4 @@ int launch_d(const AttnLaunch& a, hipStream_t st) {
 }
 
 }  // namespace
-
-int launch_attention_mfma(const AttnLaunch& a, hipStream_t st) {
-    switch (a.Hq / a.Hkv) {
-        case 1: return launch_d<1>(a, st);
-        case 2: return launch_d<2>(a, st);
-        case 4: return launch_d<4>(a, st);
-        default: return launch_d<8>(a, st);
-    }
-}
-
-
 }  // namespace kivi
