@@ -1,0 +1,346 @@
+"""KiviPackedCache: the KIVI 2-bit cache as a ``transformers.Cache`` whose
+decode attention reads the packed store directly.
+
+The reference hands the model a fresh fp32 ``DynamicCache`` built from the
+dequantised history plus the fp32 residual window on every decode step
+(src/kivi_sycl/cache/manager.py:251-290, generation/generate.py:75-77), and the
+model's attention then reads 1,024 B per token and kv head (D=128) instead of
+the 128 B the 2-bit store holds.  Here the cache plugs into the model's own
+``past_key_values.update()`` call and its attention dispatch:
+
+* ``update()`` appends the step's new K/V to the layer's HBM residual ring
+  (:class:`~intel_kivi_hybrid_amd.store.PackedKVStore`) and returns them
+  tagged with the layer;
+* the attention function registered as ``"kivi_packed"`` runs the fused HIP
+  decode kernel over [packed history ; residual ring] of that layer, with no
+  dequantised copy of anything, and then performs the flushes the step owes
+  (residual >= R), i.e. in the reference's order: attention of step t sees
+  the new token in fp32, and add_tokens() flushes afterwards
+  (manager.py:242-249);
+* a prompt (more than one token on an empty layer) attends over its own
+  unquantised K/V with PyTorch SDPA, exactly like the reference's prefill
+  forward with a plain cache (generate.py:56-60), and is then quantised into
+  the store with the same flush rule.
+
+The served-cache path (:class:`KiviCache` with ``get_full_cache()``) stays the
+drop-in for the reference's control flow; this class is the fast path for
+models that use HF's attention interface (GPT-2, Llama, Mistral, ...).
+"""
+
+from __future__ import annotations
+
+import contextlib
+from typing import List, Optional
+
+import torch
+from transformers.cache_utils import Cache, CacheLayerMixin
+from transformers.integrations.sdpa_attention import sdpa_attention_forward
+from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
+from transformers.modeling_utils import AttentionInterface
+
+from ..config.model_config import detect_model_config
+from ..extension.loader import kivi_native  # noqa: F401  (fails loudly without the HIP library)
+from ..store import PackedKVStore
+from .manager import _resolve_device
+
+__all__ = ["KIVI_ATTENTION", "KiviPackedCache", "kivi_packed_attention_forward",
+           "packed_attention", "register_packed_attention"]
+
+#: Name of the attention implementation that consumes a KiviPackedCache.
+KIVI_ATTENTION = "kivi_packed"
+
+# The store class the layers allocate (a seam for host-only tests of the
+# cache's control flow).
+_STORE_CLASS = PackedKVStore
+
+
+def store_bytes(B: int, H: int, D: int, G: int, Gv: int, n_chunks: int, res_len: int) -> dict:
+    """Byte accounting of one layer's store contents (manager.py:350-356
+    generalised to separate key and value group sizes): 2-bit codes, fp32
+    scales and zeros (keys per channel and chunk, values per token and Gv
+    channels), and the fp32 residual window."""
+    tokens = n_chunks * G
+    codes = 2 * B * H * tokens * D // 4
+    k_meta = B * H * n_chunks * D * 4 * 2
+    v_meta = B * H * tokens * (D // Gv) * 4 * 2
+    residual = 2 * B * H * res_len * D * 4
+    return {"codes": codes, "k_scales_zeros": k_meta, "v_scales_zeros": v_meta,
+            "residual": residual, "quantized": codes + k_meta + v_meta}
+
+
+class KiviPackedLayer(CacheLayerMixin):
+    """One layer of a :class:`KiviPackedCache`: an HBM store plus the count of
+    flushes it has done."""
+
+    is_compileable = False
+    is_sliding = False
+    supports_early_init = False
+
+    def __init__(self, owner: "KiviPackedCache", index: int):
+        super().__init__()
+        self.owner = owner
+        self.index = index
+        self.store: Optional[PackedKVStore] = None
+        self.flushes = 0
+        # True while the layer's latest update was a prompt (attended with SDPA).
+        self._prompt = False
+        # Set by a single-token update, cleared by the packed attention: an
+        # update that finds it still set means the model attended with some
+        # other implementation and saw only the new token.
+        self._awaiting_attention = False
+
+    # ------------------------------------------------------------ state
+    @property
+    def batch_size(self) -> int:
+        if not self.is_initialized:
+            raise AttributeError("batch_size")
+        return self.store.B
+
+    def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        o = self.owner
+        B, H, _, D = key_states.shape
+        if D != o.head_dim:
+            raise ValueError(f"KiviPackedCache was built for head_dim {o.head_dim} but layer "
+                             f"{self.index} has key head_dim {D}")
+        if o.num_kv_heads is not None and H != o.num_kv_heads:
+            raise ValueError(f"KiviPackedCache was built for {o.num_kv_heads} kv heads but "
+                             f"layer {self.index} has {H}")
+        st = self.store
+        if st is None or st.B != B or st.H != H:
+            self.store = _STORE_CLASS(B, H, D, o.G, o.R, o.device, group_size_v=o.Gv,
+                                      chunk_capacity=o.chunk_capacity)
+        else:
+            st.reset()
+        self.dtype, self.device = key_states.dtype, key_states.device
+        self.flushes = 0
+        self._awaiting_attention = False
+        self.is_initialized = True
+
+    def get_seq_length(self) -> int:
+        if not self.is_initialized:
+            return 0
+        return self.store.quantized_tokens + self.store.res_len
+
+    def get_mask_sizes(self, query_length: int) -> tuple:
+        return self.get_seq_length() + query_length, 0
+
+    def get_max_length(self) -> int:
+        return -1
+
+    def reset(self) -> None:
+        if self.store is not None:
+            self.store.reset()
+        self.flushes = 0
+        self._awaiting_attention = False
+        self.is_initialized = False
+
+    def settle(self) -> None:
+        """Flush the G oldest residual tokens while the window holds R or more
+        (manager.py:242-249)."""
+        st = self.store
+        while st.res_len >= self.owner.R:
+            st.flush()
+            self.flushes += 1
+
+    # ------------------------------------------------------------ update
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs):
+        """Append ``[B, Hkv, n, D]`` new K/V and return them tagged with this
+        layer for the ``"kivi_packed"`` attention."""
+        if self._awaiting_attention:
+            raise RuntimeError(
+                f"KiviPackedCache layer {self.index}: the previous decode step did not run the "
+                f"'{KIVI_ATTENTION}' attention, so it attended over the new token only.  Run the "
+                f"model with attn_implementation='{KIVI_ATTENTION}' (see packed_attention()).")
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        st = self.store
+        B, H = key_states.shape[0], key_states.shape[1]
+        if B != st.B or H != st.H:
+            raise ValueError(f"KiviPackedCache layer {self.index} holds batch {st.B} x {st.H} kv "
+                             f"heads but got {B} x {H}; call reset() before a new batch")
+        self.settle()
+        n = key_states.shape[-2]
+        k = key_states.to(self.owner.device, torch.float32)
+        v = value_states.to(self.owner.device, torch.float32)
+        if self.get_seq_length() == 0:
+            # Prompt: attention reads these tensors, the store takes them.
+            self.flushes += st.extend(k, v, flush_at=self.owner.R)
+            self._prompt = True
+        elif n == 1:
+            st.append(k, v)          # room: settle() left res_len < R
+            self._prompt = False
+            self._awaiting_attention = True
+        else:
+            raise NotImplementedError(
+                f"KiviPackedCache: a {n}-token forward pass on a non-empty cache (chunked "
+                f"prefill, assisted decoding) is not supported; decode one token per step")
+        kt, vt = key_states.view_as(key_states), value_states.view_as(value_states)
+        kt._kivi_layer = self
+        vt._kivi_layer = self
+        return kt, vt
+
+    # --------------------------------------------------------- attention
+    def attend(self, query: torch.Tensor, scaling: Optional[float]) -> torch.Tensor:
+        """Decode attention of ``query [B, Hq, 1, D]`` over this layer's store;
+        returns ``[B, 1, Hq, D]`` in the query's dtype and device."""
+        st = self.store
+        q = query[:, :, 0, :].to(st.device, torch.float32).contiguous()
+        o = st.attention(q, softmax_scale=scaling)
+        self._awaiting_attention = False
+        self.settle()
+        return o.unsqueeze(1).to(query.device, query.dtype)
+
+    # ------------------------------------------------ unsupported ops
+    def crop(self, tokens_to_remove: int) -> None:
+        raise NotImplementedError("KiviPackedCache cannot drop tokens once they are stored")
+
+    def reorder_cache(self, beam_idx: torch.LongTensor) -> None:
+        if self.get_seq_length() > 0:
+            self.store.select_batch(beam_idx.to(self.store.device))
+
+    def batch_select_indices(self, indices: torch.Tensor) -> None:
+        self.reorder_cache(indices)
+
+    def batch_repeat_interleave(self, repeats: int) -> None:
+        if self.get_seq_length() > 0:
+            idx = torch.arange(self.store.B, device=self.store.device).repeat_interleave(repeats)
+            self.store.select_batch(idx)
+
+    def offload(self):
+        raise NotImplementedError("KiviPackedCache keeps its store in GPU memory")
+
+    def prefetch(self):
+        raise NotImplementedError("KiviPackedCache keeps its store in GPU memory")
+
+
+class KiviPackedCache(Cache):
+    """KIVI 2-bit KV cache for HF models, attended in place.
+
+    Args mirror :class:`KiviCache` (manager.py:52-133): ``num_layers``,
+    ``head_dim``, ``num_kv_heads``, ``device`` (HIP device of the store),
+    ``group_size`` (G, key group along tokens and chunk length),
+    ``residual_length`` (R, fp32 window), plus ``value_group_size`` (value
+    group along channels, default G) and ``chunk_capacity`` (chunks to
+    preallocate per layer; the store grows by doubling beyond it).
+
+    Use it with the model's attention set to ``"kivi_packed"``::
+
+        cache = KiviPackedCache.from_model(model)
+        with packed_attention(model):
+            out = model.generate(input_ids, past_key_values=cache, do_sample=False)
+    """
+
+    def __init__(self, num_layers: int, head_dim: int, num_kv_heads: Optional[int] = None,
+                 device: str = "cuda", group_size: int = 32, residual_length: int = 128,
+                 value_group_size: Optional[int] = None, chunk_capacity: int = 0):
+        assert group_size >= 4 and group_size % 4 == 0, \
+            f"group_size ({group_size}) must be >= 4 and divisible by 4"
+        gv = group_size if value_group_size is None else value_group_size
+        assert gv >= 4 and gv % 4 == 0 and head_dim % gv == 0, \
+            f"head_dim ({head_dim}) must be divisible by value group size ({gv})"
+        assert group_size <= residual_length, (
+            f"group_size ({group_size}) must not exceed residual_length ({residual_length})")
+        register_packed_attention()
+        self.device = _resolve_device(device)
+        self.head_dim = head_dim
+        self.num_layers = num_layers
+        self.num_kv_heads = num_kv_heads
+        self.G, self.Gv, self.R = group_size, gv, residual_length
+        self.chunk_capacity = max(int(chunk_capacity), 1)
+        super().__init__(layers=[KiviPackedLayer(self, i) for i in range(num_layers)])
+
+    @classmethod
+    def from_model(cls, model, device: str = "cuda", group_size: int = 32,
+                   residual_length: int = 128, value_group_size: Optional[int] = None,
+                   chunk_capacity: int = 0) -> "KiviPackedCache":
+        """A cache sized from a HuggingFace model's config (manager.py:135-156)."""
+        cfg = detect_model_config(model)
+        return cls(cfg["num_layers"], cfg["head_dim"], cfg["num_kv_heads"], device=device,
+                   group_size=group_size, residual_length=residual_length,
+                   value_group_size=value_group_size, chunk_capacity=chunk_capacity)
+
+    # ----------------------------------------------------------- access
+    def store(self, layer: int) -> Optional[PackedKVStore]:
+        lay = self.layers[layer]
+        return lay.store if lay.is_initialized else None
+
+    @property
+    def total_flushes(self) -> int:
+        return sum(lay.flushes for lay in self.layers)
+
+    def get_stats(self, layer: int = 0) -> dict:
+        """Token and byte accounting of one layer's store, with the keys of
+        KiviCache.get_stats (manager.py:384-419); the byte counts are those
+        of the tensors actually held, itemised under ``bytes``."""
+        st = self.store(layer)
+        if st is None:
+            return {"total_tokens": 0, "quantized_tokens": 0, "residual_tokens": 0,
+                    "kivi_bytes": 0, "fp32_bytes": 0, "compression": 0}
+        b = store_bytes(st.B, st.H, st.D, st.G, st.Gv, st.n_chunks, st.res_len)
+        total = st.quantized_tokens + st.res_len
+        kivi = b["quantized"] + b["residual"]
+        fp32 = 2 * st.B * st.H * total * st.D * 4
+        return {"total_tokens": total, "quantized_tokens": st.quantized_tokens,
+                "residual_tokens": st.res_len, "kivi_bytes": kivi, "fp32_bytes": fp32,
+                "compression": fp32 / kivi if kivi > 0 else 0, "bytes": b,
+                "allocated_bytes": st.allocated_bytes()}
+
+    def __repr__(self):
+        return (f"KiviPackedCache(layers={self.num_layers}, head_dim={self.head_dim}, "
+                f"G={self.G}, Gv={self.Gv}, R={self.R}, device='{self.device}')")
+
+
+def kivi_packed_attention_forward(module, query, key, value, attention_mask, scaling=None,
+                                  dropout=0.0, **kwargs):
+    """HF attention function for a :class:`KiviPackedCache`.
+
+    One-token (decode) steps run the fused packed-KV kernel over the layer's
+    store; prompt passes go to PyTorch SDPA over the prompt's own K/V.
+    Returns ``(attn_output [B, q_len, Hq, D], None)`` as HF's attention
+    functions do (models/gpt2/modeling_gpt2.py:54-73 in transformers)."""
+    layer = getattr(key, "_kivi_layer", None)
+    if layer is None:
+        raise RuntimeError(f"the '{KIVI_ATTENTION}' attention needs past_key_values to be a "
+                           f"KiviPackedCache and use_cache=True")
+    if layer._prompt or query.shape[2] > 1:
+        return sdpa_attention_forward(module, query, key, value, attention_mask,
+                                      dropout=dropout, scaling=scaling, **kwargs)
+    if dropout:
+        raise ValueError(f"'{KIVI_ATTENTION}' attention is inference-only (dropout={dropout})")
+    if attention_mask is not None:
+        raise NotImplementedError(
+            f"'{KIVI_ATTENTION}' decode attention takes no attention mask (padded batches are "
+            f"not supported); every sequence attends over its whole cache")
+    for name in ("sliding_window", "softcap", "s_aux"):
+        if kwargs.get(name) is not None:
+            raise NotImplementedError(f"'{KIVI_ATTENTION}' attention does not support {name}")
+    return layer.attend(query, scaling), None
+
+
+_registered = False
+
+
+def register_packed_attention() -> None:
+    """Register ``"kivi_packed"`` with transformers' attention and mask
+    interfaces (the mask is SDPA's, used by prompt passes)."""
+    global _registered
+    if not _registered:
+        AttentionInterface.register(KIVI_ATTENTION, kivi_packed_attention_forward)
+        AttentionMaskInterface.register(KIVI_ATTENTION, sdpa_mask)
+        _registered = True
+
+
+@contextlib.contextmanager
+def packed_attention(model):
+    """Run ``model`` with the ``"kivi_packed"`` attention inside the block and
+    restore its previous implementation afterwards."""
+    register_packed_attention()
+    prev = model.config._attn_implementation
+    model.set_attn_implementation(KIVI_ATTENTION)
+    if model.config._attn_implementation != KIVI_ATTENTION:
+        raise RuntimeError(f"{type(model).__name__} does not accept the '{KIVI_ATTENTION}' "
+                           f"attention implementation")
+    try:
+        yield model
+    finally:
+        model.set_attn_implementation(prev)

@@ -200,6 +200,23 @@ class PackedKVStore:
     def reset(self) -> None:
         self.res_start = self.res_len = self.n_chunks = 0
 
+    _TENSORS = ("k_res", "v_res", "k_codes", "k_scale", "k_zero", "v_codes", "v_scale",
+                "v_zero", "k_hist", "v_hist")
+
+    def allocated_bytes(self) -> int:
+        """Device bytes the store's tensors hold (capacity, not contents)."""
+        return sum(t.numel() * t.element_size()
+                   for t in (getattr(self, n) for n in self._TENSORS) if t is not None)
+
+    def select_batch(self, index: torch.Tensor) -> None:
+        """Keep (and reorder or repeat) batch rows ``index`` of every tensor,
+        e.g. to follow a beam-search reorder."""
+        for name in self._TENSORS:
+            t = getattr(self, name)
+            if t is not None:
+                setattr(self, name, t.index_select(0, index))
+        self.B = int(index.numel())
+
     # ---------------------------------------------------------- inspection
     def _codes(self, which: str, chunk: int) -> torch.Tensor:
         """One chunk's 2-bit codes, one byte per element, as [B, Hkv, G, D]."""

@@ -1,0 +1,182 @@
+"""GPU parity of KiviPackedCache + the "kivi_packed" attention (the model's
+attention reads the 2-bit HBM store through the fused HIP kernel).
+
+Greedy decoding must pick the tokens the reference's generate() picks with
+its served fp32 cache (src/kivi_sycl/generation/generate.py:13-89,
+cache/manager.py:162-374), here restated by the CPU oracle, and the tokens of
+this package's served-cache generate()."""
+
+import importlib
+
+import pytest
+import torch
+
+from oracle.kivi_cache import KiviCacheOracle
+
+pytestmark = pytest.mark.gpu
+
+gen_mod = importlib.import_module("intel_kivi_hybrid_amd.generation.generate")
+pc = importlib.import_module("intel_kivi_hybrid_amd.cache.packed_cache")
+
+
+class _Tok:
+    eos_token_id = None
+
+    def __init__(self, vocab):
+        self.vocab = vocab
+
+    def __call__(self, prompt, return_tensors="pt"):
+        ids = torch.tensor([[(ord(c) * 131 + 7 * i) % self.vocab for i, c in enumerate(prompt)]])
+        return type("Enc", (), {"input_ids": ids})()
+
+    def decode(self, ids, skip_special_tokens=True):
+        return " ".join(str(int(t)) for t in ids)
+
+
+class _OracleShim(KiviCacheOracle):
+    @classmethod
+    def from_model(cls, model, device="cuda", group_size=32, residual_length=128):
+        from intel_kivi_hybrid_amd.config import detect_model_config
+        cfg = detect_model_config(model)
+        return cls(cfg["num_layers"], cfg["head_dim"], cfg["num_kv_heads"], group_size,
+                   residual_length)
+
+
+def _match(a, b):
+    n = sum(x == y for x, y in zip(a, b))
+    return n, max(len(a), len(b))
+
+
+@pytest.mark.parametrize("R,max_new", [(32, 200), (64, 200)])
+def test_packed_generate_matches_reference_flow(hip_device, monkeypatch, R, max_new):
+    """12-layer GPT-2 shape (12 heads, D=64), model on the CPU in both arms as
+    in the reference; the packed arm's decode attention runs on the GPU."""
+    from transformers import GPT2Config, GPT2LMHeadModel
+    torch.manual_seed(0)
+    model = GPT2LMHeadModel(GPT2Config(n_layer=12, n_head=12, n_embd=768)).eval()
+    tok = _Tok(model.config.vocab_size)
+    prompt = "The quick brown fox jumps over the lazy dog and"
+    print(f"[packed-greedy] R={R} max_new={max_new}", flush=True)
+    ours = gen_mod.generate_packed(model, tok, prompt, max_new_tokens=max_new, group_size=32,
+                                   residual_length=R, device="cuda:0")
+    monkeypatch.setattr(gen_mod, "KiviCache", _OracleShim)
+    ref = gen_mod.generate(model, tok, prompt, max_new_tokens=max_new, group_size=32,
+                           residual_length=R, device="cuda:0")
+    n, tot = _match(ours.split(), ref.split())
+    print(f"[packed-greedy] token match {n}/{tot}", flush=True)
+    assert ours.split() == ref.split()
+
+
+def test_packed_generate_model_on_gpu(hip_device):
+    """Model on the GPU: generate_packed picks the tokens of the served-cache
+    generate() (the same model forward, attention over the store vs SDPA
+    over the served fp32 history)."""
+    from transformers import GPT2Config, GPT2LMHeadModel
+    torch.manual_seed(1)
+    model = GPT2LMHeadModel(GPT2Config(n_layer=6, n_head=12, n_embd=768)).eval().to(hip_device)
+    tok = _Tok(model.config.vocab_size)
+    prompt = "hello there, packed cache"
+    a = gen_mod.generate_packed(model, tok, prompt, max_new_tokens=150, group_size=32,
+                                residual_length=64, device="cuda:0").split()
+    b = gen_mod.generate(model, tok, prompt, max_new_tokens=150, group_size=32,
+                         residual_length=64, device="cuda:0").split()
+    n, tot = _match(a, b)
+    print(f"[packed-gpu] token match {n}/{tot}", flush=True)
+    assert a == b
+
+
+def test_hf_generate_with_packed_cache(hip_device):
+    """transformers' generate() with a KiviPackedCache equals generate_packed."""
+    from transformers import GPT2Config, GPT2LMHeadModel
+    torch.manual_seed(2)
+    model = GPT2LMHeadModel(GPT2Config(n_layer=4, n_head=4, n_embd=256)).eval().to(hip_device)
+    tok = _Tok(model.config.vocab_size)
+    prompt = "transformers drives the cache"
+    ours = gen_mod.generate_packed(model, tok, prompt, max_new_tokens=100, group_size=32,
+                                   residual_length=32, device="cuda:0").split()
+    ids = tok(prompt).input_ids.to(hip_device)
+    cache = pc.KiviPackedCache.from_model(model, device="cuda:0", group_size=32,
+                                          residual_length=32)
+    with pc.packed_attention(model):
+        hf = model.generate(ids, past_key_values=cache, max_new_tokens=100, do_sample=False,
+                            attention_mask=torch.ones_like(ids), pad_token_id=0)
+    assert tok.decode(hf[0].cpu()).split() == ours
+    st = cache.get_stats(0)
+    assert st["total_tokens"] == ids.shape[1] + 99
+    assert cache.total_flushes == 4 * ((st["total_tokens"] - 32) // 32 + 1)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gqa_llama_packed_vs_served(hip_device, dtype):
+    """Grouped-query Llama (8 query heads over 2 kv heads, D=128), model on
+    the GPU: packed vs served cache pick the same tokens in fp32.  In bf16
+    (which the reference's fp32 served cache cannot feed) the packed path
+    runs end to end; its agreement with the fp32 tokens is printed."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+    torch.manual_seed(3)
+    cfg = LlamaConfig(vocab_size=1024, hidden_size=1024, intermediate_size=2048,
+                      num_hidden_layers=4, num_attention_heads=8, num_key_value_heads=2,
+                      max_position_embeddings=1024)
+    model = LlamaForCausalLM(cfg).eval().to(hip_device)
+    tok = _Tok(cfg.vocab_size)
+    prompt = "grouped query attention over a packed cache"
+    a = gen_mod.generate_packed(model, tok, prompt, max_new_tokens=120, group_size=32,
+                                residual_length=64, device="cuda:0").split()
+    if dtype == torch.float32:
+        b = gen_mod.generate(model, tok, prompt, max_new_tokens=120, group_size=32,
+                             residual_length=64, device="cuda:0").split()
+        n, tot = _match(a, b)
+        print(f"[packed-gqa] token match {n}/{tot}", flush=True)
+        assert a == b
+    else:
+        model = model.to(dtype)
+        c = gen_mod.generate_packed(model, tok, prompt, max_new_tokens=120, group_size=32,
+                                    residual_length=64, device="cuda:0").split()
+        n, tot = _match(a, c)
+        print(f"[packed-gqa] bf16 vs fp32 token match {n}/{tot}", flush=True)
+        assert len(c) == len(a)
+
+
+def test_attention_output_matches_oracle(hip_device):
+    """One decode step of the packed attention function against the float64
+    oracle over the same store contents (1e-3 relative)."""
+    from oracle.attention import decode_attention
+    B, Hq, Hkv, D, G, R = 3, 8, 2, 128, 32, 64
+    cache = pc.KiviPackedCache(1, D, Hkv, device="cuda:0", group_size=G, residual_length=R)
+    g = torch.Generator().manual_seed(9)
+    k = torch.randn(B, Hkv, 150, D, generator=g)
+    v = torch.randn(B, Hkv, 150, D, generator=g)
+    cache.update(k.cuda(), v.cuda(), 0)                      # prompt: 150 tokens
+    k1, v1 = torch.randn(B, Hkv, 1, D, generator=g), torch.randn(B, Hkv, 1, D, generator=g)
+    kt, _ = cache.update(k1.cuda(), v1.cuda(), 0)
+    st = cache.store(0)
+    n = st.n_chunks
+    # dequantised history in token order, from the store's own codes
+    kh, vh = [], []
+    for c in range(n):
+        kc = st.unpermuted_k_codes(c).cpu().numpy()                  # [B,H,G,D/4] token-major
+        ks, kz = st.k_scale[:, :, c].cpu().numpy(), st.k_zero[:, :, c].cpu().numpy()
+        codes = torch.from_numpy(kc)
+        kd = torch.stack([(codes.to(torch.int32) >> (2 * j)) & 3 for j in range(4)], -1)
+        kd = kd.reshape(B, Hkv, G, D).float()
+        kh.append(kd * torch.from_numpy(ks)[:, :, None, :] + torch.from_numpy(kz)[:, :, None, :])
+        vc = torch.from_numpy(st.unpermuted_v_codes(c).cpu().numpy())   # [B,H,D,G/4]
+        vd = torch.stack([(vc.to(torch.int32) >> (2 * j)) & 3 for j in range(4)], -1)
+        vd = vd.reshape(B, Hkv, D, G).transpose(2, 3).float()
+        vs = st.chunk_v_scale(c).cpu()                                 # [B,H,G,D/Gv]
+        vz = st.chunk_v_zero(c).cpu()
+        vh.append(vd * vs.repeat_interleave(st.Gv, -1) + vz.repeat_interleave(st.Gv, -1))
+    kr, vr = st.residual()
+    q = torch.randn(B, Hq, 1, D, generator=g)
+
+    class _M(torch.nn.Module):
+        is_causal = True
+    out, w = pc.kivi_packed_attention_forward(_M(), q.cuda(), kt, kt, None, scaling=D ** -0.5)
+    ref = decode_attention(q[:, :, 0].numpy(), torch.cat(kh, 2).numpy(), torch.cat(vh, 2).numpy(),
+                           kr.cpu().numpy(), vr.cpu().numpy())
+    got = out[:, 0].cpu().double().numpy()
+    err = abs(got - ref).max() / abs(ref).max()
+    print(f"[packed-attn] chunks={n} res={kr.shape[2]} rel_err={err:.2e}", flush=True)
+    assert w is None and out.shape == (B, 1, Hq, D)
+    assert err <= 1e-3
+    assert st.res_len == 150 - n * G + 1

@@ -1,0 +1,212 @@
+"""Host checks of KiviPackedCache, the transformers.Cache whose decode attention
+reads the packed store.  The GPU store is replaced by a CPU stand-in built on
+the oracle (tests/cpu_store.py), so these tests exercise the cache's control
+flow -- when tokens are appended, attended and flushed -- against the
+reference's generate()/KiviCache flow (oracle restatement of
+src/kivi_sycl/generation/generate.py:13-89 and cache/manager.py:162-374)."""
+
+import importlib
+
+import pytest
+import torch
+from transformers import GPT2Config, GPT2LMHeadModel, LlamaConfig, LlamaForCausalLM
+from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS
+
+from oracle.kivi_cache import KiviCacheOracle, closed_form_stats
+from tests.cpu_store import CpuPackedStore
+
+pc = importlib.import_module("intel_kivi_hybrid_amd.cache.packed_cache")
+gen_mod = importlib.import_module("intel_kivi_hybrid_amd.generation.generate")
+
+
+class _Tok:
+    eos_token_id = None
+
+    def __init__(self, vocab):
+        self.vocab = vocab
+
+    def __call__(self, prompt, return_tensors="pt"):
+        ids = torch.tensor([[(ord(c) * 131 + 7 * i) % self.vocab for i, c in enumerate(prompt)]])
+        return type("Enc", (), {"input_ids": ids})()
+
+    def decode(self, ids, skip_special_tokens=True):
+        return " ".join(str(int(t)) for t in ids)
+
+
+class _OracleShim(KiviCacheOracle):
+    @classmethod
+    def from_model(cls, model, device="cuda", group_size=32, residual_length=128):
+        from intel_kivi_hybrid_amd.config import detect_model_config
+        cfg = detect_model_config(model)
+        return cls(cfg["num_layers"], cfg["head_dim"], cfg["num_kv_heads"], group_size,
+                   residual_length)
+
+
+@pytest.fixture
+def cpu_store(monkeypatch):
+    monkeypatch.setattr(pc, "_STORE_CLASS", CpuPackedStore)
+    monkeypatch.setattr(pc, "_resolve_device", lambda d: torch.device("cpu"))
+
+
+def _gpt2(layers=4, heads=4, embd=256, seed=0):
+    torch.manual_seed(seed)
+    return GPT2LMHeadModel(GPT2Config(n_layer=layers, n_head=heads, n_embd=embd)).eval()
+
+
+def test_registered_with_transformers():
+    pc.register_packed_attention()
+    assert ALL_ATTENTION_FUNCTIONS[pc.KIVI_ATTENTION] is pc.kivi_packed_attention_forward
+    assert pc.KIVI_ATTENTION in ALL_MASK_ATTENTION_FUNCTIONS
+    model = _gpt2(2, 2, 64)
+    with pc.packed_attention(model):
+        assert model.config._attn_implementation == pc.KIVI_ATTENTION
+    assert model.config._attn_implementation == "sdpa"
+
+
+def test_signature_matches_generate():
+    import inspect
+    a = inspect.signature(gen_mod.generate).parameters
+    b = inspect.signature(gen_mod.generate_packed).parameters
+    assert list(a) == list(b)
+    assert all(a[n].default == b[n].default for n in a)
+
+
+@pytest.mark.parametrize("R,prompt_len,max_new", [(32, 9, 90), (64, 70, 80), (32, 32, 40)])
+def test_generate_packed_follows_reference_flow(cpu_store, monkeypatch, R, prompt_len, max_new):
+    """Token for token, generate_packed (model-driven cache updates, attention
+    from the store, flush after the step's attention) picks what the
+    reference's generate() picks with its served fp32 cache."""
+    model = _gpt2()
+    tok = _Tok(model.config.vocab_size)
+    prompt = ("The quick brown fox jumps over the lazy dog " * 4)[:prompt_len]
+    ours = gen_mod.generate_packed(model, tok, prompt, max_new_tokens=max_new, group_size=32,
+                                   residual_length=R, device="cuda")
+    monkeypatch.setattr(gen_mod, "KiviCache", _OracleShim)
+    ref = gen_mod.generate(model, tok, prompt, max_new_tokens=max_new, group_size=32,
+                           residual_length=R, device="cuda")
+    assert ours.split() == ref.split()
+
+
+def test_cache_state_matches_reference_after_each_step(cpu_store):
+    """After every forward pass the packed cache holds what the reference's
+    KiviCache holds after add_tokens(): the same quantised/residual split in
+    every layer, and in layer 0 (whose K/V depend only on the tokens) the
+    same dequantised history and residual, bit for bit.  Deeper layers see
+    K/V computed from attention outputs, which differ in the last bits
+    between the float64 oracle attention and the reference flow's fp32 SDPA."""
+    model = _gpt2(3, 4, 128, seed=3)
+    G, R = 32, 64
+    ours = pc.KiviPackedCache.from_model(model, group_size=G, residual_length=R)
+    ref = _OracleShim.from_model(model, group_size=G, residual_length=R)
+    ids = torch.randint(0, model.config.vocab_size, (2, 75), generator=torch.Generator().manual_seed(5))
+    with torch.no_grad(), pc.packed_attention(model):
+        out = model(ids, past_key_values=ours, use_cache=True)
+    with torch.no_grad():
+        ref_out = model(ids, use_cache=True)
+    ref.add_tokens(ref_out.past_key_values)
+    nxt = out.logits[:, -1:].argmax(-1)
+    for step in range(70):
+        for i in range(3):
+            st = ours.store(i)
+            k, v = list(ref.get_full_cache().layers)[i].keys, list(ref.get_full_cache().layers)[i].values
+            n_hist = st.quantized_tokens
+            assert st.res_len == k.shape[2] - n_hist
+            if i:
+                continue
+            assert torch.equal(st.hist_k, k[:, :, :n_hist]) and torch.equal(st.hist_v, v[:, :, :n_hist])
+            assert torch.equal(st.res_k, k[:, :, n_hist:]) and torch.equal(st.res_v, v[:, :, n_hist:])
+        s_ours, s_ref = ours.get_stats(0), ref.get_stats(0)
+        for key in ("total_tokens", "quantized_tokens", "residual_tokens", "kivi_bytes",
+                    "fp32_bytes"):
+            assert s_ours[key] == s_ref[key], key
+        with torch.no_grad(), pc.packed_attention(model):
+            out = model(nxt, past_key_values=ours, use_cache=True)
+        with torch.no_grad():
+            ref_out = model(nxt, past_key_values=ref.get_full_cache(), use_cache=True)
+        ref.add_tokens(ref_out.past_key_values)
+        nxt = out.logits[:, -1:].argmax(-1)
+    assert ours.total_flushes == ref.total_flushes
+    assert ours.get_seq_length() == 75 + 70
+
+
+def test_stats_closed_form(cpu_store):
+    """get_stats byte counts follow the flush formula (manager.py:350-356)."""
+    B, H, D, G, R = 1, 12, 64, 32, 32
+    cache = pc.KiviPackedCache(12, D, H, group_size=G, residual_length=R)
+    for t in range(200):
+        for i in range(12):
+            k = torch.randn(B, H, 1, D)
+            cache.update(k, k.clone(), i)
+            cache.layers[i]._awaiting_attention = False
+            cache.layers[i].settle()
+    s = cache.get_stats(0)
+    expect = closed_form_stats(B, H, D, G, R, 200)
+    for key in ("total_tokens", "quantized_tokens", "residual_tokens", "kivi_bytes",
+                "fp32_bytes"):
+        assert s[key] == expect[key], key
+    assert s["compression"] == pytest.approx(6.25)
+    assert cache.total_flushes == 12 * 6
+
+
+def test_wrong_attention_is_detected(cpu_store):
+    """A decode step run with another attention implementation sees only the
+    new token; the cache refuses the next update instead of going on."""
+    model = _gpt2(2, 2, 64)
+    cache = pc.KiviPackedCache.from_model(model, group_size=32, residual_length=32)
+    ids = torch.tensor([[1, 2, 3, 4]])
+    with torch.no_grad():
+        with pc.packed_attention(model):
+            model(ids, past_key_values=cache, use_cache=True)
+        model(torch.tensor([[5]]), past_key_values=cache, use_cache=True)   # plain sdpa
+        with pytest.raises(RuntimeError, match="did not run"):
+            model(torch.tensor([[6]]), past_key_values=cache, use_cache=True)
+
+
+def test_unsupported_inputs_raise(cpu_store):
+    model = _gpt2(2, 2, 64)
+    cache = pc.KiviPackedCache.from_model(model, group_size=32, residual_length=32)
+    with torch.no_grad(), pc.packed_attention(model):
+        model(torch.tensor([[1, 2, 3]]), past_key_values=cache, use_cache=True)
+        with pytest.raises(NotImplementedError, match="non-empty cache"):
+            model(torch.tensor([[4, 5]]), past_key_values=cache, use_cache=True)
+    with torch.no_grad(), pc.packed_attention(model):
+        with pytest.raises(RuntimeError, match="KiviPackedCache"):
+            model(torch.tensor([[1, 2, 3]]), use_cache=False)
+    with pytest.raises(ValueError, match="head_dim"):
+        bad = pc.KiviPackedCache(2, 64, 2, group_size=32, residual_length=32)
+        bad.update(torch.zeros(1, 2, 3, 48), torch.zeros(1, 2, 3, 48), 0)
+
+
+def test_hf_generate_uses_the_cache(cpu_store):
+    """transformers' own generate() drives the cache: greedy output equals
+    generate_packed's for the same prompt."""
+    model = _gpt2(3, 4, 128, seed=7)
+    tok = _Tok(model.config.vocab_size)
+    prompt = "hello packed world"
+    ours = gen_mod.generate_packed(model, tok, prompt, max_new_tokens=50, group_size=32,
+                                   residual_length=32)
+    ids = tok(prompt).input_ids
+    cache = pc.KiviPackedCache.from_model(model, group_size=32, residual_length=32)
+    with pc.packed_attention(model):
+        hf = model.generate(ids, past_key_values=cache, max_new_tokens=50, do_sample=False,
+                            attention_mask=torch.ones_like(ids), pad_token_id=0)
+    assert tok.decode(hf[0]).split() == ours.split()
+    assert cache.get_seq_length() == ids.shape[1] + 49
+
+
+def test_gqa_model(cpu_store, monkeypatch):
+    """A grouped-query Llama (8 query heads over 2 kv heads) through the
+    packed cache picks the reference flow's tokens."""
+    torch.manual_seed(11)
+    cfg = LlamaConfig(vocab_size=512, hidden_size=256, intermediate_size=512,
+                      num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2,
+                      max_position_embeddings=512)
+    model = LlamaForCausalLM(cfg).eval()
+    tok = _Tok(cfg.vocab_size)
+    ours = gen_mod.generate_packed(model, tok, "grouped query heads", max_new_tokens=60,
+                                   group_size=32, residual_length=32)
+    monkeypatch.setattr(gen_mod, "KiviCache", _OracleShim)
+    ref = gen_mod.generate(model, tok, "grouped query heads", max_new_tokens=60,
+                           group_size=32, residual_length=32)
+    assert ours.split() == ref.split()
