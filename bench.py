@@ -196,6 +196,48 @@ def quantize_bench(device, iters=10):
     return res
 
 
+def prefill_bench(device, iters=20):
+    """Batched prefill flush: a 4096-token prompt of config 2's shape
+    (B=8, 32 kv heads, D=128) appended to an empty PackedKVStore (R=128,
+    G=32), which quantises its 125 owed chunks per (b, head) in one launch
+    reading the [B,H,T,D] K/V in place; fp32 and bf16 inputs.  Algorithmic
+    bytes: the flushed tokens' K/V read once plus the codes, scales and
+    zeros written; Mtokens/s counts (b, t) positions with all heads of K and
+    V."""
+    import torch
+    from intel_kivi_hybrid_amd.store import PackedKVStore
+    B, H, T, D, G, R = 8, 32, 4096, 128, 32, 128
+    k, v = synth_kv(B, H, T, D, 1237, device)
+    out = {}
+    for name, dt in (("fp32", torch.float32), ("bf16", torch.bfloat16)):
+        kk, vv = k.to(dt), v.to(dt)
+        st = PackedKVStore(B, H, D, G, R, device, chunk_capacity=T // G + 1)
+
+        def one():
+            st.reset()
+            st.extend(kk, vv, flush_at=R)
+
+        settle_clocks(one)
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            one()
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / iters
+        n_tok = st.n_chunks * G
+        nbytes = (2 * B * H * n_tok * D * kk.element_size()       # K/V read
+                  + 2 * B * H * n_tok * D // 4                     # codes
+                  + B * H * st.n_chunks * D * 8                    # key scales + zeros
+                  + B * H * n_tok * (D // G) * 8)                  # value scales + zeros
+        out[name] = {"us": round(us, 1), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "mtokens_s": round(B * n_tok / us, 1), "chunks": st.n_chunks,
+                     "bytes": nbytes}
+        del st, kk, vv
+    return out
+
+
 # --------------------------------------------------------------------------
 # CPU baselines (the reference's CPU path, restated; test infrastructure)
 # --------------------------------------------------------------------------
@@ -275,7 +317,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--attn-iters", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["config4", "attention", "quantize", "copy"], default=None,
+    ap.add_argument("--only", choices=["config4", "attention", "quantize", "prefill", "copy"],
+                    default=None,
                     help="run one workload (for profiling); 'copy' is a plain 512 MiB device "
                          "copy used to calibrate the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
@@ -298,6 +341,11 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"[bench] copy: {n} bytes read and {n} bytes written per launch, 5 launches")
+        return
+
+    if args.only == "prefill":
+        for name, r in prefill_bench(dev).items():
+            log(f"[bench] prefill flush ({name}): {r}")
         return
 
     # ---- config 4: the headline decode loop -------------------------------
@@ -343,6 +391,12 @@ def main():
         f"{qb['mtokens_s']:.1f} Mtokens/s")
     if args.only == "quantize":
         return
+    if args.only is None:
+        pf = prefill_bench(dev)
+        for name, r in pf.items():
+            log(f"[bench] prefill flush ({name} K/V, 4096-token prompt, B=8, 32 heads): "
+                f"{r['us']:.1f} us, {r['gbs']:.0f} GB/s, {r['mtokens_s']:.1f} Mtokens/s")
+        extra["prefill_flush"] = pf
 
     cpu = cpu_q = None
     if not args.no_cpu_baseline:

@@ -122,6 +122,32 @@ int kivi_store_flush(const float* k_res, const float* v_res, uint8_t* k_codes,
                      int32_t res_start, int32_t chunk_capacity, int32_t chunk_index,
                      void* stream);
 
+/* Quantise n_chunks consecutive chunks in one launch (grid: (b, kv-head) x
+ * chunk) from the run of tokens formed by the residual window (res_len tokens
+ * of the ring, starting at slot res_start) followed by new_tokens new tokens
+ * that have not been copied anywhere: element (b, h, t, d) of k_new/v_new is
+ * at b*new_batch_stride + h*new_head_stride + t*new_token_stride + d (in
+ * elements of new_dtype: 0 f32, 1 bf16, 2 f16; both tensors share the
+ * strides).  Chunk j takes tokens [j*G, (j+1)*G) of that run and is written
+ * as chunk chunk_index + j in the layout of kivi_store_flush (same codes,
+ * scales, zeros and history rows).  bf16/f16 inputs are widened exactly.
+ * Replaces the flush loop of KiviCache.add_tokens (manager.py:242-249) and the
+ * host-side transpose of each chunk (manager.py:332-334): a prompt of P
+ * tokens is quantised by one launch.  The caller then keeps the tokens after
+ * the last chunk (in the ring, and the new tokens past n_chunks*G - res_len).
+ * Requires n_chunks*G <= res_len + new_tokens and group_size_k * head_dim <=
+ * 65536. */
+int kivi_store_flush_chunks(const float* k_res, const float* v_res, const void* k_new,
+                            const void* v_new, int32_t new_dtype, int64_t new_batch_stride,
+                            int64_t new_head_stride, int64_t new_token_stride,
+                            int32_t new_tokens, uint8_t* k_codes, float* k_scale,
+                            float* k_zero, uint8_t* v_codes, float* v_scale, float* v_zero,
+                            float* k_hist, float* v_hist, int64_t hist_capacity,
+                            int32_t batch, int32_t kv_heads, int32_t head_dim,
+                            int32_t group_size_k, int32_t group_size_v, int32_t res_capacity,
+                            int32_t res_start, int32_t res_len, int32_t chunk_capacity,
+                            int32_t chunk_index, int32_t n_chunks, void* stream);
+
 /* Code layout of a store with these shapes: 1 (matrix-core operand order)
  * when head_dim is 64, 128 or 256, group_size_k is 32 or 64 and
  * group_size_v is a multiple of 32 dividing head_dim; 0 (plain) otherwise.

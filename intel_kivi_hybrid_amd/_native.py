@@ -38,6 +38,9 @@ SIGNATURES = {
     "kivi_quant_dequant_roundtrip_values": [_vp, _vp, _i64, _i32, _i32, _vp],
     "kivi_store_flush": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+    "kivi_store_flush_chunks": [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _vp, _vp,
+                                _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32,
+                                _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     "kivi_store_code_layout": [_i32, _i32, _i32],
     "kivi_packed_decode_attention_workspace_size": [_i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                                     _i32, _i32],

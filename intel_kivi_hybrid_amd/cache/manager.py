@@ -14,10 +14,12 @@ layer owns a :class:`~intel_kivi_hybrid_amd.store.PackedKVStore` in HBM:
 * the dequantised history that ``get_full_cache()`` serves, written by the
   flush kernel itself (bit-identical to the reference's round-trip ops).
 
-A flush is one kernel launch over all (batch, kv-head) pairs of a layer,
-reading the residual ring in place; no host copy is involved.  New tokens are
-copied to the device once (a no-op move when the model already runs on it);
-served tensors are placed on the device the model's K/V came from.
+All the flushes one add_tokens() owes for a layer are one kernel launch over
+every (batch, kv-head) pair, reading the residual ring and the new K/V in
+place (fp32, bf16 or fp16, any strides); no host copy is involved and only
+the tokens left over are copied into the ring.  New tokens are moved to the
+device once (a no-op when the model already runs on it); served tensors are
+placed on the device the model's K/V came from.
 """
 
 from typing import List, Optional
@@ -184,8 +186,9 @@ class KiviCache:
 
             store = self._store_for(i, k.shape[0], k.shape[1], new_k.shape[2])
             self._serve_device[i] = k.device
-            flushes = store.extend(new_k.to(self.device, torch.float32),
-                                   new_v.to(self.device, torch.float32), flush_at=self.R)
+            # fp32, bf16 and fp16 K/V are read as they are (widening to fp32
+            # is exact, as the reference's .float() is, manager.py:210-214).
+            flushes = store.extend(new_k, new_v, flush_at=self.R)
             if flushes:
                 self._record_flushes(i, flushes)
                 self._cache_view_valid = False

@@ -160,10 +160,11 @@ class KiviPackedLayer(CacheLayerMixin):
                              f"heads but got {B} x {H}; call reset() before a new batch")
         self.settle()
         n = key_states.shape[-2]
-        k = key_states.to(self.owner.device, torch.float32)
-        v = value_states.to(self.owner.device, torch.float32)
+        k = key_states.to(self.owner.device)
+        v = value_states.to(self.owner.device)
         if self.get_seq_length() == 0:
-            # Prompt: attention reads these tensors, the store takes them.
+            # Prompt: attention reads these tensors, the store takes them
+            # (every owed chunk in one flush launch).
             self.flushes += st.extend(k, v, flush_at=self.owner.R)
             self._prompt = True
         elif n == 1:

@@ -1,11 +1,14 @@
 // HBM-resident packed KV store: flush of the oldest residual tokens into 2-bit
 // chunks.
 //
-// Replaces KiviCache._flush_group (src/kivi_sycl/cache/manager.py:309-374):
-// instead of transposing on the host, copying to the device, round-tripping,
-// copying back and concatenating a CPU history, one kernel reads the G oldest
-// tokens of every (batch, kv-head) straight out of the device residual ring and
-// writes the packed chunk (and, optionally, the dequantised tokens the served
+// Replaces KiviCache._flush_group and the flush loop of add_tokens
+// (src/kivi_sycl/cache/manager.py:242-249,309-374): instead of transposing on
+// the host, copying to the device, round-tripping, copying back and
+// concatenating a CPU history once per G tokens, one launch quantises every
+// chunk a call owes, reading the tokens straight from where they are: the
+// device residual ring first, then the caller's new-token tensor (any batch,
+// head and token strides, fp32 / bf16 / fp16, channels contiguous).  It
+// writes the packed chunks (and, optionally, the dequantised tokens the served
 // cache needs) in place.
 //
 // Per (b, kv-head), chunk c of G tokens holds (layouts in kivi_common.hpp):
@@ -16,7 +19,11 @@
 //                 codes quantize_values produces on the chunk's [G, D] rows
 //   v_scale/v_zero [D/Gv][G]
 // The codes are byte-for-byte those of the reference ops, only arranged in the
-// store's own order (plain or MFMA-operand order).
+// store's own order (plain or MFMA-operand order).  bf16/fp16 inputs are
+// widened exactly, so they quantise as their fp32 upcast does (the reference
+// upcasts with .float(), manager.py:210-214).
+#include <algorithm>
+
 #include "kivi_common.hpp"
 #include "../../include/kivi_hip.h"
 
@@ -24,11 +31,15 @@ namespace kivi {
 namespace {
 
 constexpr int kFlushBlock = 256;
-constexpr int kTileMaxElems = 8192;   // G*D staged in LDS (fp32 tile + u8 codes)
+constexpr int kTileMaxElems = 8192;
+constexpr int kMaxPerBlock = 1;       // chunks per flush_fast_kernel workgroup   // G*D staged in LDS (fp32 tile + u8 codes)
 
 struct FlushArgs {
-    const float* k_res;   // [B, H, Rcap, D]
+    const float* k_res;   // [B, H, Rcap, D] ring
     const float* v_res;
+    const void* k_new;    // new tokens: element (b, h, t, d) at b*new_sb + h*new_sh + t*new_st + d
+    const void* v_new;
+    int64_t new_sb, new_sh, new_st;
     uint8_t* k_codes;     // [B, H, Cmax, G*D/4]
     float* k_scale;       // [B, H, Cmax, D]
     float* k_zero;
@@ -38,12 +49,79 @@ struct FlushArgs {
     float* k_hist;        // optional [B, H, Tcap, D] dequantised keys
     float* v_hist;
     int64_t hist_cap;     // Tcap
-    int D, G, Gv, Rcap, res_start, Cmax, chunk;
+    // Token vt of the flushed run is ring slot (res_start + vt) % Rcap while
+    // vt < res_len, else new token vt - res_len.  Launch chunk j covers
+    // tokens [j*G, (j+1)*G) and is stored as chunk `chunk + j`.
+    int H, D, G, Gv, Rcap, res_start, res_len, Cmax, chunk;
+    int n_chunks;         // chunks in this launch: run chunks first .. first+n_chunks-1
+    int first;            // (flush_fast_kernel only; flush_kernel starts at 0)
+    bool new_vec;         // new rows allow 16-byte (fp32) / 8-byte (16-bit) loads
 };
+
+enum SrcType { kSrcF32 = 0, kSrcBF16 = 1, kSrcF16 = 2 };
+// Where a flush_fast_kernel launch's chunks come from: all from the ring, all
+// from the new tokens, or across both.
+enum RunMode { kFromRing = 0, kFromNew = 1, kFromBoth = 2 };
 
 __device__ __forceinline__ int ring(int start, int t, int cap) {
     const int s = start + t;
     return s >= cap ? s - cap : s;
+}
+
+template <int SRC>
+__device__ __forceinline__ float widen(const void* p, int64_t i) {
+    if constexpr (SRC == kSrcF32) {
+        return static_cast<const float*>(p)[i];
+    } else if constexpr (SRC == kSrcBF16) {
+        return __uint_as_float((uint32_t)static_cast<const uint16_t*>(p)[i] << 16);
+    } else {
+        return (float)static_cast<const _Float16*>(p)[i];
+    }
+}
+
+// Four consecutive channels of one new-token row, widened to fp32, with one
+// 16-byte (fp32) or 8-byte (16-bit) load: the row and channel offsets must
+// be aligned to that size.
+template <int SRC>
+__device__ __forceinline__ float4 load4_vec(const void* p, int64_t i) {
+    if constexpr (SRC == kSrcF32) {
+        return *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+    } else {
+        const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+        if constexpr (SRC == kSrcBF16) {
+            return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                               __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+        } else {
+            return make_float4((float)__builtin_bit_cast(_Float16, (uint16_t)(u.x & 0xffffu)),
+                               (float)__builtin_bit_cast(_Float16, (uint16_t)(u.x >> 16)),
+                               (float)__builtin_bit_cast(_Float16, (uint16_t)(u.y & 0xffffu)),
+                               (float)__builtin_bit_cast(_Float16, (uint16_t)(u.y >> 16)));
+        }
+    }
+}
+
+// Four consecutive channels of one new-token row, widened to fp32.
+template <int SRC>
+__device__ __forceinline__ float4 load4_new(const void* p, int64_t i, bool vec) {
+    if constexpr (SRC == kSrcF32) {
+        if (vec) return *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+    } else {
+        if (vec) {
+            const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+            if constexpr (SRC == kSrcBF16) {
+                return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                                   __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+            } else {
+                return make_float4(
+                    (float)__builtin_bit_cast(_Float16, (uint16_t)(u.x & 0xffffu)),
+                    (float)__builtin_bit_cast(_Float16, (uint16_t)(u.x >> 16)),
+                    (float)__builtin_bit_cast(_Float16, (uint16_t)(u.y & 0xffffu)),
+                    (float)__builtin_bit_cast(_Float16, (uint16_t)(u.y >> 16)));
+            }
+        }
+    }
+    return make_float4(widen<SRC>(p, i), widen<SRC>(p, i + 1), widen<SRC>(p, i + 2),
+                       widen<SRC>(p, i + 3));
 }
 
 // Writes one chunk's codes (u8 per element in `codes`, [G][D]) in the store
@@ -97,33 +175,46 @@ __device__ void write_codes(const uint8_t* codes, uint8_t* out, int G, int D) {
     }
 }
 
-// One workgroup per (b, kv-head).  TILE: the chunk's G x D fp32 tokens are
-// first staged in LDS with coalesced loads (needs G*D <= kTileMaxElems);
-// otherwise elements are read from the residual ring directly.
-template <int LAYOUT, bool TILE>
+// One workgroup per (b, kv-head, chunk).  TILE: the chunk's G x D tokens are
+// first staged in LDS as fp32 with coalesced loads (needs G*D <=
+// kTileMaxElems); otherwise elements are read from their source directly.
+// SRC is the element type of the new-token source (the ring is fp32).
+template <int LAYOUT, bool TILE, int SRC>
 __global__ __launch_bounds__(kFlushBlock) void flush_kernel(FlushArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int D = a.D, G = a.G, Gv = a.Gv, NG = D / Gv;
     float* tile = reinterpret_cast<float*>(smem);                       // [G][D] if TILE
     uint8_t* codes = smem + (TILE ? (size_t)G * D * sizeof(float) : 0); // [G][D]
     const int bh = blockIdx.x;
+    const int chunk = a.chunk + (int)blockIdx.y;
+    const int vt0 = (int)blockIdx.y * G;            // first token of this chunk in the run
     const int64_t res_base = (int64_t)bh * a.Rcap * D;
-    const int64_t chunk_id = (int64_t)bh * a.Cmax + a.chunk;
+    const int64_t new_base = (int64_t)(bh / a.H) * a.new_sb + (int64_t)(bh % a.H) * a.new_sh;
+    const int64_t chunk_id = (int64_t)bh * a.Cmax + chunk;
     const int64_t code_bytes = (int64_t)G * D / 4;
-    const int64_t hist_row0 = (int64_t)bh * a.hist_cap + (int64_t)a.chunk * G;
+    const int64_t hist_row0 = (int64_t)bh * a.hist_cap + (int64_t)chunk * G;
 
-    auto stage = [&](const float* src) {
+    auto stage = [&](const float* res, const void* nw) {
         const int nv = G * (D / 4);
         for (int e = threadIdx.x; e < nv; e += blockDim.x) {
             const int t = e / (D / 4), d4 = e % (D / 4);
-            const float4 x = reinterpret_cast<const float4*>(
-                src + res_base + (int64_t)ring(a.res_start, t, a.Rcap) * D)[d4];
+            const int vt = vt0 + t;
+            float4 x;
+            if (vt < a.res_len) {
+                x = reinterpret_cast<const float4*>(
+                    res + res_base + (int64_t)ring(a.res_start, vt, a.Rcap) * D)[d4];
+            } else {
+                x = load4_new<SRC>(nw, new_base + (int64_t)(vt - a.res_len) * a.new_st + 4 * d4,
+                                   a.new_vec);
+            }
             reinterpret_cast<float4*>(tile)[e] = x;
         }
     };
-    auto elem = [&](const float* src, int t, int d) -> float {
+    auto elem = [&](const float* res, const void* nw, int t, int d) -> float {
         if constexpr (TILE) return tile[t * D + d];
-        return src[res_base + (int64_t)ring(a.res_start, t, a.Rcap) * D + d];
+        const int vt = vt0 + t;
+        if (vt < a.res_len) return res[res_base + (int64_t)ring(a.res_start, vt, a.Rcap) * D + d];
+        return widen<SRC>(nw, new_base + (int64_t)(vt - a.res_len) * a.new_st + d);
     };
     // Dequantised tokens go back into the tile (TILE) and are then copied to
     // the history with coalesced stores.
@@ -139,13 +230,13 @@ __global__ __launch_bounds__(kFlushBlock) void flush_kernel(FlushArgs a) {
 
     // ---- keys: one group per channel, along the chunk's G tokens ----------
     if constexpr (TILE) {
-        stage(a.k_res);
+        stage(a.k_res, a.k_new);
         __syncthreads();
     }
     for (int d = threadIdx.x; d < D; d += blockDim.x) {
         float mn = 1e30f, mx = -1e30f;
         for (int t = 0; t < G; ++t) {
-            const float x = elem(a.k_res, t, d);
+            const float x = elem(a.k_res, a.k_new, t, d);
             mn = fmin_nan(mn, x);
             mx = fmax_nan(mx, x);
         }
@@ -154,7 +245,7 @@ __global__ __launch_bounds__(kFlushBlock) void flush_kernel(FlushArgs a) {
         a.k_scale[chunk_id * D + d] = scale;
         a.k_zero[chunk_id * D + d] = mn;
         for (int t = 0; t < G; ++t) {
-            const uint32_t q = code_exact(elem(a.k_res, t, d), mn, scale);
+            const uint32_t q = code_exact(elem(a.k_res, a.k_new, t, d), mn, scale);
             codes[t * D + d] = (uint8_t)q;
             const float xh = decode1(q, scale, mn);
             if constexpr (TILE) {
@@ -171,7 +262,7 @@ __global__ __launch_bounds__(kFlushBlock) void flush_kernel(FlushArgs a) {
 
     // ---- values: groups of Gv channels within each token --------------------
     if constexpr (TILE) {
-        stage(a.v_res);
+        stage(a.v_res, a.v_new);
         __syncthreads();
     }
     for (int e = threadIdx.x; e < G * NG; e += blockDim.x) {
@@ -184,7 +275,7 @@ __global__ __launch_bounds__(kFlushBlock) void flush_kernel(FlushArgs a) {
         for (int jj = 0; jj < Gv; ++jj) {
             int j = jj + rot;
             j = j >= Gv ? j - Gv : j;
-            const float x = elem(a.v_res, t, gi * Gv + j);
+            const float x = elem(a.v_res, a.v_new, t, gi * Gv + j);
             mn = fmin_nan(mn, x);
             mx = fmax_nan(mx, x);
         }
@@ -196,7 +287,7 @@ __global__ __launch_bounds__(kFlushBlock) void flush_kernel(FlushArgs a) {
             int j = jj + rot;
             j = j >= Gv ? j - Gv : j;
             const int d = gi * Gv + j;
-            const uint32_t q = code_exact(elem(a.v_res, t, d), mn, scale);
+            const uint32_t q = code_exact(elem(a.v_res, a.v_new, t, d), mn, scale);
             codes[t * D + d] = (uint8_t)q;
             const float xh = decode1(q, scale, mn);
             if constexpr (TILE) {
@@ -211,6 +302,331 @@ __global__ __launch_bounds__(kFlushBlock) void flush_kernel(FlushArgs a) {
     write_codes<LAYOUT, false>(codes, a.v_codes + chunk_id * code_bytes, G, D);
 }
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also
+// waits for every outstanding global load (s_waitcnt vmcnt(0)), which would
+// drain the next chunk's prefetch at each barrier; no thread here reads
+// global memory another thread of the workgroup wrote.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// 1/scale for code_rcp, or NaN when the scale is outside the range where
+// v_rcp_f32 is accurate, so that code_rcp flags every element of that group.
+__device__ __forceinline__ float rcp_or_nan(float scale) {
+    return (scale >= 1e-10f) && (scale <= 0x1.0p120f) ? __builtin_amdgcn_rcpf(scale)
+                                                       : __builtin_nanf("");
+}
+
+// Code of one element from its group's min and rcp_or_nan(scale): the
+// reciprocal path of encode4.  `bad` collects the elements that need the
+// exact divide (near a rounding tie, NaN input, or a flagged scale).
+__device__ __forceinline__ uint32_t code_rcp(float x, float mn, float r, bool& bad) {
+    const float u = fmaf(x - mn, r, 0.5f);
+    bad |= !(fabsf(__builtin_amdgcn_fractf(u) - 0.5f) < 0.5f - kTieGuard);
+    return (uint32_t)fminf(fmaxf(u, 0.0f), 3.0f);
+}
+
+// Matrix-core layout with compile-time shapes (G*D <= kTileMaxElems).  One
+// workgroup of 256 threads per (b, kv-head, chunk) loads the chunk's K and V
+// at once (V waits in registers while K is quantised).  Per tensor:
+//  1. the [G][D] tokens go to an fp32 LDS tile whose rows are padded by four
+//     floats (bank spread for the column and 8-channel reads below);
+//  2. group statistics: keys -- thread (segment s, channel d) scans tokens
+//     [s*E, (s+1)*E) of channel d, segments combine through LDS; values --
+//     thread (token t, group g, segment s) scans channels [g*GV + s*E, +E),
+//     segments are adjacent lanes and combine with DPP.  Each group's
+//     (min, scale, rcp_or_nan(scale)) is published in LDS (scale and zero
+//     also go to HBM);
+//  3. each thread builds whole output dwords of the matrix-core code order
+//     (16 codes: two tiles x 8 elements) from the tile and the group
+//     parameters and stores them straight to HBM, so codes never pass
+//     through LDS as bytes.
+// Same codes, scales, zeros and history as flush_kernel.
+template <int G, int D, int GV, int SRC, int MODE>
+__global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
+    constexpr int N = G * D;
+    constexpr int E = N / kFlushBlock;        // elements per thread in step 2
+    constexpr int NG = D / GV;
+    constexpr int NSK = kFlushBlock / D;
+    constexpr int NSV = GV / E;
+    constexpr int NV = N / 4 / kFlushBlock;   // float4 per thread per tensor
+    constexpr int LD = D + 4;                 // padded tile row (floats)
+    constexpr int NP = N / 1024;              // code dwords per lane per tensor
+    constexpr int NW = (64 * NP + kFlushBlock - 1) / kFlushBlock;
+    static_assert(N % (4 * kFlushBlock) == 0 && E * NSK == G && NSV >= 1 && NSV <= 64 &&
+                  (NSV & (NSV - 1)) == 0 && kFlushBlock % D == 0 && G % 16 == 0 &&
+                  GV % 32 == 0, "flush_fast shape");
+    __shared__ __align__(16) float tile[G * LD];
+    __shared__ __align__(16) float kpar[3][D];          // min, scale, 1/scale per channel
+    __shared__ __align__(16) float4 vpar[G * NG];       // (min, scale, 1/scale, -) per group
+    __shared__ float part[2][NSK][D];
+
+    const int tid = threadIdx.x;
+    const int bh = blockIdx.x;
+    const int64_t res_base = (int64_t)bh * a.Rcap * D;
+    const int64_t new_base = (int64_t)(bh / a.H) * a.new_sb + (int64_t)(bh % a.H) * a.new_sh;
+    const int j = a.first + (int)blockIdx.y;   // run chunk of this workgroup
+
+    // K or V of run chunk j: float4 slot i*256 + tid of the [G][D] chunk.  The
+    // source is fixed per launch (MODE), so the loads carry no branches and
+    // the compiler's wait counting keeps the next chunk's loads in flight.
+    auto load = [&](float4 (&x)[NV], const float* res, const void* nw, int j) {
+        const int vt0 = j * G;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int e = i * kFlushBlock + tid;
+            const int t = e / (D / 4), d4 = e % (D / 4);
+            const int vt = vt0 + t;
+            if constexpr (MODE == kFromNew) {
+                x[i] = load4_vec<SRC>(nw, new_base + (int64_t)(vt - a.res_len) * a.new_st + 4 * d4);
+            } else if constexpr (MODE == kFromRing) {
+                const int64_t row = res_base + (int64_t)ring(a.res_start, vt, a.Rcap) * D;
+                x[i] = reinterpret_cast<const float4*>(res + row)[d4];
+            } else {
+                if (vt < a.res_len) {
+                    const int64_t row = res_base + (int64_t)ring(a.res_start, vt, a.Rcap) * D;
+                    x[i] = reinterpret_cast<const float4*>(res + row)[d4];
+                } else {
+                    x[i] = load4_vec<SRC>(nw, new_base + (int64_t)(vt - a.res_len) * a.new_st + 4 * d4);
+                }
+            }
+        }
+    };
+    auto put = [&](const float4 (&x)[NV]) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int e = i * kFlushBlock + tid;
+            const int t = e / (D / 4), d4 = e % (D / 4);
+            *reinterpret_cast<float4*>(tile + t * LD + 4 * d4) = x[i];
+        }
+    };
+    // Dequantised tokens (written back into the tile) -> history rows.
+    auto copy_hist = [&](float* hist, int64_t row0) {
+        for (int e = tid; e < N / 4; e += kFlushBlock) {
+            const int t = e / (D / 4), d4 = e % (D / 4);
+            reinterpret_cast<float4*>(hist + (row0 + t) * D)[d4] =
+                *reinterpret_cast<const float4*>(tile + t * LD + 4 * d4);
+        }
+    };
+
+    float4 kx[NV], vx[NV];
+    load(kx, a.k_res, a.k_new, j);
+    load(vx, a.v_res, a.v_new, j);
+    {
+        const int chunk = a.chunk + j;
+        const int64_t chunk_id = (int64_t)bh * a.Cmax + chunk;
+        const int64_t hist_row0 = (int64_t)bh * a.hist_cap + (int64_t)chunk * G;
+        uint32_t* const kout = reinterpret_cast<uint32_t*>(a.k_codes + chunk_id * (N / 4));
+        uint32_t* const vout = reinterpret_cast<uint32_t*>(a.v_codes + chunk_id * (N / 4));
+
+        // ================================ keys ================================
+        put(kx);
+        lds_barrier();
+        {
+            const int d = tid % D, sg = tid / D;
+            float mn = 1e30f, mx = -1e30f;
+#pragma unroll
+            for (int i = 0; i < E; ++i) {
+                const float x = tile[(sg * E + i) * LD + d];
+                mn = fmin_nan(mn, x);
+                mx = fmax_nan(mx, x);
+            }
+            if constexpr (NSK > 1) {
+                part[0][sg][d] = mn;
+                part[1][sg][d] = mx;
+                lds_barrier();
+#pragma unroll
+                for (int s2 = 0; s2 < NSK; ++s2) {
+                    mn = fmin_nan(mn, part[0][s2][d]);
+                    mx = fmax_nan(mx, part[1][s2][d]);
+                }
+            }
+            float scale;
+            finish_group(mn, mx, scale);
+            if (sg == 0) {
+                a.k_scale[chunk_id * D + d] = scale;
+                a.k_zero[chunk_id * D + d] = mn;
+                kpar[0][d] = mn;
+                kpar[1][d] = scale;
+                kpar[2][d] = rcp_or_nan(scale);
+            }
+        }
+        lds_barrier();
+        // Key tile ks*(G/16)+nb: lane l element j = token 16nb + l%16, channel
+        // 32ks + 8(l/16) + j.  Dword (l, w) holds tiles 2w and 2w+1.
+#pragma unroll
+        for (int it = 0; it < NW; ++it) {
+            const int e = it * kFlushBlock + tid;
+            if (e < 64 * NP) {
+                const int l = e / NP, w = e % NP;
+                uint32_t word = 0;
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    const int tl = 2 * w + m, ks = tl / (G / 16), nb = tl % (G / 16);
+                    const int t = 16 * nb + l % 16, d0 = 32 * ks + 8 * (l / 16);
+                    float x[8], mnv[8], scv[8], rcv[8];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const float4 f = *reinterpret_cast<const float4*>(tile + t * LD + d0 + 4 * h);
+                        const float4 pm = *reinterpret_cast<const float4*>(&kpar[0][d0 + 4 * h]);
+                        const float4 ps = *reinterpret_cast<const float4*>(&kpar[1][d0 + 4 * h]);
+                        const float4 pr = *reinterpret_cast<const float4*>(&kpar[2][d0 + 4 * h]);
+                        x[4 * h] = f.x; x[4 * h + 1] = f.y; x[4 * h + 2] = f.z; x[4 * h + 3] = f.w;
+                        mnv[4 * h] = pm.x; mnv[4 * h + 1] = pm.y; mnv[4 * h + 2] = pm.z; mnv[4 * h + 3] = pm.w;
+                        scv[4 * h] = ps.x; scv[4 * h + 1] = ps.y; scv[4 * h + 2] = ps.z; scv[4 * h + 3] = ps.w;
+                        rcv[4 * h] = pr.x; rcv[4 * h + 1] = pr.y; rcv[4 * h + 2] = pr.z; rcv[4 * h + 3] = pr.w;
+                    }
+                    bool bad = false;
+                    uint32_t q[8];
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) q[jj] = code_rcp(x[jj], mnv[jj], rcv[jj], bad);
+                    if (__builtin_expect(bad, 0)) {
+#pragma unroll
+                        for (int jj = 0; jj < 8; ++jj) q[jj] = code_exact(x[jj], mnv[jj], scv[jj]);
+                    }
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) {
+                        word |= q[jj] << mfma_code_bit(m, jj);
+                        if (a.k_hist) tile[t * LD + d0 + jj] = decode1(q[jj], scv[jj], mnv[jj]);
+                    }
+                }
+                kout[e] = word;
+            }
+        }
+        if (a.k_hist) {
+            lds_barrier();
+            copy_hist(a.k_hist, hist_row0);
+        }
+
+        // =============================== values ===============================
+        lds_barrier();
+        put(vx);
+        lds_barrier();
+        {
+            const int sg = tid % NSV, grp = tid / NSV;
+            const int t = grp / NG, gi = grp % NG;
+            const int c0 = gi * GV + sg * E;
+            float mn = 1e30f, mx = -1e30f;
+#pragma unroll
+            for (int q4 = 0; q4 < E / 4; ++q4) {
+                const float4 f = *reinterpret_cast<const float4*>(tile + t * LD + c0 + 4 * q4);
+                mn = fmin_nan(fmin_nan(mn, f.x), fmin_nan(f.y, fmin_nan(f.z, f.w)));
+                mx = fmax_nan(fmax_nan(mx, f.x), fmax_nan(f.y, fmax_nan(f.z, f.w)));
+            }
+            seg_min_max<NSV>(mn, mx);
+            float scale;
+            finish_group(mn, mx, scale);
+            if (sg == 0) {
+                a.v_scale[(chunk_id * NG + gi) * G + t] = scale;
+                a.v_zero[(chunk_id * NG + gi) * G + t] = mn;
+                vpar[t * NG + gi] = make_float4(mn, scale, rcp_or_nan(scale), 0.0f);
+            }
+        }
+        lds_barrier();
+        // Value tile kt*(D/16)+nb: lane l element j = token 32kt + 8(l/16) + j,
+        // channel 16nb + l%16.
+#pragma unroll
+        for (int it = 0; it < NW; ++it) {
+            const int e = it * kFlushBlock + tid;
+            if (e < 64 * NP) {
+                const int l = e / NP, w = e % NP;
+                uint32_t word = 0;
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    const int tl = 2 * w + m, kt = tl / (D / 16), nb = tl % (D / 16);
+                    const int c = 16 * nb + l % 16, t0 = 32 * kt + 8 * (l / 16);
+                    float x[8];
+                    float4 par[8];
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) {
+                        x[jj] = tile[(t0 + jj) * LD + c];
+                        par[jj] = vpar[(t0 + jj) * NG + c / GV];
+                    }
+                    bool bad = false;
+                    uint32_t q[8];
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj)
+                        q[jj] = code_rcp(x[jj], par[jj].x, par[jj].z, bad);
+                    if (__builtin_expect(bad, 0)) {
+#pragma unroll
+                        for (int jj = 0; jj < 8; ++jj) q[jj] = code_exact(x[jj], par[jj].x, par[jj].y);
+                    }
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) {
+                        word |= q[jj] << mfma_code_bit(m, jj);
+                        if (a.v_hist) tile[(t0 + jj) * LD + c] = decode1(q[jj], par[jj].y, par[jj].x);
+                    }
+                }
+                vout[e] = word;
+            }
+        }
+        if (a.v_hist) {
+            lds_barrier();
+            copy_hist(a.v_hist, hist_row0);
+        }
+    }
+}
+
+template <int G, int D, int GV, int MODE>
+void launch_fast4(const FlushArgs& a, int src, dim3 grid, hipStream_t st) {
+    switch (src) {
+        case kSrcBF16: flush_fast_kernel<G, D, GV, kSrcBF16, MODE><<<grid, kFlushBlock, 0, st>>>(a); break;
+        case kSrcF16: flush_fast_kernel<G, D, GV, kSrcF16, MODE><<<grid, kFlushBlock, 0, st>>>(a); break;
+        default: flush_fast_kernel<G, D, GV, kSrcF32, MODE><<<grid, kFlushBlock, 0, st>>>(a); break;
+    }
+}
+
+template <int G, int D, int GV>
+void launch_fast3(const FlushArgs& a, int src, int mode, dim3 grid, hipStream_t st) {
+    if (mode == kFromNew) launch_fast4<G, D, GV, kFromNew>(a, src, grid, st);
+    else if (mode == kFromRing) launch_fast4<G, D, GV, kFromRing>(a, kSrcF32, grid, st);
+    else launch_fast4<G, D, GV, kFromBoth>(a, src, grid, st);
+}
+
+template <int G, int D>
+bool launch_fast2(const FlushArgs& a, int src, int mode, dim3 grid, hipStream_t st) {
+    switch (a.Gv) {
+        case 32: launch_fast3<G, D, 32>(a, src, mode, grid, st); return true;
+        case 64: launch_fast3<G, D, 64>(a, src, mode, grid, st); return true;
+        case 128:
+            if constexpr (D >= 128) { launch_fast3<G, D, 128>(a, src, mode, grid, st); return true; }
+            return false;
+        case 256:
+            if constexpr (D >= 256) { launch_fast3<G, D, 256>(a, src, mode, grid, st); return true; }
+            return false;
+        default: return false;
+    }
+}
+
+bool fast_shape(int G, int D) {
+    return (G == 32 && (D == 64 || D == 128 || D == 256)) || (G == 64 && (D == 64 || D == 128));
+}
+
+// One flush_fast_kernel launch over run chunks [first, first + count) whose
+// source is `mode`: one workgroup per (b, kv-head, chunk).
+bool launch_fast(FlushArgs a, int src, int mode, int first, int count, int bh, hipStream_t st) {
+    a.first = first;
+    a.n_chunks = count;
+    const dim3 grid(bh, count);
+    if (a.G == 32 && a.D == 64) return launch_fast2<32, 64>(a, src, mode, grid, st);
+    if (a.G == 32 && a.D == 128) return launch_fast2<32, 128>(a, src, mode, grid, st);
+    if (a.G == 32 && a.D == 256) return launch_fast2<32, 256>(a, src, mode, grid, st);
+    if (a.G == 64 && a.D == 64) return launch_fast2<64, 64>(a, src, mode, grid, st);
+    if (a.G == 64 && a.D == 128) return launch_fast2<64, 128>(a, src, mode, grid, st);
+    return false;
+}
+
+template <int LAYOUT, bool TILE>
+void launch_flush(const FlushArgs& a, int src, dim3 grid, size_t lds, hipStream_t st) {
+    switch (src) {
+        case kSrcBF16: flush_kernel<LAYOUT, TILE, kSrcBF16><<<grid, kFlushBlock, lds, st>>>(a); break;
+        case kSrcF16: flush_kernel<LAYOUT, TILE, kSrcF16><<<grid, kFlushBlock, lds, st>>>(a); break;
+        default: flush_kernel<LAYOUT, TILE, kSrcF32><<<grid, kFlushBlock, lds, st>>>(a); break;
+    }
+}
+
 }  // namespace
 }  // namespace kivi
 
@@ -221,14 +637,15 @@ extern "C" int kivi_store_code_layout(int32_t head_dim, int32_t group_size_k,
     return code_layout_for(head_dim, group_size_k, group_size_v);
 }
 
-extern "C" int kivi_store_flush(const float* k_res, const float* v_res, uint8_t* k_codes,
-                                float* k_scale, float* k_zero, uint8_t* v_codes,
-                                float* v_scale, float* v_zero, float* k_hist, float* v_hist,
-                                int64_t hist_capacity, int32_t batch, int32_t kv_heads,
-                                int32_t head_dim, int32_t group_size_k,
-                                int32_t group_size_v, int32_t res_capacity,
-                                int32_t res_start, int32_t chunk_capacity,
-                                int32_t chunk_index, void* stream) {
+extern "C" int kivi_store_flush_chunks(
+        const float* k_res, const float* v_res, const void* k_new, const void* v_new,
+        int32_t new_dtype, int64_t new_batch_stride, int64_t new_head_stride,
+        int64_t new_token_stride, int32_t new_tokens, uint8_t* k_codes, float* k_scale,
+        float* k_zero, uint8_t* v_codes, float* v_scale, float* v_zero, float* k_hist,
+        float* v_hist, int64_t hist_capacity, int32_t batch, int32_t kv_heads,
+        int32_t head_dim, int32_t group_size_k, int32_t group_size_v, int32_t res_capacity,
+        int32_t res_start, int32_t res_len, int32_t chunk_capacity, int32_t chunk_index,
+        int32_t n_chunks, void* stream) {
     if (!k_res || !v_res || !k_codes || !k_scale || !k_zero || !v_codes || !v_scale || !v_zero)
         return set_error(kErrInvalidArgument, "null tensor pointer");
     if ((k_hist == nullptr) != (v_hist == nullptr))
@@ -249,10 +666,26 @@ extern "C" int kivi_store_flush(const float* k_res, const float* v_res, uint8_t*
     if (res_start < 0 || res_start >= res_capacity)
         return set_error(kErrInvalidArgument, "res_start %d outside [0, %d)", res_start,
                          res_capacity);
-    if (chunk_index < 0 || chunk_index >= chunk_capacity)
-        return set_error(kErrInvalidArgument, "chunk %d outside capacity %d", chunk_index,
-                         chunk_capacity);
-    if (k_hist && (int64_t)(chunk_index + 1) * group_size_k > hist_capacity)
+    if (res_len < 0 || res_len > res_capacity)
+        return set_error(kErrInvalidArgument, "res_len %d outside [0, %d]", res_len,
+                         res_capacity);
+    if (new_tokens < 0 || (new_tokens > 0 && (!k_new || !v_new)))
+        return set_error(kErrInvalidArgument, "new tokens given without k_new/v_new");
+    if (new_dtype < kSrcF32 || new_dtype > kSrcF16)
+        return set_error(kErrInvalidArgument, "new_dtype %d is not 0 (f32), 1 (bf16) or 2 (f16)",
+                         new_dtype);
+    if (new_batch_stride < 0 || new_head_stride < 0 || new_token_stride < 0)
+        return set_error(kErrInvalidArgument, "negative new-token strides");
+    if (n_chunks <= 0 || n_chunks > 65535)
+        return set_error(kErrInvalidArgument, "n_chunks %d outside [1, 65535]", n_chunks);
+    if ((int64_t)n_chunks * group_size_k > (int64_t)res_len + new_tokens)
+        return set_error(kErrInvalidArgument, "%d chunks of %d need %lld tokens, %lld available",
+                         n_chunks, group_size_k, (long long)n_chunks * group_size_k,
+                         (long long)res_len + new_tokens);
+    if (chunk_index < 0 || (int64_t)chunk_index + n_chunks > chunk_capacity)
+        return set_error(kErrInvalidArgument, "chunks %d..%d outside capacity %d", chunk_index,
+                         chunk_index + n_chunks - 1, chunk_capacity);
+    if (k_hist && (int64_t)(chunk_index + n_chunks) * group_size_k > hist_capacity)
         return set_error(kErrInvalidArgument, "history capacity %lld too small",
                          (long long)hist_capacity);
     const int64_t elems = (int64_t)group_size_k * head_dim;
@@ -261,20 +694,57 @@ extern "C" int kivi_store_flush(const float* k_res, const float* v_res, uint8_t*
                          (long long)elems);
     const bool aligned = ((uintptr_t)k_res % 16 == 0) && ((uintptr_t)v_res % 16 == 0) &&
                          (!k_hist || ((uintptr_t)k_hist % 16 == 0 && (uintptr_t)v_hist % 16 == 0));
+    const int esize = new_dtype == kSrcF32 ? 4 : 2;
+    const int64_t vec_bytes = 4 * esize;   // four channels per load
+    const bool new_vec = new_tokens == 0 ||
+        ((uintptr_t)k_new % vec_bytes == 0 && (uintptr_t)v_new % vec_bytes == 0 &&
+         (new_batch_stride * esize) % vec_bytes == 0 && (new_head_stride * esize) % vec_bytes == 0 &&
+         (new_token_stride * esize) % vec_bytes == 0);
     const bool tile = elems <= kTileMaxElems && aligned;
     const int layout = code_layout_for(head_dim, group_size_k, group_size_v);
     const size_t lds = (size_t)elems * (tile ? sizeof(float) + 1 : 1);
-    FlushArgs a{k_res, v_res, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero,
-                k_hist, v_hist, hist_capacity, head_dim, group_size_k, group_size_v,
-                res_capacity, res_start, chunk_capacity, chunk_index};
-    const dim3 grid(batch * kv_heads);
+    FlushArgs a{k_res, v_res, k_new, v_new, new_batch_stride, new_head_stride,
+                new_token_stride, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero,
+                k_hist, v_hist, hist_capacity, kv_heads, head_dim, group_size_k,
+                group_size_v, res_capacity, res_start, res_len, chunk_capacity, chunk_index,
+                n_chunks, 0, new_vec};
+    const dim3 grid(batch * kv_heads, n_chunks);
     hipStream_t st = (hipStream_t)stream;
+    const bool fast_gv = group_size_v % 32 == 0 && group_size_v <= head_dim;
+    if (layout == kLayoutMfma && tile && new_vec && fast_gv &&
+        fast_shape(group_size_k, head_dim)) {
+        // Chunks wholly in the ring, at most one across ring and new tokens,
+        // then chunks wholly in the new tokens: one launch each.
+        const int bh = batch * kv_heads;
+        const int n_ring = std::min(n_chunks, res_len / group_size_k);
+        const int n_both = (n_ring < n_chunks && res_len % group_size_k) ? 1 : 0;
+        const int n_new = n_chunks - n_ring - n_both;
+        if (n_ring) launch_fast(a, new_dtype, kFromRing, 0, n_ring, bh, st);
+        if (n_both) launch_fast(a, new_dtype, kFromBoth, n_ring, 1, bh, st);
+        if (n_new) launch_fast(a, new_dtype, kFromNew, n_ring + n_both, n_new, bh, st);
+        return check_launch("store_flush");
+    }
     if (layout == kLayoutMfma) {
-        if (tile) flush_kernel<kLayoutMfma, true><<<grid, kFlushBlock, lds, st>>>(a);
-        else flush_kernel<kLayoutMfma, false><<<grid, kFlushBlock, lds, st>>>(a);
+        if (tile) launch_flush<kLayoutMfma, true>(a, new_dtype, grid, lds, st);
+        else launch_flush<kLayoutMfma, false>(a, new_dtype, grid, lds, st);
     } else {
-        if (tile) flush_kernel<kLayoutPlain, true><<<grid, kFlushBlock, lds, st>>>(a);
-        else flush_kernel<kLayoutPlain, false><<<grid, kFlushBlock, lds, st>>>(a);
+        if (tile) launch_flush<kLayoutPlain, true>(a, new_dtype, grid, lds, st);
+        else launch_flush<kLayoutPlain, false>(a, new_dtype, grid, lds, st);
     }
     return check_launch("store_flush");
+}
+
+extern "C" int kivi_store_flush(const float* k_res, const float* v_res, uint8_t* k_codes,
+                                float* k_scale, float* k_zero, uint8_t* v_codes,
+                                float* v_scale, float* v_zero, float* k_hist, float* v_hist,
+                                int64_t hist_capacity, int32_t batch, int32_t kv_heads,
+                                int32_t head_dim, int32_t group_size_k,
+                                int32_t group_size_v, int32_t res_capacity,
+                                int32_t res_start, int32_t chunk_capacity,
+                                int32_t chunk_index, void* stream) {
+    return kivi_store_flush_chunks(k_res, v_res, nullptr, nullptr, kSrcF32, 0, 0, 0, 0,
+                                   k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_hist,
+                                   v_hist, hist_capacity, batch, kv_heads, head_dim,
+                                   group_size_k, group_size_v, res_capacity, res_start,
+                                   group_size_k, chunk_capacity, chunk_index, 1, stream);
 }

@@ -27,6 +27,10 @@ from . import _native
 
 _lib = _native.load()
 
+# Element types the flush kernel reads directly (code passed to the C ABI).
+_SRC_DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+_MAX_CHUNKS_PER_LAUNCH = 65535
+
 
 def _vp(t: Optional[torch.Tensor]):
     return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
@@ -140,8 +144,9 @@ class PackedKVStore:
         return self.n_chunks * self.G
 
     def append(self, k: torch.Tensor, v: torch.Tensor) -> None:
-        """Copy new tokens ``[B, Hkv, n, D]`` into the residual window.  The
-        window must have room (callers flush first)."""
+        """Copy new tokens ``[B, Hkv, n, D]`` into the residual window (as
+        fp32; bf16/fp16 widen exactly).  The window must have room (callers
+        flush first)."""
         n = k.shape[2]
         if self.res_len + n > self.R:
             raise RuntimeError(f"residual window overflow ({self.res_len} + {n} > {self.R})")
@@ -154,23 +159,69 @@ class PackedKVStore:
             self.v_res[:, :, :n - first].copy_(v[:, :, first:])
         self.res_len += n
 
+    def _token_source(self, k: torch.Tensor, v: torch.Tensor):
+        """New tokens as the flush kernel reads them: on the store's device,
+        fp32/bf16/fp16, channels contiguous, K and V with the same strides
+        (copies are made only when the inputs are not already so)."""
+        if k.shape != v.shape or k.dim() != 4 or tuple(k.shape[:2]) != (self.B, self.H) \
+                or k.shape[3] != self.D:
+            raise ValueError(f"new tokens must be [B={self.B}, Hkv={self.H}, n, D={self.D}] for "
+                             f"both K and V, got {tuple(k.shape)} and {tuple(v.shape)}")
+        k, v = k.to(self.device), v.to(self.device)
+        if k.dtype not in _SRC_DTYPES or v.dtype != k.dtype:
+            k, v = k.to(torch.float32), v.to(torch.float32)
+        if k.stride(-1) != 1 or v.stride() != k.stride():
+            k, v = k.contiguous(), v.contiguous()
+        return k, v
+
     def extend(self, k: torch.Tensor, v: torch.Tensor, flush_at: Optional[int] = None) -> int:
-        """Append ``[B, Hkv, n, D]`` tokens, flushing the G oldest whenever the
-        residual reaches ``flush_at`` (default: the ring capacity), exactly as
-        KiviCache.add_tokens does (manager.py:226-249).  Returns the number of
-        flushes."""
+        """Append ``[B, Hkv, n, D]`` tokens and flush the G oldest while the
+        residual holds ``flush_at`` (default: the ring capacity) or more, with
+        the result of KiviCache.add_tokens (manager.py:226-249): the flushes
+        are ``0`` if res_len + n < flush_at, else ``(res_len + n - flush_at)
+        // G + 1``, and they take the oldest tokens of [residual ; new].
+
+        All owed chunks are quantised by one launch that reads the ring and
+        ``k``/``v`` in place (any strides with contiguous channels; fp32,
+        bf16 or fp16, widened exactly); only the tokens left over are copied
+        into the ring.  Returns the number of flushes."""
         R = self.R if flush_at is None else int(flush_at)
         if not self.G <= R <= self.R:
             raise ValueError(f"flush threshold {R} must lie in [{self.G}, {self.R}]")
-        n, t, flushes = k.shape[2], 0, 0
-        while t < n:
-            take = min(n - t, R - self.res_len)
-            self.append(k[:, :, t:t + take], v[:, :, t:t + take])
-            t += take
-            while self.res_len >= R:
-                self.flush()
-                flushes += 1
-        return flushes
+        k, v = self._token_source(k, v)
+        n = k.shape[2]
+        total = self.res_len + n
+        n_flush = 0 if total < R else (total - R) // self.G + 1
+        skip = 0                        # new tokens already quantised
+        done = 0
+        if n_flush:
+            self.reserve(self.n_chunks + n_flush)
+        while done < n_flush:
+            m = min(n_flush - done, _MAX_CHUNKS_PER_LAUNCH)
+            self._flush_run(k[:, :, skip:], v[:, :, skip:], m)
+            used = m * self.G
+            from_ring = min(used, self.res_len)
+            self.res_start = (self.res_start + from_ring) % self.R
+            self.res_len -= from_ring
+            skip += used - from_ring
+            done += m
+        if skip < n:
+            self.append(k[:, :, skip:], v[:, :, skip:])
+        return n_flush
+
+    def _flush_run(self, k: torch.Tensor, v: torch.Tensor, n_chunks: int) -> None:
+        """Quantise ``n_chunks`` chunks from [ring window ; k/v] (one launch)."""
+        hist_cap = self.capacity * self.G if self.keep_history else 0
+        sb, sh, st, _ = k.stride()
+        with torch.cuda.device(self.device):
+            _native.check(_lib.kivi_store_flush_chunks(
+                _vp(self.k_res), _vp(self.v_res), _vp(k), _vp(v), _SRC_DTYPES[k.dtype],
+                sb, sh, st, k.shape[2], _vp(self.k_codes), _vp(self.k_scale), _vp(self.k_zero),
+                _vp(self.v_codes), _vp(self.v_scale), _vp(self.v_zero), _vp(self.k_hist),
+                _vp(self.v_hist), hist_cap, self.B, self.H, self.D, self.G, self.Gv, self.R,
+                self.res_start, self.res_len, self.capacity, self.n_chunks, n_chunks,
+                _stream(self.device)), "kivi_store_flush_chunks")
+        self.n_chunks += n_chunks
 
     def residual(self):
         """The residual window in token order (a copy when it wraps)."""

@@ -73,6 +73,37 @@ def oracle_history(k, v, n_chunks, G, Gv):
     return np.concatenate(ks, axis=2), np.concatenate(vs, axis=2)
 
 
+def _u32(t):
+    return t.detach().cpu().numpy().view(np.uint32)
+
+
+def check_store_bit_exact(st, k, v):
+    """Every flushed chunk of store ``st`` (codes through the documented byte
+    transposes, scales, zeros and, if kept, the dequantised history) equals
+    the oracle's quantisation of tokens [c*G, (c+1)*G) of ``k``/``v``
+    ([B,H,T,D] fp32, CPU), and the residual window holds the tokens after
+    the last chunk."""
+    G, Gv = st.G, st.Gv
+    for c in range(st.n_chunks):
+        o = oracle_chunk(k[:, :, c * G:(c + 1) * G], v[:, :, c * G:(c + 1) * G], G, Gv)
+        assert np.array_equal(st.unpermuted_k_codes(c).cpu().numpy(), o["k_codes"]), \
+            f"k codes chunk {c}"
+        assert np.array_equal(_u32(st.k_scale[:, :, c]), o["k_scale"].view(np.uint32))
+        assert np.array_equal(_u32(st.k_zero[:, :, c]), o["k_zero"].view(np.uint32))
+        assert np.array_equal(st.unpermuted_v_codes(c).cpu().numpy(), o["v_codes"]), \
+            f"v codes chunk {c}"
+        assert np.array_equal(_u32(st.chunk_v_scale(c).contiguous()), o["v_scale"].view(np.uint32))
+        assert np.array_equal(_u32(st.chunk_v_zero(c).contiguous()), o["v_zero"].view(np.uint32))
+        if st.k_hist is not None:
+            kh = st.k_hist[:, :, c * G:(c + 1) * G]
+            vh = st.v_hist[:, :, c * G:(c + 1) * G]
+            assert np.array_equal(_u32(kh), o["k_deq"].view(np.uint32)), f"k history chunk {c}"
+            assert np.array_equal(_u32(vh), o["v_deq"].view(np.uint32)), f"v history chunk {c}"
+    rk, rv = st.residual()
+    q0 = st.n_chunks * G
+    assert torch.equal(rk.cpu(), k[:, :, q0:]) and torch.equal(rv.cpu(), v[:, :, q0:])
+
+
 def rel_err(out, ref):
     """max |out - ref| / max |ref| per (b, head) row, worst row."""
     out = np.asarray(out, np.float64)

@@ -12,8 +12,8 @@ import pytest
 import torch
 
 from oracle.attention import decode_attention
-from tests.kv_helpers import (fill_store, make_kv, oracle_chunk, oracle_history, rel_err,
-                              seeded_q)
+from tests.kv_helpers import (check_store_bit_exact, fill_store, make_kv, oracle_history,
+                              rel_err, seeded_q)
 
 pytestmark = pytest.mark.gpu
 
@@ -24,10 +24,6 @@ ATTN_TOL = 1e-3
 def store_cls(hip_device):
     from intel_kivi_hybrid_amd.store import PackedKVStore
     return PackedKVStore
-
-
-def _u32(t):
-    return t.detach().cpu().numpy().view(np.uint32)
 
 
 @pytest.mark.parametrize("B,H,D,G,Gv,R,T", [
@@ -43,23 +39,7 @@ def test_flush_bit_exact(store_cls, B, H, D, G, Gv, R, T):
     fill_store(st, k, v, R)
     n_flush = 0 if T < R else (T - R) // G + 1
     assert st.n_chunks == n_flush and st.res_len == T - n_flush * G
-    for c in range(st.n_chunks):
-        o = oracle_chunk(k[:, :, c * G:(c + 1) * G], v[:, :, c * G:(c + 1) * G], G, Gv)
-        assert np.array_equal(st.unpermuted_k_codes(c).cpu().numpy(), o["k_codes"]), \
-            f"k codes chunk {c}"
-        assert np.array_equal(_u32(st.k_scale[:, :, c]), o["k_scale"].view(np.uint32))
-        assert np.array_equal(_u32(st.k_zero[:, :, c]), o["k_zero"].view(np.uint32))
-        assert np.array_equal(st.unpermuted_v_codes(c).cpu().numpy(), o["v_codes"]), \
-            f"v codes chunk {c}"
-        assert np.array_equal(_u32(st.chunk_v_scale(c).contiguous()), o["v_scale"].view(np.uint32))
-        assert np.array_equal(_u32(st.chunk_v_zero(c).contiguous()), o["v_zero"].view(np.uint32))
-        kh = st.k_hist[:, :, c * G:(c + 1) * G]
-        vh = st.v_hist[:, :, c * G:(c + 1) * G]
-        assert np.array_equal(_u32(kh), o["k_deq"].view(np.uint32)), f"k history chunk {c}"
-        assert np.array_equal(_u32(vh), o["v_deq"].view(np.uint32)), f"v history chunk {c}"
-    rk, rv = st.residual()
-    q0 = st.n_chunks * G
-    assert torch.equal(rk.cpu(), k[:, :, q0:]) and torch.equal(rv.cpu(), v[:, :, q0:])
+    check_store_bit_exact(st, k, v)
 
 
 def _attention_case(store_cls, B, Hq, Hkv, D, G, Gv, R, T, splits=0, seed=0):
