@@ -43,11 +43,15 @@ from ..extension.loader import kivi_native  # noqa: F401  (fails loudly without 
 from ..store import PackedKVStore
 from .manager import _resolve_device
 
-__all__ = ["KIVI_ATTENTION", "KiviPackedCache", "kivi_packed_attention_forward",
-           "packed_attention", "register_packed_attention"]
+__all__ = ["KIVI_ATTENTION", "FORMAT_NAME", "FORMAT_VERSION", "KiviPackedCache",
+           "kivi_packed_attention_forward", "packed_attention", "register_packed_attention"]
 
 #: Name of the attention implementation that consumes a KiviPackedCache.
 KIVI_ATTENTION = "kivi_packed"
+
+#: safetensors metadata tags of a saved KiviPackedCache.
+FORMAT_NAME = "kivi-packed-kv"
+FORMAT_VERSION = 1
 
 # The store class the layers allocate (a seam for host-only tests of the
 # cache's control flow).
@@ -285,6 +289,74 @@ class KiviPackedCache(Cache):
                 "residual_tokens": st.res_len, "kivi_bytes": kivi, "fp32_bytes": fp32,
                 "compression": fp32 / kivi if kivi > 0 else 0, "bytes": b,
                 "allocated_bytes": st.allocated_bytes()}
+
+    # ----------------------------------------------------------- format
+    def save(self, path: str) -> None:
+        """Write the cache to a safetensors file.
+
+        Per fed layer i, tensors ``layers.{i}.k_codes`` ``[B, Hkv, D, T/4]``
+        u8, ``k_scale``/``k_zero`` ``[B, Hkv, D, T/G]``, ``v_codes``
+        ``[B, Hkv, T, D/4]`` u8, ``v_scale``/``v_zero`` ``[B, Hkv, T, D/Gv]``
+        (the layouts of the reference's quantize_keys / quantize_values over
+        the T quantised tokens, kv_cache_ops.cpp:179-199) and the fp32
+        residual windows ``k_residual``/``v_residual`` ``[B, Hkv, r, D]``;
+        the file metadata holds the format tag, version, cache geometry and
+        per-layer flush counts."""
+        from safetensors.torch import save_file
+        meta = {"format": FORMAT_NAME, "version": str(FORMAT_VERSION),
+                "num_layers": str(self.num_layers), "head_dim": str(self.head_dim),
+                "num_kv_heads": str(self.num_kv_heads or 0), "group_size": str(self.G),
+                "value_group_size": str(self.Gv), "residual_length": str(self.R)}
+        tensors = {}
+        for i, lay in enumerate(self.layers):
+            st = self.store(i)
+            if st is None:
+                continue
+            for name, t in st.export_state().items():
+                tensors[f"layers.{i}.{name}"] = t.contiguous().cpu()
+            meta[f"layers.{i}.flushes"] = str(lay.flushes)
+        save_file(tensors, path, metadata=meta)
+
+    @classmethod
+    def load(cls, path: str, device: str = "cuda") -> "KiviPackedCache":
+        """Read a file written by :meth:`save` into a new cache on ``device``;
+        the codes are re-ordered into this build's store layout."""
+        from safetensors import safe_open
+        with safe_open(path, framework="pt") as f:
+            meta = f.metadata() or {}
+            if meta.get("format") != FORMAT_NAME:
+                raise ValueError(f"{path} is not a KiviPackedCache file "
+                                 f"(format tag {meta.get('format')!r})")
+            if meta.get("version") != str(FORMAT_VERSION):
+                raise ValueError(f"{path} has format version {meta.get('version')!r}; this "
+                                 f"build reads version {FORMAT_VERSION}")
+            try:
+                geo = {k: int(meta[k]) for k in ("num_layers", "head_dim", "num_kv_heads",
+                                                 "group_size", "value_group_size",
+                                                 "residual_length")}
+            except (KeyError, ValueError) as exc:
+                raise ValueError(f"{path} has incomplete cache metadata: {exc}") from exc
+            cache = cls(geo["num_layers"], geo["head_dim"], geo["num_kv_heads"] or None,
+                        device=device, group_size=geo["group_size"],
+                        residual_length=geo["residual_length"],
+                        value_group_size=geo["value_group_size"])
+            keys = list(f.keys())
+            for i, lay in enumerate(cache.layers):
+                prefix = f"layers.{i}."
+                names = [k for k in keys if k.startswith(prefix)]
+                if not names:
+                    continue
+                state = {k[len(prefix):]: f.get_tensor(k) for k in names}
+                lay.store = _STORE_CLASS.from_state(state, cache.G, cache.R, cache.device,
+                                                    group_size_v=cache.Gv)
+                lay.flushes = int(meta.get(prefix + "flushes", "0"))
+                lay.dtype, lay.device = torch.float32, cache.device
+                lay.is_initialized = True
+            stray = [k for k in keys if not k.startswith("layers.")
+                     or int(k.split(".")[1]) >= cache.num_layers]
+            if stray:
+                raise ValueError(f"{path} holds tensors outside the cache's layers: {stray[:4]}")
+        return cache
 
     def __repr__(self):
         return (f"KiviPackedCache(layers={self.num_layers}, head_dim={self.head_dim}, "

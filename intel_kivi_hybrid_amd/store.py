@@ -77,6 +77,46 @@ def _mfma_maps(G: int, D: int, key: bool):
     return _MAPS[cache_key]
 
 
+def _unpack_last(packed: torch.Tensor) -> torch.Tensor:
+    """[..., N/4] bytes -> [..., N] codes (uint8), element 4j+k from bits 2k of byte j."""
+    b = packed.to(torch.int32)
+    c = torch.stack([(b >> (2 * k)) & 3 for k in range(4)], dim=-1)
+    return c.reshape(*packed.shape[:-1], packed.shape[-1] * 4).to(torch.uint8)
+
+
+def decode_codes(raw: torch.Tensor, G: int, D: int, layout: int, key: bool) -> torch.Tensor:
+    """Chunk code bytes in the store's order (``raw [..., G*D/4]``) -> one
+    code per byte as ``[..., G, D]`` (token, channel)."""
+    lead = raw.shape[:-1]
+    if layout == 0:
+        c = _unpack_last(raw)
+        if key:                                        # [G][D/4], channels packed
+            return c.reshape(*lead, G, D)
+        return c.reshape(*lead, D, G).transpose(-1, -2).contiguous()   # [D][G/4]
+    words = raw.contiguous().view(torch.int32).reshape(*lead, -1)        # [..., 64*NP]
+    flat, shifts = _mfma_maps(G, D, key)
+    vals = (words[..., :, None] >> shifts.to(raw.device)) & 3          # [..., 64*NP, 16]
+    out = torch.empty(*lead, G * D, dtype=torch.int32, device=raw.device)
+    out[..., flat.to(raw.device)] = vals.reshape(*lead, -1)
+    return out.reshape(*lead, G, D).to(torch.uint8)
+
+
+def encode_codes(codes: torch.Tensor, G: int, D: int, layout: int, key: bool) -> torch.Tensor:
+    """Inverse of :func:`decode_codes`: ``codes [..., G, D]`` (values 0..3) ->
+    chunk code bytes ``[..., G*D/4]`` in the store's order."""
+    lead = codes.shape[:-2]
+    if layout == 0:
+        if key:
+            return _pack_last(codes).reshape(*lead, G * D // 4)
+        return _pack_last(codes.transpose(-1, -2)).reshape(*lead, G * D // 4)
+    flat, shifts = _mfma_maps(G, D, key)
+    c = codes.reshape(*lead, G * D).to(torch.int64)[..., flat.to(codes.device)]
+    c = c.reshape(*lead, -1, 16) << shifts.to(codes.device, torch.int64)
+    words = c.sum(dim=-1)                                                # [..., 64*NP]
+    b = torch.stack([(words >> (8 * k)) & 0xFF for k in range(4)], dim=-1)
+    return b.to(torch.uint8).reshape(*lead, G * D // 4)
+
+
 class PackedKVStore:
     """Residual ring + packed chunks for one layer (all on ``device``)."""
 
@@ -271,20 +311,8 @@ class PackedKVStore:
     # ---------------------------------------------------------- inspection
     def _codes(self, which: str, chunk: int) -> torch.Tensor:
         """One chunk's 2-bit codes, one byte per element, as [B, Hkv, G, D]."""
-        B, H, G, D = self.B, self.H, self.G, self.D
-        raw = getattr(self, which)[:, :, chunk]
-        if self.code_layout == 0:
-            b = raw.reshape(B, H, -1).to(torch.int32)
-            c = torch.stack([(b >> (2 * k)) & 3 for k in range(4)], dim=-1).reshape(B, H, -1)
-            if which == "k_codes":
-                return c.reshape(B, H, G, D).to(torch.uint8)
-            return c.reshape(B, H, D, G).transpose(2, 3).contiguous().to(torch.uint8)
-        words = raw.contiguous().view(torch.int32).reshape(B, H, -1)     # [B, H, 64*NP]
-        flat, shifts = _mfma_maps(G, D, which == "k_codes")
-        vals = (words[..., :, None] >> shifts.to(raw.device)) & 3        # [B, H, 64*NP, 16]
-        out = torch.empty(B, H, G * D, dtype=torch.int32, device=raw.device)
-        out[..., flat.to(raw.device)] = vals.reshape(B, H, -1)
-        return out.reshape(B, H, G, D).to(torch.uint8)
+        return decode_codes(getattr(self, which)[:, :, chunk], self.G, self.D, self.code_layout,
+                            which == "k_codes")
 
     def unpermuted_k_codes(self, chunk: int) -> torch.Tensor:
         """Key codes of one chunk as ``[B, Hkv, G, D/4]`` bytes: byte (t, i)
@@ -302,6 +330,92 @@ class PackedKVStore:
 
     def chunk_v_zero(self, chunk: int) -> torch.Tensor:
         return self.v_zero[:, :, chunk].transpose(2, 3)
+
+    # ------------------------------------------------------------ format
+    def export_state(self) -> dict:
+        """The store's contents as tensors in the reference's own layouts
+        (those of ``quantize_keys`` / ``quantize_values`` over the whole
+        quantised history, kv_cache_ops.cpp:179-199), on the store's device:
+
+        * ``k_codes [B, Hkv, D, T/4]`` u8, ``k_scale``/``k_zero [B, Hkv, D, T/G]``
+          -- keys per channel, groups of G along the T quantised tokens;
+        * ``v_codes [B, Hkv, T, D/4]`` u8, ``v_scale``/``v_zero [B, Hkv, T, D/Gv]``
+          -- values per token, groups of Gv channels;
+        * ``k_residual``/``v_residual [B, Hkv, r, D]`` fp32, the residual
+          window in token order.
+
+        ``_C.dequantize_keys``/``dequantize_values`` (or the reference's
+        own ops) turn the codes back into the served history."""
+        B, H, D, G, n = self.B, self.H, self.D, self.G, self.n_chunks
+        ng = D // self.Gv
+        kc = decode_codes(self.k_codes[:, :, :n], G, D, self.code_layout, True)    # [B,H,n,G,D]
+        vc = decode_codes(self.v_codes[:, :, :n], G, D, self.code_layout, False)
+        kr, vr = self.residual()
+        return {
+            "k_codes": _pack_last(kc.permute(0, 1, 4, 2, 3).reshape(B, H, D, n * G)),
+            "k_scale": self.k_scale[:, :, :n].permute(0, 1, 3, 2).contiguous(),
+            "k_zero": self.k_zero[:, :, :n].permute(0, 1, 3, 2).contiguous(),
+            "v_codes": _pack_last(vc.reshape(B, H, n * G, D)),
+            "v_scale": self.v_scale[:, :, :n].permute(0, 1, 2, 4, 3).reshape(B, H, n * G, ng)
+                           .contiguous(),
+            "v_zero": self.v_zero[:, :, :n].permute(0, 1, 2, 4, 3).reshape(B, H, n * G, ng)
+                          .contiguous(),
+            "k_residual": kr.contiguous(),
+            "v_residual": vr.contiguous(),
+        }
+
+    @classmethod
+    def from_state(cls, state: dict, group_size: int, residual_capacity: int, device,
+                   group_size_v: Optional[int] = None, chunk_capacity: int = 0) -> "PackedKVStore":
+        """A store holding what :meth:`export_state` returned (tensors on any
+        device); codes are re-ordered into this build's code layout."""
+        need = ("k_codes", "k_scale", "k_zero", "v_codes", "v_scale", "v_zero",
+                "k_residual", "v_residual")
+        missing = [k for k in need if k not in state]
+        if missing:
+            raise ValueError(f"packed-store state lacks {missing}")
+        G = int(group_size)
+        ks = state["k_scale"]
+        if ks.dim() != 4:
+            raise ValueError(f"k_scale must be [B, Hkv, D, T/G], got {tuple(ks.shape)}")
+        B, H, D, n = ks.shape
+        gv = G if group_size_v is None else int(group_size_v)
+        T = n * G
+        ng = D // gv if gv > 0 and D % gv == 0 else -1
+        expect = {
+            "k_codes": ((B, H, D, T // 4), torch.uint8), "k_zero": ((B, H, D, n), torch.float32),
+            "k_scale": ((B, H, D, n), torch.float32), "v_codes": ((B, H, T, D // 4), torch.uint8),
+            "v_scale": ((B, H, T, ng), torch.float32), "v_zero": ((B, H, T, ng), torch.float32),
+        }
+        for name, (shape, dtype) in expect.items():
+            t = state[name]
+            if tuple(t.shape) != shape or t.dtype != dtype:
+                raise ValueError(f"{name} must be {dtype} {shape} for G={G}, Gv={gv}, got "
+                                 f"{t.dtype} {tuple(t.shape)}")
+        kr, vr = state["k_residual"], state["v_residual"]
+        if kr.dim() != 4 or tuple(kr.shape[:2]) != (B, H) or kr.shape[3] != D or \
+                kr.shape != vr.shape or kr.dtype != torch.float32 or vr.dtype != torch.float32:
+            raise ValueError(f"residuals must be fp32 [B={B}, Hkv={H}, r, D={D}], got "
+                             f"{tuple(kr.shape)} and {tuple(vr.shape)}")
+        if kr.shape[2] > residual_capacity:
+            raise ValueError(f"residual of {kr.shape[2]} tokens exceeds capacity "
+                             f"{residual_capacity}")
+        st = cls(B, H, D, G, residual_capacity, device, group_size_v=gv,
+                 chunk_capacity=max(n, int(chunk_capacity)))
+        dev = st.device
+        if n:
+            kc = _unpack_last(state["k_codes"].to(dev)).reshape(B, H, D, n, G).permute(0, 1, 3, 4, 2)
+            st.k_codes[:, :, :n] = encode_codes(kc, G, D, st.code_layout, True)
+            st.k_scale[:, :, :n] = state["k_scale"].to(dev).permute(0, 1, 3, 2)
+            st.k_zero[:, :, :n] = state["k_zero"].to(dev).permute(0, 1, 3, 2)
+            vc = _unpack_last(state["v_codes"].to(dev)).reshape(B, H, n, G, D)
+            st.v_codes[:, :, :n] = encode_codes(vc, G, D, st.code_layout, False)
+            st.v_scale[:, :, :n] = state["v_scale"].to(dev).reshape(B, H, n, G, ng).permute(0, 1, 2, 4, 3)
+            st.v_zero[:, :, :n] = state["v_zero"].to(dev).reshape(B, H, n, G, ng).permute(0, 1, 2, 4, 3)
+        st.n_chunks = n
+        if kr.shape[2]:
+            st.append(kr.to(dev), vr.to(dev))
+        return st
 
     # ------------------------------------------------------------ attention
     def workspace_bytes(self, q_heads: int, num_splits: int = 0) -> int:
