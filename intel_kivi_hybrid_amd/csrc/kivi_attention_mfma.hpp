@@ -226,11 +226,14 @@ struct Shape {
     static constexpr int WA_ROW = D + 16;            // bf16 per key A row
     static constexpr int BA_ROW = 32 * NBB + 16;     // bf16 per correction A row
     static constexpr int PA_ROW = G + 16;            // bf16 per value A row
-    static constexpr int PA_MAT = 16 * PA_ROW;       // bf16 per value A matrix (one group)
+    // A operands have 16 rows, of which only 2*HG (hi / lo per head) carry
+    // data: the rest are stored once, as one zero row that those lanes read.
+    static constexpr int AROWS = 2 * HG < 16 ? 2 * HG + 1 : 16;
+    static constexpr int PA_MAT = AROWS * PA_ROW;    // bf16 per value A matrix (one group)
     static constexpr int PL_ROW = G + 8;             // floats per probability row
     static constexpr int OFF_WA = 0;
-    static constexpr int OFF_BA = OFF_WA + 16 * WA_ROW * 2;
-    static constexpr int OFF_PA = OFF_BA + 16 * BA_ROW * 2;
+    static constexpr int OFF_BA = OFF_WA + AROWS * WA_ROW * 2;
+    static constexpr int OFF_PA = OFF_BA + AROWS * BA_ROW * 2;
     // The rest depends on the number of value groups NG = D / Gv.
     __host__ __device__ static constexpr int off_pl(int NG) { return OFF_PA + NG * PA_MAT * 2; }
     __host__ __device__ static constexpr int off_al(int NG) { return off_pl(NG) + 2 * HG * PL_ROW * 4; }
@@ -255,11 +258,15 @@ struct Shape {
     // chunk loop
     static constexpr int RSTATE = HG * D + 2 * HG;
     static constexpr int MERGE_LDS = kWaves * RSTATE * 4;
-    // residual region: scaled q [HG][D], per-wave probabilities [HG][16] and
-    // the combined state of the workgroup's residual slices
-    static constexpr int RES_LDS = HG * D * 4 + kWaves * HG * kResPass * 4 + RSTATE * 4;
+    // residual pass: scaled q [HG][D] and per-wave probabilities [HG][16].
+    // They are live only before the chunk loop, so they sit in the per-wave
+    // regions, past the merge slots that the residual pass writes.
+    static constexpr int QRES_LDS = HG * D * 4 + kWaves * HG * kResPass * 4;
+    static constexpr int SHARED_LDS = MERGE_LDS + QRES_LDS;
+    // the combined state of the workgroup's residual slices, kept to the end
+    static constexpr int RES_LDS = RSTATE * 4;
     __host__ __device__ static constexpr int lds(int NG) {
-        return (kWaves * wave_lds(NG) > MERGE_LDS ? kWaves * wave_lds(NG) : MERGE_LDS) + RES_LDS;
+        return (kWaves * wave_lds(NG) > SHARED_LDS ? kWaves * wave_lds(NG) : SHARED_LDS) + RES_LDS;
     }
     static_assert(NP >= 1 && LPH * CPL == D && CPL % 2 == 0, "shape");
 };
@@ -433,10 +440,10 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     const int meta_floats = S::meta_floats(NG);
     const int meta_stride = S::meta_stride(NG);
 
-    // Residual region: scaled q of the group, per-wave probabilities and the
-    // combined residual state.
-    float* qres = reinterpret_cast<float*>(smem + S::lds(NG) - S::RES_LDS);   // [HG][D]
-    float* rstate = qres + HG * D + kWaves * HG * kResPass;
+    // Residual pass buffers (scaled q of the group, per-wave probabilities)
+    // after the merge slots, and the combined residual state at the end.
+    float* qres = reinterpret_cast<float*>(smem + S::MERGE_LDS);                // [HG][D]
+    float* rstate = reinterpret_cast<float*>(smem + S::lds(NG) - S::RES_LDS);
     for (int e = threadIdx.x; e < HG * D; e += kBlock)
         qres[e] = a.q[((int64_t)b * a.Hq + kvh * HG) * D + e] * a.qscale;
     __syncthreads();
@@ -463,6 +470,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
 #pragma unroll
     for (int i = 0; i < S::NBV; ++i) O[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const int gq = lane / 16, col = lane % 16;
+    const int arow = col < 2 * HG ? col : 2 * HG;     // A-operand row this lane reads
     float m_run[2] = {-INFINITY, -INFINITY}, l_part[2] = {0.f, 0.f};
     float m_thr[2] = {-INFINITY, -INFINITY};     // m_run + kRescaleThreshold
     const bool hvalid[2] = {2 * gq < HG, 2 * gq + 1 < HG};
@@ -544,10 +552,10 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         bf16x8_t Aw[S::KS], Ab[S::NBB];
 #pragma unroll
         for (int ks = 0; ks < S::KS; ++ks)
-            Aw[ks] = *reinterpret_cast<const bf16x8_t*>(WA + col * S::WA_ROW + 32 * ks + 8 * gq);
+            Aw[ks] = *reinterpret_cast<const bf16x8_t*>(WA + arow * S::WA_ROW + 32 * ks + 8 * gq);
 #pragma unroll
         for (int kb = 0; kb < S::NBB; ++kb)
-            Ab[kb] = *reinterpret_cast<const bf16x8_t*>(BA + col * S::BA_ROW + 32 * kb + 8 * gq);
+            Ab[kb] = *reinterpret_cast<const bf16x8_t*>(BA + arow * S::BA_ROW + 32 * kb + 8 * gq);
         // The correction is the same for every token: one accumulator, shared
         // as the starting value of every n-block's chain.
         f32x4_t s0 = {0.f, 0.f, 0.f, 0.f};
@@ -688,7 +696,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             for (int nb = 0; nb < S::NBV; ++nb) {
                 const int g = (16 * nb) / Gv;
                 if (g != g_loaded) {
-                    Ap = *reinterpret_cast<const bf16x8_t*>(PA + g * S::PA_MAT + col * S::PA_ROW +
+                    Ap = *reinterpret_cast<const bf16x8_t*>(PA + g * S::PA_MAT + arow * S::PA_ROW +
                                                             32 * kt + 8 * gq);
                     g_loaded = g;
                 }
@@ -833,7 +841,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     }
     combine_residual<HG, D>(smem, rstate);
 
-    // Zero the A operands once: rows >= 2*HG and correction columns >= LPH
+    // Zero the A operands once: the zero row and correction columns >= LPH
     // are never written and must read as 0.
     for (int e = lane; e < S::off_pl(NG) / 4; e += kWave) reinterpret_cast<uint32_t*>(wl)[e] = 0u;
 
