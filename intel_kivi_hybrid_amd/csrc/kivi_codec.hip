@@ -24,6 +24,7 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kUnroll = 4;
+constexpr int kQuantVPL = 2;        // float4s per thread in quantize_vec_kernel
 
 __device__ __forceinline__ void min_max4(const float4& v, float& mn, float& mx) {
     mn = fmin_nan(fmin_nan(v.x, v.y), fmin_nan(v.z, v.w));
@@ -60,6 +61,48 @@ __global__ __launch_bounds__(kBlock) void quantize_seg_kernel(
                 zeros[idx / LANES] = mn;
             }
         }
+    }
+}
+
+// Segment kernels: thread t owns VPL consecutive float4s (a "segment") of a
+// group, LANES = G/(4*VPL) adjacent lanes per group.  Larger segments mean
+// fewer cross-lane reduction steps and fewer scale divisions per element;
+// each load instruction then reads 16 bytes per lane at a VPL*16-byte stride.
+template <int LANES, int VPL>
+__global__ __launch_bounds__(kBlock) void quantize_vec_kernel(
+    const float4* __restrict__ in, uint8_t* __restrict__ packed,
+    float* __restrict__ scales, float* __restrict__ zeros, int64_t n_seg) {
+    const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (t >= n_seg) return;              // groups are whole: n_seg % LANES == 0
+    float4 v[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) v[j] = in[t * VPL + j];
+    float mn, mx, scale;
+    min_max4(v[0], mn, mx);
+#pragma unroll
+    for (int j = 1; j < VPL; ++j) {
+        float a, b;
+        min_max4(v[j], a, b);
+        mn = fmin_nan(mn, a);
+        mx = fmax_nan(mx, b);
+    }
+    seg_min_max<LANES>(mn, mx);
+    finish_group(mn, mx, scale);
+    uint32_t bytes[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) bytes[j] = encode4(v[j].x, v[j].y, v[j].z, v[j].w, mn, scale);
+    if constexpr (VPL % 4 == 0) {
+#pragma unroll
+        for (int j = 0; j < VPL; j += 4)
+            reinterpret_cast<uint32_t*>(packed + t * VPL)[j / 4] =
+                bytes[j] | (bytes[j + 1] << 8) | (bytes[j + 2] << 16) | (bytes[j + 3] << 24);
+    } else {
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) packed[t * VPL + j] = (uint8_t)bytes[j];
+    }
+    if ((threadIdx.x & (LANES - 1)) == 0) {
+        scales[t / LANES] = scale;
+        zeros[t / LANES] = mn;
     }
 }
 
@@ -201,7 +244,17 @@ int launch_quantize_groups(const float* in, uint8_t* packed, float* scales, floa
     const int lanes = G / 4;
     const int64_t n_vec = n_groups * lanes;
     const bool pow2 = (lanes & (lanes - 1)) == 0 && lanes <= kWave;
-    if (pow2 && aligned16(in)) {
+    if (pow2 && aligned16(in) && lanes >= kQuantVPL && kQuantVPL > 1 &&
+        ((uintptr_t)packed % (kQuantVPL >= 4 ? 4 : 1)) == 0) {
+        const int64_t n_seg = n_vec / kQuantVPL;
+        const unsigned grid = grid_for(n_seg, kBlock);
+        const float4* in4 = reinterpret_cast<const float4*>(in);
+        switch (lanes / kQuantVPL) {
+#define KIVI_QV(L) case L: quantize_vec_kernel<L, kQuantVPL><<<grid, kBlock, 0, stream>>>(in4, packed, scales, zeros, n_seg); break;
+            KIVI_QV(1) KIVI_QV(2) KIVI_QV(4) KIVI_QV(8) KIVI_QV(16) KIVI_QV(32) KIVI_QV(64)
+#undef KIVI_QV
+        }
+    } else if (pow2 && aligned16(in)) {
         const unsigned grid = grid_for(n_vec, kBlock * kUnroll);
         const float4* in4 = reinterpret_cast<const float4*>(in);
         switch (lanes) {
