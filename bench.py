@@ -347,6 +347,11 @@ def main():
         for name, r in prefill_bench(dev).items():
             log(f"[bench] prefill flush ({name}): {r}")
         return
+    if args.only == "quantize":
+        qb = quantize_bench(dev)
+        log(f"[bench] config2 quantize K+V: {qb['us_per_pair']:.1f} us, {qb['gbs']:.0f} GB/s, "
+            f"{qb['mtokens_s']:.1f} Mtokens/s")
+        return
 
     # ---- config 4: the headline decode loop -------------------------------
     B, Hq, Hkv, D, T, R, G = 64, 32, 8, 128, 8192, 128, 32
@@ -389,8 +394,6 @@ def main():
     qb = quantize_bench(dev)
     log(f"[bench] config2 quantize K+V: {qb['us_per_pair']:.1f} us, {qb['gbs']:.0f} GB/s, "
         f"{qb['mtokens_s']:.1f} Mtokens/s")
-    if args.only == "quantize":
-        return
     if args.only is None:
         pf = prefill_bench(dev)
         for name, r in pf.items():
