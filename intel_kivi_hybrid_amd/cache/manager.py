@@ -119,6 +119,11 @@ class KiviCache:
         self._fed: List[bool] = [False] * num_layers
         self._stores: List[Optional[PackedKVStore]] = [None] * num_layers
         self._serve_device: List[Optional[torch.device]] = [None] * num_layers
+        # Served tensors take the dtype of the model's own K/V: fp32 for the
+        # fp32 models the reference runs (identical to its .float() cache), and
+        # bf16/fp16 for half-precision models, whose attention cannot take an
+        # fp32 cache (the store itself is fp32 either way).
+        self._serve_dtype: List[Optional[torch.dtype]] = [None] * num_layers
 
         # The DynamicCache handed out by get_full_cache(); valid while the
         # model grows that same object in place and no flush has happened.
@@ -186,6 +191,8 @@ class KiviCache:
 
             store = self._store_for(i, k.shape[0], k.shape[1], new_k.shape[2])
             self._serve_device[i] = k.device
+            self._serve_dtype[i] = k.dtype if k.dtype in (torch.bfloat16, torch.float16) \
+                else torch.float32
             # fp32, bf16 and fp16 K/V are read as they are (widening to fp32
             # is exact, as the reference's .float() is, manager.py:210-214).
             flushes = store.extend(new_k, new_v, flush_at=self.R)
@@ -196,7 +203,9 @@ class KiviCache:
     def get_full_cache(self) -> DynamicCache:
         """The cache to pass as ``past_key_values`` to the next forward pass
         (manager.py:251-290): per layer, the dequantised history followed by
-        the fp32 residual window, as fp32 tensors on the model's device."""
+        the fp32 residual window, on the model's device -- fp32 as in the
+        reference, or the model's own bf16/fp16 dtype for half-precision
+        models."""
         if self._cache_view is not None and self._cache_view_valid:
             return self._cache_view
         full = []
@@ -219,6 +228,7 @@ class KiviCache:
             self._flush_count[i] = 0
             self._fed[i] = False
             self._serve_device[i] = None
+            self._serve_dtype[i] = None
             if self._stores[i] is not None:
                 self._stores[i].reset()
         self.batch_size = None
@@ -276,7 +286,8 @@ class KiviCache:
                 k, v = k.clone(), v.clone()
         else:
             k, v = torch.cat(parts_k, dim=2), torch.cat(parts_v, dim=2)
-        return k.to(dev), v.to(dev)
+        dt = self._serve_dtype[i] or torch.float32
+        return k.to(dev, dt), v.to(dev, dt)
 
     # ------------------------------------------------------------ stats / debug
     @property

@@ -110,8 +110,9 @@ def test_hf_generate_with_packed_cache(hip_device):
 def test_gqa_llama_packed_vs_served(hip_device, dtype):
     """Grouped-query Llama (8 query heads over 2 kv heads, D=128), model on
     the GPU: packed vs served cache pick the same tokens in fp32.  In bf16
-    (which the reference's fp32 served cache cannot feed) the packed path
-    runs end to end; its agreement with the fp32 tokens is printed."""
+    (which the reference's fp32 served cache cannot feed) both paths run end
+    to end -- the served cache takes the model's dtype -- and their
+    agreement with the fp32 tokens is printed."""
     from transformers import LlamaConfig, LlamaForCausalLM
     torch.manual_seed(3)
     cfg = LlamaConfig(vocab_size=1024, hidden_size=1024, intermediate_size=2048,
@@ -132,9 +133,14 @@ def test_gqa_llama_packed_vs_served(hip_device, dtype):
         model = model.to(dtype)
         c = gen_mod.generate_packed(model, tok, prompt, max_new_tokens=120, group_size=32,
                                     residual_length=64, device="cuda:0").split()
+        d = gen_mod.generate(model, tok, prompt, max_new_tokens=120, group_size=32,
+                             residual_length=64, device="cuda:0").split()
         n, tot = _match(a, c)
-        print(f"[packed-gqa] bf16 vs fp32 token match {n}/{tot}", flush=True)
-        assert len(c) == len(a)
+        n2, _ = _match(a, d)
+        n3, _ = _match(c, d)
+        print(f"[packed-gqa] bf16 packed vs fp32 {n}/{tot}, bf16 served vs fp32 {n2}/{tot}, "
+              f"bf16 packed vs served {n3}/{tot}", flush=True)
+        assert len(c) == len(a) == len(d)
 
 
 def test_attention_output_matches_oracle(hip_device):
