@@ -148,6 +148,19 @@ int kivi_store_flush_chunks(const float* k_res, const float* v_res, const void* 
                             int32_t res_start, int32_t res_len, int32_t chunk_capacity,
                             int32_t chunk_index, int32_t n_chunks, void* stream);
 
+/* Append new_tokens tokens to the residual ring of every (b, kv-head): token
+ * t of k_new/v_new (element (b, h, t, d) at b*new_batch_stride +
+ * h*new_head_stride + t*new_token_stride + d, in elements of new_dtype: 0
+ * f32, 1 bf16, 2 f16, widened exactly) goes to ring slot
+ * (slot + t) % res_capacity.  K and V in one launch.  Replaces the residual
+ * append of KiviCache.add_tokens (manager.py:226-231, a torch.cat of the
+ * fp32 residual); the caller keeps the window's start and length. */
+int kivi_store_append(const void* k_new, const void* v_new, int32_t new_dtype,
+                      int64_t new_batch_stride, int64_t new_head_stride,
+                      int64_t new_token_stride, int32_t new_tokens, float* k_res, float* v_res,
+                      int32_t batch, int32_t kv_heads, int32_t head_dim, int32_t res_capacity,
+                      int32_t slot, void* stream);
+
 /* Code layout of a store with these shapes: 1 (matrix-core operand order)
  * when head_dim is 64, 128 or 256, group_size_k is 32 or 64 and
  * group_size_v is a multiple of 32 dividing head_dim; 0 (plain) otherwise.
@@ -184,6 +197,25 @@ int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const f
                                  int32_t num_chunks, int32_t res_capacity, int32_t res_start,
                                  int32_t res_len, float softmax_scale, int32_t num_splits,
                                  void* stream);
+
+/* kivi_packed_decode_attention with this step's new token appended in the
+ * same launch: the window (res_start, res_len) already counts the new token
+ * as its last (index res_len - 1, ring slot (res_start + res_len - 1) %
+ * res_capacity); the kernel reads it from k_new / v_new (fp32, element
+ * (b, h, d) at b*new_batch_stride + h*new_head_stride + d, rows 16-byte
+ * aligned) and writes it into that ring slot for later launches.  Same
+ * result as kivi_store_append followed by kivi_packed_decode_attention,
+ * without the separate launch.  Replaces the residual append of
+ * KiviCache.add_tokens (manager.py:226-231) together with the step's
+ * attention. */
+int kivi_packed_decode_attention_append(
+    const float* q, const float* k_new, const float* v_new, int64_t new_batch_stride,
+    int64_t new_head_stride, const uint8_t* k_codes, const float* k_scale, const float* k_zero,
+    const uint8_t* v_codes, const float* v_scale, const float* v_zero, float* k_res,
+    float* v_res, float* out, void* workspace, size_t workspace_bytes, int32_t batch,
+    int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t group_size_k,
+    int32_t group_size_v, int32_t chunk_capacity, int32_t num_chunks, int32_t res_capacity,
+    int32_t res_start, int32_t res_len, float softmax_scale, int32_t num_splits, void* stream);
 
 #ifdef __cplusplus
 }

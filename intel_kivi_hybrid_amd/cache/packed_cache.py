@@ -172,7 +172,7 @@ class KiviPackedLayer(CacheLayerMixin):
             self.flushes += st.extend(k, v, flush_at=self.owner.R)
             self._prompt = True
         elif n == 1:
-            st.append(k, v)          # room: settle() left res_len < R
+            st.stage_token(k, v)     # room: settle() left res_len < R; written by attend()
             self._prompt = False
             self._awaiting_attention = True
         else:

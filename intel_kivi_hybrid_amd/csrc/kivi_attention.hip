@@ -390,7 +390,7 @@ size_t kivi_packed_decode_attention_workspace_size(int32_t batch, int32_t q_head
     return (size_t)batch * q_heads * p.n_splits * (head_dim + 2) * sizeof(float);
 }
 
-int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const float* k_scale,
+static int decode_attention_impl(const float* q, const uint8_t* k_codes, const float* k_scale,
                                  const float* k_zero, const uint8_t* v_codes,
                                  const float* v_scale, const float* v_zero, const float* k_res,
                                  const float* v_res, float* out, void* workspace,
@@ -399,7 +399,8 @@ int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const f
                                  int32_t group_size_v, int32_t chunk_capacity,
                                  int32_t num_chunks, int32_t res_capacity, int32_t res_start,
                                  int32_t res_len, float softmax_scale, int32_t num_splits,
-                                 void* stream) {
+                                 const float* k_new, const float* v_new, int64_t new_sb,
+                                 int64_t new_sh, void* stream) {
     if (!q || !out)
         return set_error(kErrInvalidArgument, "null q/out pointer");
     if (batch <= 0 || kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads)
@@ -453,12 +454,20 @@ int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const f
         part_ml = part_o + (size_t)batch * q_heads * p.n_splits * head_dim;
     }
     hipStream_t st = (hipStream_t)stream;
+    const int new_slot = k_new ? (res_start + res_len - 1) % res_capacity : 0;
+    if (k_new && layout != kLayoutMfma) {
+        // the generic kernel reads the ring only: file the token there first
+        const int rc = kivi_store_append(k_new, v_new, 0, new_sb, new_sh, 0, 1,
+                                         const_cast<float*>(k_res), const_cast<float*>(v_res),
+                                         batch, kv_heads, head_dim, res_capacity, new_slot, stream);
+        if (rc) return rc;
+    }
     if (layout == kLayoutMfma) {
         AttnLaunch L{q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res, v_res, out,
                      part_o, part_ml, batch, q_heads, kv_heads, head_dim, group_size_k,
                      group_size_v, chunk_capacity, num_chunks, res_capacity, res_start, res_len,
                      p.n_qsplits, p.chunks_per_wave, p.res_per_wave, p.n_splits,
-                     softmax_scale * kLog2e};
+                     softmax_scale * kLog2e, k_new, v_new, new_sb, new_sh, new_slot};
         int rc = launch_attention_mfma(L, st);
         if (rc || !needs_workspace(p)) return rc;
     } else {
@@ -482,6 +491,49 @@ int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const f
                                                                   q_heads, head_dim,
                                                                   p.n_splits);
     return check_launch("packed_decode_attention_merge");
+}
+
+int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const float* k_scale,
+                                 const float* k_zero, const uint8_t* v_codes,
+                                 const float* v_scale, const float* v_zero, const float* k_res,
+                                 const float* v_res, float* out, void* workspace,
+                                 size_t workspace_bytes, int32_t batch, int32_t q_heads,
+                                 int32_t kv_heads, int32_t head_dim, int32_t group_size_k,
+                                 int32_t group_size_v, int32_t chunk_capacity,
+                                 int32_t num_chunks, int32_t res_capacity, int32_t res_start,
+                                 int32_t res_len, float softmax_scale, int32_t num_splits,
+                                 void* stream) {
+    return decode_attention_impl(q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
+                                 v_res, out, workspace, workspace_bytes, batch, q_heads,
+                                 kv_heads, head_dim, group_size_k, group_size_v, chunk_capacity,
+                                 num_chunks, res_capacity, res_start, res_len, softmax_scale,
+                                 num_splits, nullptr, nullptr, 0, 0, stream);
+}
+
+int kivi_packed_decode_attention_append(
+        const float* q, const float* k_new, const float* v_new, int64_t new_batch_stride,
+        int64_t new_head_stride, const uint8_t* k_codes, const float* k_scale,
+        const float* k_zero, const uint8_t* v_codes, const float* v_scale, const float* v_zero,
+        float* k_res, float* v_res, float* out, void* workspace, size_t workspace_bytes,
+        int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+        int32_t group_size_k, int32_t group_size_v, int32_t chunk_capacity, int32_t num_chunks,
+        int32_t res_capacity, int32_t res_start, int32_t res_len, float softmax_scale,
+        int32_t num_splits, void* stream) {
+    if (!k_new || !v_new)
+        return set_error(kErrInvalidArgument, "null new-token pointer");
+    if (!k_res || !v_res || res_len < 1)
+        return set_error(kErrInvalidArgument,
+                         "the window must hold the new token (res_len %d >= 1)", res_len);
+    if (new_batch_stride < 0 || new_head_stride < 0 || new_batch_stride % 4 ||
+        new_head_stride % 4 || (uintptr_t)k_new % 16 || (uintptr_t)v_new % 16)
+        return set_error(kErrInvalidArgument,
+                         "new-token rows must be 16-byte aligned (strides multiples of 4)");
+    return decode_attention_impl(q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
+                                 v_res, out, workspace, workspace_bytes, batch, q_heads,
+                                 kv_heads, head_dim, group_size_k, group_size_v, chunk_capacity,
+                                 num_chunks, res_capacity, res_start, res_len, softmax_scale,
+                                 num_splits, k_new, v_new, new_batch_stride, new_head_stride,
+                                 stream);
 }
 
 }  // extern "C"

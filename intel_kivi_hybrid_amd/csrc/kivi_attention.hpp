@@ -26,6 +26,14 @@ struct AttnLaunch {
     int res_per_wave;        // residual tokens per wave
     int n_splits;            // partial states per row (= n_qsplits)
     float qscale;            // softmax scale * log2(e)
+    // Optional new token, the window's last (index res_len - 1): when k_new
+    // is set the kernel reads that token from k_new / v_new (element
+    // (b, h, d) at b*new_sb + h*new_sh + d) and writes it to ring slot
+    // new_slot, so no separate append launch is needed.
+    const float* k_new = nullptr;
+    const float* v_new = nullptr;
+    int64_t new_sb = 0, new_sh = 0;
+    int new_slot = 0;
 };
 
 // Launches the matrix-core kernel (kLayoutMfma stores, Hq/Hkv in {1,2,4,8}).

@@ -446,6 +446,19 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     float* rstate = reinterpret_cast<float*>(smem + S::lds(NG) - S::RES_LDS);
     for (int e = threadIdx.x; e < HG * D; e += kBlock)
         qres[e] = a.q[((int64_t)b * a.Hq + kvh * HG) * D + e] * a.qscale;
+    // The new token (if any) is read from its own tensor by the residual
+    // pass below; one wave of the first split also files it in the ring for
+    // later launches.  Nothing in this launch reads that ring slot.
+    const float* knew_row = a.k_new ? a.k_new + b * a.new_sb + kvh * a.new_sh : nullptr;
+    const float* vnew_row = a.k_new ? a.v_new + b * a.new_sb + kvh * a.new_sh : nullptr;
+    if (knew_row && split == 0 && threadIdx.x < kWave) {
+        float* kdst = const_cast<float*>(a.k_res) + (bh * a.Rcap + a.new_slot) * D;
+        float* vdst = const_cast<float*>(a.v_res) + (bh * a.Rcap + a.new_slot) * D;
+        for (int e = threadIdx.x; e < D / 4; e += kWave) {
+            reinterpret_cast<float4*>(kdst)[e] = reinterpret_cast<const float4*>(knew_row)[e];
+            reinterpret_cast<float4*>(vdst)[e] = reinterpret_cast<const float4*>(vnew_row)[e];
+        }
+    }
     __syncthreads();
 
     // W-prep lane: head wh, channels [wseg*CPL, +CPL).
@@ -750,11 +763,12 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         for (int t0 = r0; t0 < r1; t0 += kResPass) {
             const int n = min(kResPass, r1 - t0);
             // scores
-            int slot = a.res_start + t0 + min(tk, n - 1);
+            const int ktok = t0 + min(tk, n - 1);          // index in the window
+            int slot = a.res_start + ktok;
             slot = slot >= a.Rcap ? slot - a.Rcap : slot;
             // lane (tk, qq) takes float4s qq, qq+4, ... of token tk's row
             const float4* krow = reinterpret_cast<const float4*>(
-                a.k_res + (bh * a.Rcap + slot) * D) + qq;
+                knew_row && ktok == a.res_len - 1 ? knew_row : a.k_res + (bh * a.Rcap + slot) * D) + qq;
             float4 kv[KQ];
 #pragma unroll
             for (int j = 0; j < KQ; ++j) kv[j] = krow[4 * j];
@@ -763,9 +777,11 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             float4 vv[kResPass / TS];
 #pragma unroll
             for (int j = 0; j < kResPass / TS; ++j) {
-                int vs = a.res_start + t0 + min(ts + TS * j, n - 1);
+                const int vtok = t0 + min(ts + TS * j, n - 1);
+                int vs = a.res_start + vtok;
                 vs = vs >= a.Rcap ? vs - a.Rcap : vs;
-                vv[j] = reinterpret_cast<const float4*>(a.v_res + (bh * a.Rcap + vs) * D)[c4];
+                vv[j] = reinterpret_cast<const float4*>(
+                    vnew_row && vtok == a.res_len - 1 ? vnew_row : a.v_res + (bh * a.Rcap + vs) * D)[c4];
             }
             float sres[HG];
 #pragma unroll

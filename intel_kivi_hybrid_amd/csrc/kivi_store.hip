@@ -627,6 +627,37 @@ void launch_flush(const FlushArgs& a, int src, dim3 grid, size_t lds, hipStream_
     }
 }
 
+// Residual append: token t of the new K/V goes to ring slot (slot + t) % Rcap
+// of every (b, kv-head), one float4 of channels per thread, K and V in the
+// same launch.
+struct AppendArgs {
+    const void* k_new;
+    const void* v_new;
+    int64_t sb, sh, st;            // element strides of the new tokens (channels contiguous)
+    float* k_res;                  // [B, H, Rcap, D]
+    float* v_res;
+    int64_t total;                 // B * H * n * D/4
+    int H, D, n, Rcap, slot;
+    bool vec;
+};
+
+template <int SRC>
+__global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.total) return;
+    const int d4n = a.D / 4;
+    const int d4 = (int)(i % d4n);
+    const int64_t r = i / d4n;
+    const int t = (int)(r % a.n);
+    const int64_t bh = r / a.n;
+    const int64_t off = (bh / a.H) * a.sb + (bh % a.H) * a.sh + (int64_t)t * a.st + 4 * d4;
+    int s = a.slot + t;
+    s = s >= a.Rcap ? s - a.Rcap : s;
+    const int64_t dst = (bh * a.Rcap + s) * a.D / 4 + d4;
+    reinterpret_cast<float4*>(a.k_res)[dst] = load4_new<SRC>(a.k_new, off, a.vec);
+    reinterpret_cast<float4*>(a.v_res)[dst] = load4_new<SRC>(a.v_new, off, a.vec);
+}
+
 }  // namespace
 }  // namespace kivi
 
@@ -747,4 +778,47 @@ extern "C" int kivi_store_flush(const float* k_res, const float* v_res, uint8_t*
                                    v_hist, hist_capacity, batch, kv_heads, head_dim,
                                    group_size_k, group_size_v, res_capacity, res_start,
                                    group_size_k, chunk_capacity, chunk_index, 1, stream);
+}
+
+extern "C" int kivi_store_append(const void* k_new, const void* v_new, int32_t new_dtype,
+                                 int64_t new_batch_stride, int64_t new_head_stride,
+                                 int64_t new_token_stride, int32_t new_tokens, float* k_res,
+                                 float* v_res, int32_t batch, int32_t kv_heads,
+                                 int32_t head_dim, int32_t res_capacity, int32_t slot,
+                                 void* stream) {
+    if (!k_new || !v_new || !k_res || !v_res)
+        return set_error(kErrInvalidArgument, "null tensor pointer");
+    if (batch <= 0 || kv_heads <= 0)
+        return set_error(kErrInvalidArgument, "batch and kv_heads must be positive");
+    if (head_dim <= 0 || head_dim % 4)
+        return set_error(kErrInvalidArgument, "head_dim must be positive and divisible by 4");
+    if (new_dtype < kSrcF32 || new_dtype > kSrcF16)
+        return set_error(kErrInvalidArgument, "new_dtype %d is not 0 (f32), 1 (bf16) or 2 (f16)",
+                         new_dtype);
+    if (new_batch_stride < 0 || new_head_stride < 0 || new_token_stride < 0)
+        return set_error(kErrInvalidArgument, "negative new-token strides");
+    if (res_capacity <= 0 || slot < 0 || slot >= res_capacity)
+        return set_error(kErrInvalidArgument, "slot %d outside [0, %d)", slot, res_capacity);
+    if (new_tokens < 0 || new_tokens > res_capacity)
+        return set_error(kErrInvalidArgument, "%d new tokens exceed the ring capacity %d",
+                         new_tokens, res_capacity);
+    if ((uintptr_t)k_res % 16 || (uintptr_t)v_res % 16)
+        return set_error(kErrInvalidArgument, "residual ring must be 16-byte aligned");
+    if (new_tokens == 0) return 0;
+    const int esize = new_dtype == kSrcF32 ? 4 : 2;
+    const int64_t vb = 4 * esize;
+    const bool vec = (uintptr_t)k_new % vb == 0 && (uintptr_t)v_new % vb == 0 &&
+                     (new_batch_stride * esize) % vb == 0 && (new_head_stride * esize) % vb == 0 &&
+                     (new_token_stride * esize) % vb == 0;
+    AppendArgs a{k_new, v_new, new_batch_stride, new_head_stride, new_token_stride, k_res, v_res,
+                 (int64_t)batch * kv_heads * new_tokens * (head_dim / 4), kv_heads, head_dim,
+                 new_tokens, res_capacity, slot, vec};
+    const unsigned grid = (unsigned)((a.total + 255) / 256);
+    hipStream_t st = (hipStream_t)stream;
+    switch (new_dtype) {
+        case kSrcBF16: append_kernel<kSrcBF16><<<grid, 256, 0, st>>>(a); break;
+        case kSrcF16: append_kernel<kSrcF16><<<grid, 256, 0, st>>>(a); break;
+        default: append_kernel<kSrcF32><<<grid, 256, 0, st>>>(a); break;
+    }
+    return check_launch("store_append");
 }

@@ -143,6 +143,10 @@ class PackedKVStore:
         self.res_len = 0
         self.n_chunks = 0
         self.capacity = 0
+        # A token counted in res_len whose K/V are not in the ring yet: the
+        # next attention launch writes it (fused), any other use of the ring
+        # commits it first.
+        self._pending = None
         self._alloc(max(int(chunk_capacity), 1))
 
     # ------------------------------------------------------------------ alloc
@@ -183,20 +187,54 @@ class PackedKVStore:
     def quantized_tokens(self) -> int:
         return self.n_chunks * self.G
 
+    def _launch_append(self, k: torch.Tensor, v: torch.Tensor, slot: int) -> None:
+        sb, sh, st, _ = k.stride()
+        with torch.cuda.device(self.device):
+            _native.check(_lib.kivi_store_append(
+                _vp(k), _vp(v), _SRC_DTYPES[k.dtype], sb, sh, st, k.shape[2], _vp(self.k_res),
+                _vp(self.v_res), self.B, self.H, self.D, self.R, slot, _stream(self.device)),
+                "kivi_store_append")
+
+    def _commit(self) -> None:
+        """Write a staged token into the ring (see stage_token)."""
+        if self._pending is not None:
+            k, v = self._pending
+            self._pending = None
+            self._launch_append(k, v, (self.res_start + self.res_len - 1) % self.R)
+
+    def stage_token(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Add one new token ``[B, Hkv, 1, D]`` to the window.  It counts at
+        once; its K/V are written by the next :meth:`attention` launch
+        itself, which reads them from ``k``/``v`` (fp32 rows 16-byte
+        aligned), or by a separate append when anything else reads the ring
+        first or the layout does not allow the fused path."""
+        k, v = self._token_source(k, v)
+        if k.shape[2] != 1:
+            raise ValueError(f"stage_token takes one token, got {k.shape[2]}")
+        self._commit()
+        if self.res_len + 1 > self.R:
+            raise RuntimeError(f"residual window overflow ({self.res_len} + 1 > {self.R})")
+        sb, sh = k.stride(0), k.stride(1)
+        if k.dtype == torch.float32 and sb % 4 == 0 and sh % 4 == 0 and \
+                k.data_ptr() % 16 == 0 and v.data_ptr() % 16 == 0:
+            self._pending = (k, v)
+            self.res_len += 1
+        else:
+            self.append(k, v)
+
     def append(self, k: torch.Tensor, v: torch.Tensor) -> None:
-        """Copy new tokens ``[B, Hkv, n, D]`` into the residual window (as
-        fp32; bf16/fp16 widen exactly).  The window must have room (callers
-        flush first)."""
+        """Copy new tokens ``[B, Hkv, n, D]`` into the residual window (one
+        launch for K and V; fp32/bf16/fp16 widened exactly, any strides with
+        contiguous channels).  The window must have room (callers flush
+        first)."""
+        self._commit()
+        k, v = self._token_source(k, v)
         n = k.shape[2]
         if self.res_len + n > self.R:
             raise RuntimeError(f"residual window overflow ({self.res_len} + {n} > {self.R})")
-        pos = (self.res_start + self.res_len) % self.R
-        first = min(n, self.R - pos)
-        self.k_res[:, :, pos:pos + first].copy_(k[:, :, :first])
-        self.v_res[:, :, pos:pos + first].copy_(v[:, :, :first])
-        if first < n:
-            self.k_res[:, :, :n - first].copy_(k[:, :, first:])
-            self.v_res[:, :, :n - first].copy_(v[:, :, first:])
+        if n == 0:
+            return
+        self._launch_append(k, v, (self.res_start + self.res_len) % self.R)
         self.res_len += n
 
     def _token_source(self, k: torch.Tensor, v: torch.Tensor):
@@ -228,6 +266,7 @@ class PackedKVStore:
         R = self.R if flush_at is None else int(flush_at)
         if not self.G <= R <= self.R:
             raise ValueError(f"flush threshold {R} must lie in [{self.G}, {self.R}]")
+        self._commit()
         k, v = self._token_source(k, v)
         n = k.shape[2]
         total = self.res_len + n
@@ -265,6 +304,7 @@ class PackedKVStore:
 
     def residual(self):
         """The residual window in token order (a copy when it wraps)."""
+        self._commit()
         s, n = self.res_start, self.res_len
         if s + n <= self.R:
             return self.k_res[:, :, s:s + n], self.v_res[:, :, s:s + n]
@@ -275,6 +315,7 @@ class PackedKVStore:
         """Quantise the G oldest residual tokens into the next chunk."""
         if self.res_len < self.G:
             raise RuntimeError(f"Cannot flush {self.G} tokens: residual only has {self.res_len}")
+        self._commit()
         self.reserve(self.n_chunks + 1)
         hist_cap = self.capacity * self.G if self.keep_history else 0
         with torch.cuda.device(self.device):
@@ -290,6 +331,7 @@ class PackedKVStore:
 
     def reset(self) -> None:
         self.res_start = self.res_len = self.n_chunks = 0
+        self._pending = None
 
     _TENSORS = ("k_res", "v_res", "k_codes", "k_scale", "k_zero", "v_codes", "v_scale",
                 "v_zero", "k_hist", "v_hist")
@@ -302,6 +344,7 @@ class PackedKVStore:
     def select_batch(self, index: torch.Tensor) -> None:
         """Keep (and reorder or repeat) batch rows ``index`` of every tensor,
         e.g. to follow a beam-search reorder."""
+        self._commit()
         for name in self._TENSORS:
             t = getattr(self, name)
             if t is not None:

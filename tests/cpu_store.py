@@ -42,6 +42,9 @@ class CpuPackedStore:
         self.res_k = torch.cat([self.res_k, k.float().cpu()], dim=2)
         self.res_v = torch.cat([self.res_v, v.float().cpu()], dim=2)
 
+    def stage_token(self, k, v):
+        self.append(k, v)
+
     def flush(self):
         G = self.G
         if self.res_len < G:
