@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define KIVI_HIP_ABI_VERSION 2
+#define KIVI_HIP_ABI_VERSION 3
 
 #define KIVI_OK 0
 #define KIVI_ERR_INVALID_ARGUMENT 1
@@ -89,10 +89,14 @@ int kivi_quant_dequant_roundtrip_values(const float* input, float* output,
 
 /* ---- HBM-resident packed store --------------------------------------------
  * Replaces KiviCache._flush_group (src/kivi_sycl/cache/manager.py:309-374):
- * quantises the `group_size_k` oldest tokens of the fp32 residual ring of
- * every (batch, kv-head) into chunk `chunk_index` of the packed store, on the
+ * quantises the `group_size_k` oldest tokens of the residual ring of every
+ * (batch, kv-head) into chunk `chunk_index` of the packed store, on the
  * device, without host copies.  Per (b, kv-head):
- *   k_res, v_res    [res_capacity][head_dim] f32 ring; token t of the window
+ *   k_res, v_res    [res_capacity][head_dim] ring, 16-byte aligned, of
+ *                   element type res_dtype (0 f32, 1 bf16, 2 f16; 16-bit
+ *                   values are widened exactly, so a 16-bit ring holding a
+ *                   half-precision model's K/V gives the results of an f32
+ *                   ring holding the same values); token t of the window
  *                   sits at slot (res_start + t) % res_capacity
  *   k_codes, v_codes [chunk_capacity][G*head_dim/4] u8 per chunk, in the code
  *                   layout kivi_store_code_layout() reports:
@@ -114,8 +118,8 @@ int kivi_quant_dequant_roundtrip_values(const float* input, float* output,
  * the dequantised tokens are also written at rows chunk_index*G .. +G-1
  * (bit-identical to the round-trip ops, manager.py:337-345).  Requires
  * group_size_k * head_dim <= 65536. */
-int kivi_store_flush(const float* k_res, const float* v_res, uint8_t* k_codes,
-                     float* k_scale, float* k_zero, uint8_t* v_codes, float* v_scale,
+int kivi_store_flush(const void* k_res, const void* v_res, int32_t res_dtype,
+                     uint8_t* k_codes, float* k_scale, float* k_zero, uint8_t* v_codes, float* v_scale,
                      float* v_zero, float* k_hist, float* v_hist, int64_t hist_capacity,
                      int32_t batch, int32_t kv_heads, int32_t head_dim,
                      int32_t group_size_k, int32_t group_size_v, int32_t res_capacity,
@@ -137,8 +141,8 @@ int kivi_store_flush(const float* k_res, const float* v_res, uint8_t* k_codes,
  * the last chunk (in the ring, and the new tokens past n_chunks*G - res_len).
  * Requires n_chunks*G <= res_len + new_tokens and group_size_k * head_dim <=
  * 65536. */
-int kivi_store_flush_chunks(const float* k_res, const float* v_res, const void* k_new,
-                            const void* v_new, int32_t new_dtype, int64_t new_batch_stride,
+int kivi_store_flush_chunks(const void* k_res, const void* v_res, int32_t res_dtype,
+                            const void* k_new, const void* v_new, int32_t new_dtype, int64_t new_batch_stride,
                             int64_t new_head_stride, int64_t new_token_stride,
                             int32_t new_tokens, uint8_t* k_codes, float* k_scale,
                             float* k_zero, uint8_t* v_codes, float* v_scale, float* v_zero,
@@ -151,14 +155,15 @@ int kivi_store_flush_chunks(const float* k_res, const float* v_res, const void* 
 /* Append new_tokens tokens to the residual ring of every (b, kv-head): token
  * t of k_new/v_new (element (b, h, t, d) at b*new_batch_stride +
  * h*new_head_stride + t*new_token_stride + d, in elements of new_dtype: 0
- * f32, 1 bf16, 2 f16, widened exactly) goes to ring slot
- * (slot + t) % res_capacity.  K and V in one launch.  Replaces the residual
+ * f32, 1 bf16, 2 f16) goes to ring slot (slot + t) % res_capacity.  An f32
+ * ring (res_dtype 0) takes any new_dtype, widened exactly; a bf16 or f16 ring
+ * takes its own type only, copied bit for bit.  K and V in one launch.  Replaces the residual
  * append of KiviCache.add_tokens (manager.py:226-231, a torch.cat of the
  * fp32 residual); the caller keeps the window's start and length. */
 int kivi_store_append(const void* k_new, const void* v_new, int32_t new_dtype,
                       int64_t new_batch_stride, int64_t new_head_stride,
-                      int64_t new_token_stride, int32_t new_tokens, float* k_res, float* v_res,
-                      int32_t batch, int32_t kv_heads, int32_t head_dim, int32_t res_capacity,
+                      int64_t new_token_stride, int32_t new_tokens, void* k_res, void* v_res,
+                      int32_t res_dtype, int32_t batch, int32_t kv_heads, int32_t head_dim, int32_t res_capacity,
                       int32_t slot, void* stream);
 
 /* Code layout of a store with these shapes: 1 (matrix-core operand order)
@@ -174,7 +179,8 @@ int kivi_store_code_layout(int32_t head_dim, int32_t group_size_k, int32_t group
  * [head_dim] f32, computes out [batch][q_heads][head_dim] =
  *   softmax(q . [K_hat ; K_res]^T * softmax_scale) . [V_hat ; V_res]
  * over the first num_chunks chunks of the packed store (layout above) and the
- * res_len residual tokens, query head h reading kv head h / (q_heads/kv_heads).
+ * res_len residual tokens (ring of element type res_dtype, as for
+ * kivi_store_flush), query head h reading kv head h / (q_heads/kv_heads).
  * num_splits <= 0 picks the split-K factor; workspace must hold
  * kivi_packed_decode_attention_workspace_size(...) bytes (0 means none is
  * needed and workspace may be NULL).  Supported: q_heads/kv_heads in
@@ -189,8 +195,8 @@ size_t kivi_packed_decode_attention_workspace_size(int32_t batch, int32_t q_head
 
 int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const float* k_scale,
                                  const float* k_zero, const uint8_t* v_codes,
-                                 const float* v_scale, const float* v_zero, const float* k_res,
-                                 const float* v_res, float* out, void* workspace,
+                                 const float* v_scale, const float* v_zero, const void* k_res,
+                                 const void* v_res, int32_t res_dtype, float* out, void* workspace,
                                  size_t workspace_bytes, int32_t batch, int32_t q_heads,
                                  int32_t kv_heads, int32_t head_dim, int32_t group_size_k,
                                  int32_t group_size_v, int32_t chunk_capacity,
@@ -201,18 +207,19 @@ int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const f
 /* kivi_packed_decode_attention with this step's new token appended in the
  * same launch: the window (res_start, res_len) already counts the new token
  * as its last (index res_len - 1, ring slot (res_start + res_len - 1) %
- * res_capacity); the kernel reads it from k_new / v_new (fp32, element
- * (b, h, d) at b*new_batch_stride + h*new_head_stride + d, rows 16-byte
- * aligned) and writes it into that ring slot for later launches.  Same
+ * res_capacity); the kernel reads it from k_new / v_new (element type
+ * res_dtype, element (b, h, d) at b*new_batch_stride + h*new_head_stride + d,
+ * rows aligned to four elements: 16 bytes for f32, 8 for bf16/f16) and writes
+ * it into that ring slot for later launches.  Same
  * result as kivi_store_append followed by kivi_packed_decode_attention,
  * without the separate launch.  Replaces the residual append of
  * KiviCache.add_tokens (manager.py:226-231) together with the step's
  * attention. */
 int kivi_packed_decode_attention_append(
-    const float* q, const float* k_new, const float* v_new, int64_t new_batch_stride,
+    const float* q, const void* k_new, const void* v_new, int64_t new_batch_stride,
     int64_t new_head_stride, const uint8_t* k_codes, const float* k_scale, const float* k_zero,
-    const uint8_t* v_codes, const float* v_scale, const float* v_zero, float* k_res,
-    float* v_res, float* out, void* workspace, size_t workspace_bytes, int32_t batch,
+    const uint8_t* v_codes, const float* v_scale, const float* v_zero, void* k_res,
+    void* v_res, int32_t res_dtype, float* out, void* workspace, size_t workspace_bytes, int32_t batch,
     int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t group_size_k,
     int32_t group_size_v, int32_t chunk_capacity, int32_t num_chunks, int32_t res_capacity,
     int32_t res_start, int32_t res_len, float softmax_scale, int32_t num_splits, void* stream);

@@ -432,6 +432,7 @@ def packed_decode_attention(q, store, softmax_scale=None, out=None, num_splits=0
         _check(workspace.is_contiguous() and workspace.numel() * workspace.element_size() >= need,
                "workspace must be contiguous and hold ", need, " bytes")
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    res_dt = store.res_dtype_code
     pend = getattr(store, "_pending", None)
     if pend is not None:
         # the staged token goes into the ring within this launch
@@ -444,7 +445,7 @@ def packed_decode_attention(q, store, softmax_scale=None, out=None, num_splits=0
                 ctypes.c_void_p(store.k_scale.data_ptr()), ctypes.c_void_p(store.k_zero.data_ptr()),
                 ctypes.c_void_p(store.v_codes.data_ptr()), ctypes.c_void_p(store.v_scale.data_ptr()),
                 ctypes.c_void_p(store.v_zero.data_ptr()), ctypes.c_void_p(store.k_res.data_ptr()),
-                ctypes.c_void_p(store.v_res.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                ctypes.c_void_p(store.v_res.data_ptr()), res_dt, ctypes.c_void_p(out.data_ptr()),
                 ctypes.c_void_p(workspace.data_ptr() if workspace is not None else 0), ws_bytes,
                 B, Hq, store.H, D, store.G, store.Gv, store.capacity, store.n_chunks, store.R,
                 store.res_start, store.res_len, scale, int(num_splits),
@@ -457,7 +458,7 @@ def packed_decode_attention(q, store, softmax_scale=None, out=None, num_splits=0
             ctypes.c_void_p(store.k_scale.data_ptr()), ctypes.c_void_p(store.k_zero.data_ptr()),
             ctypes.c_void_p(store.v_codes.data_ptr()), ctypes.c_void_p(store.v_scale.data_ptr()),
             ctypes.c_void_p(store.v_zero.data_ptr()), ctypes.c_void_p(store.k_res.data_ptr()),
-            ctypes.c_void_p(store.v_res.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+            ctypes.c_void_p(store.v_res.data_ptr()), res_dt, ctypes.c_void_p(out.data_ptr()),
             ctypes.c_void_p(workspace.data_ptr() if workspace is not None else 0), ws_bytes,
             B, Hq, store.H, D, store.G, store.Gv, store.capacity, store.n_chunks, store.R,
             store.res_start, store.res_len, scale, int(num_splits),

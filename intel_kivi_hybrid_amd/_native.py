@@ -36,21 +36,21 @@ SIGNATURES = {
     "kivi_dequantize_values_per_token": [_vp, _vp, _vp, _vp, _i64, _i32, _vp],
     "kivi_quant_dequant_roundtrip_keys": [_vp, _vp, _i64, _i32, _vp],
     "kivi_quant_dequant_roundtrip_values": [_vp, _vp, _i64, _i32, _i32, _vp],
-    "kivi_store_flush": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+    "kivi_store_flush": [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
-    "kivi_store_flush_chunks": [_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _vp, _vp,
+    "kivi_store_flush_chunks": [_vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _vp, _vp,
                                 _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32,
                                 _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     "kivi_store_append": [_vp, _vp, _i32, _i64, _i64, _i64, _i32, _vp, _vp, _i32, _i32, _i32,
-                          _i32, _i32, _vp],
+                          _i32, _i32, _i32, _vp],
     "kivi_store_code_layout": [_i32, _i32, _i32],
     "kivi_packed_decode_attention_workspace_size": [_i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                                     _i32, _i32],
     "kivi_packed_decode_attention_append": [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
-                                            _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _i32,
+                                            _vp, _vp, _vp, _i32, _vp, _vp, ctypes.c_size_t, _i32,
                                             _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                             _i32, _i32, _f32, _i32, _vp],
-    "kivi_packed_decode_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+    "kivi_packed_decode_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp,
                                      _vp, ctypes.c_size_t, _i32, _i32, _i32, _i32, _i32,
                                      _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp],
 }

@@ -58,16 +58,18 @@ FORMAT_VERSION = 1
 _STORE_CLASS = PackedKVStore
 
 
-def store_bytes(B: int, H: int, D: int, G: int, Gv: int, n_chunks: int, res_len: int) -> dict:
+def store_bytes(B: int, H: int, D: int, G: int, Gv: int, n_chunks: int, res_len: int,
+                res_elem_bytes: int = 4) -> dict:
     """Byte accounting of one layer's store contents (manager.py:350-356
     generalised to separate key and value group sizes): 2-bit codes, fp32
     scales and zeros (keys per channel and chunk, values per token and Gv
-    channels), and the fp32 residual window."""
+    channels), and the residual window (fp32 like the reference's, or 2
+    bytes per element for a bf16/fp16 ring)."""
     tokens = n_chunks * G
     codes = 2 * B * H * tokens * D // 4
     k_meta = B * H * n_chunks * D * 4 * 2
     v_meta = B * H * tokens * (D // Gv) * 4 * 2
-    residual = 2 * B * H * res_len * D * 4
+    residual = 2 * B * H * res_len * D * res_elem_bytes
     return {"codes": codes, "k_scales_zeros": k_meta, "v_scales_zeros": v_meta,
             "residual": residual, "quantized": codes + k_meta + v_meta}
 
@@ -109,10 +111,14 @@ class KiviPackedLayer(CacheLayerMixin):
         if o.num_kv_heads is not None and H != o.num_kv_heads:
             raise ValueError(f"KiviPackedCache was built for {o.num_kv_heads} kv heads but "
                              f"layer {self.index} has {H}")
+        # The ring keeps a half-precision model's K/V in their own type
+        # (lossless, half the bytes); anything else in fp32.
+        rdt = key_states.dtype if key_states.dtype in (torch.bfloat16, torch.float16) \
+            else torch.float32
         st = self.store
-        if st is None or st.B != B or st.H != H:
+        if st is None or st.B != B or st.H != H or st.residual_dtype != rdt:
             self.store = _STORE_CLASS(B, H, D, o.G, o.R, o.device, group_size_v=o.Gv,
-                                      chunk_capacity=o.chunk_capacity)
+                                      chunk_capacity=o.chunk_capacity, residual_dtype=rdt)
         else:
             st.reset()
         self.dtype, self.device = key_states.dtype, key_states.device
@@ -224,7 +230,8 @@ class KiviPackedCache(Cache):
     Args mirror :class:`KiviCache` (manager.py:52-133): ``num_layers``,
     ``head_dim``, ``num_kv_heads``, ``device`` (HIP device of the store),
     ``group_size`` (G, key group along tokens and chunk length),
-    ``residual_length`` (R, fp32 window), plus ``value_group_size`` (value
+    ``residual_length`` (R, the residual window: in the model's K/V type for
+    bf16/fp16 models, else fp32), plus ``value_group_size`` (value
     group along channels, default G) and ``chunk_capacity`` (chunks to
     preallocate per layer; the store grows by doubling beyond it).
 
@@ -281,7 +288,8 @@ class KiviPackedCache(Cache):
         if st is None:
             return {"total_tokens": 0, "quantized_tokens": 0, "residual_tokens": 0,
                     "kivi_bytes": 0, "fp32_bytes": 0, "compression": 0}
-        b = store_bytes(st.B, st.H, st.D, st.G, st.Gv, st.n_chunks, st.res_len)
+        b = store_bytes(st.B, st.H, st.D, st.G, st.Gv, st.n_chunks, st.res_len,
+                        st.residual_dtype.itemsize)
         total = st.quantized_tokens + st.res_len
         kivi = b["quantized"] + b["residual"]
         fp32 = 2 * st.B * st.H * total * st.D * 4
@@ -298,8 +306,9 @@ class KiviPackedCache(Cache):
         u8, ``k_scale``/``k_zero`` ``[B, Hkv, D, T/G]``, ``v_codes``
         ``[B, Hkv, T, D/4]`` u8, ``v_scale``/``v_zero`` ``[B, Hkv, T, D/Gv]``
         (the layouts of the reference's quantize_keys / quantize_values over
-        the T quantised tokens, kv_cache_ops.cpp:179-199) and the fp32
-        residual windows ``k_residual``/``v_residual`` ``[B, Hkv, r, D]``;
+        the T quantised tokens, kv_cache_ops.cpp:179-199) and the residual
+        windows ``k_residual``/``v_residual`` ``[B, Hkv, r, D]`` in the
+        ring's type (fp32, or bf16/fp16 for a half-precision model);
         the file metadata holds the format tag, version, cache geometry and
         per-layer flush counts."""
         from safetensors.torch import save_file
@@ -350,7 +359,7 @@ class KiviPackedCache(Cache):
                 lay.store = _STORE_CLASS.from_state(state, cache.G, cache.R, cache.device,
                                                     group_size_v=cache.Gv)
                 lay.flushes = int(meta.get(prefix + "flushes", "0"))
-                lay.dtype, lay.device = torch.float32, cache.device
+                lay.dtype, lay.device = lay.store.residual_dtype, cache.device
                 lay.is_initialized = True
             stray = [k for k in keys if not k.startswith("layers.")
                      or int(k.split(".")[1]) >= cache.num_layers]

@@ -41,14 +41,15 @@ struct AttnArgs {
     const uint8_t* v_codes;
     const float* v_scale;
     const float* v_zero;
-    const float* k_res;
-    const float* v_res;
+    const void* k_res;  // ring of element type res_dt
+    const void* v_res;
     float* out;
     float* part_o;     // [B, Hq, S, D]
     float* part_ml;    // [B, Hq, S, 2]
     int Hq, Hkv, D, G, Gv, Cmax, n_chunks, Rcap, res_start, res_len;
     int n_units, n_splits, units_per_split;
     float qscale;      // softmax scale * log2(e)
+    int res_dt;        // 0 fp32, 1 bf16, 2 fp16
 };
 
 __device__ __forceinline__ void wave_sync() {
@@ -167,10 +168,9 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
 #pragma unroll
             for (int h = 0; h < HG; ++h) acc[h] = 0.f;
             if (valid) {
-                const float4* kr = reinterpret_cast<const float4*>(
-                    a.k_res + (bh * a.Rcap + ring_slot(a.res_start, t, a.Rcap)) * D);
+                const int64_t kr = ((int64_t)bh * a.Rcap + ring_slot(a.res_start, t, a.Rcap)) * D;
                 for (int d4 = 0; d4 < D / 4; ++d4) {
-                    const float4 kv = kr[d4];
+                    const float4 kv = load4_dt(a.k_res, kr + 4 * d4, a.res_dt);
 #pragma unroll
                     for (int h = 0; h < HG; ++h) {
                         const float* qh = sq + h * D + 4 * d4;
@@ -232,8 +232,10 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
                 const int d = lane + kWave * j;
                 if (d >= D) break;
                 for (int tt = 0; tt < rcount; ++tt) {
-                    const float vv =
-                        a.v_res[(bh * a.Rcap + ring_slot(a.res_start, rbase + tt, a.Rcap)) * D + d];
+                    const float vv = load1_dt(
+                        a.v_res,
+                        ((int64_t)bh * a.Rcap + ring_slot(a.res_start, rbase + tt, a.Rcap)) * D + d,
+                        a.res_dt);
 #pragma unroll
                     for (int h = 0; h < HG; ++h)
                         o[h][j] = fmaf(sp[h * kWave + tt], vv, o[h][j]);
@@ -363,11 +365,12 @@ bool needs_workspace(const Plan& p) { return p.n_splits > 1; }
 }  // namespace
 
 int launch_attention_mfma(const AttnLaunch& a, hipStream_t st) {
+    const bool r16 = a.res_dt != kSrcF32;
     switch (a.Hq / a.Hkv) {
-        case 1: return launch_attention_mfma_hg1(a, st);
-        case 2: return launch_attention_mfma_hg2(a, st);
-        case 4: return launch_attention_mfma_hg4(a, st);
-        default: return launch_attention_mfma_hg8(a, st);
+        case 1: return r16 ? launch_attention_mfma_hg1_r16(a, st) : launch_attention_mfma_hg1(a, st);
+        case 2: return r16 ? launch_attention_mfma_hg2_r16(a, st) : launch_attention_mfma_hg2(a, st);
+        case 4: return r16 ? launch_attention_mfma_hg4_r16(a, st) : launch_attention_mfma_hg4(a, st);
+        default: return r16 ? launch_attention_mfma_hg8_r16(a, st) : launch_attention_mfma_hg8(a, st);
     }
 }
 }  // namespace kivi
@@ -392,14 +395,14 @@ size_t kivi_packed_decode_attention_workspace_size(int32_t batch, int32_t q_head
 
 static int decode_attention_impl(const float* q, const uint8_t* k_codes, const float* k_scale,
                                  const float* k_zero, const uint8_t* v_codes,
-                                 const float* v_scale, const float* v_zero, const float* k_res,
-                                 const float* v_res, float* out, void* workspace,
+                                 const float* v_scale, const float* v_zero, const void* k_res,
+                                 const void* v_res, int32_t res_dtype, float* out, void* workspace,
                                  size_t workspace_bytes, int32_t batch, int32_t q_heads,
                                  int32_t kv_heads, int32_t head_dim, int32_t group_size_k,
                                  int32_t group_size_v, int32_t chunk_capacity,
                                  int32_t num_chunks, int32_t res_capacity, int32_t res_start,
                                  int32_t res_len, float softmax_scale, int32_t num_splits,
-                                 const float* k_new, const float* v_new, int64_t new_sb,
+                                 const void* k_new, const void* v_new, int64_t new_sb,
                                  int64_t new_sh, void* stream) {
     if (!q || !out)
         return set_error(kErrInvalidArgument, "null q/out pointer");
@@ -433,9 +436,14 @@ static int decode_attention_impl(const float* q, const uint8_t* k_codes, const f
             return set_error(kErrInvalidArgument, "num_chunks %d exceeds capacity %d",
                              num_chunks, chunk_capacity);
     }
+    if (res_dtype < kSrcF32 || res_dtype > kSrcF16)
+        return set_error(kErrInvalidArgument, "res_dtype %d is not 0 (f32), 1 (bf16) or 2 (f16)",
+                         res_dtype);
     if (res_len > 0) {
         if (!k_res || !v_res)
             return set_error(kErrInvalidArgument, "null residual pointer");
+        if ((uintptr_t)k_res % 16 || (uintptr_t)v_res % 16)
+            return set_error(kErrInvalidArgument, "residual ring must be 16-byte aligned");
         if (res_len > res_capacity || res_start < 0 || res_start >= res_capacity)
             return set_error(kErrInvalidArgument,
                              "residual window (start %d, len %d) outside capacity %d",
@@ -457,9 +465,10 @@ static int decode_attention_impl(const float* q, const uint8_t* k_codes, const f
     const int new_slot = k_new ? (res_start + res_len - 1) % res_capacity : 0;
     if (k_new && layout != kLayoutMfma) {
         // the generic kernel reads the ring only: file the token there first
-        const int rc = kivi_store_append(k_new, v_new, 0, new_sb, new_sh, 0, 1,
-                                         const_cast<float*>(k_res), const_cast<float*>(v_res),
-                                         batch, kv_heads, head_dim, res_capacity, new_slot, stream);
+        const int rc = kivi_store_append(k_new, v_new, res_dtype, new_sb, new_sh, 0, 1,
+                                         const_cast<void*>(k_res), const_cast<void*>(v_res),
+                                         res_dtype, batch, kv_heads, head_dim, res_capacity,
+                                         new_slot, stream);
         if (rc) return rc;
     }
     if (layout == kLayoutMfma) {
@@ -467,14 +476,14 @@ static int decode_attention_impl(const float* q, const uint8_t* k_codes, const f
                      part_o, part_ml, batch, q_heads, kv_heads, head_dim, group_size_k,
                      group_size_v, chunk_capacity, num_chunks, res_capacity, res_start, res_len,
                      p.n_qsplits, p.chunks_per_wave, p.res_per_wave, p.n_splits,
-                     softmax_scale * kLog2e, k_new, v_new, new_sb, new_sh, new_slot};
+                     softmax_scale * kLog2e, k_new, v_new, new_sb, new_sh, new_slot, res_dtype};
         int rc = launch_attention_mfma(L, st);
         if (rc || !needs_workspace(p)) return rc;
     } else {
         AttnArgs a{q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res, v_res, out,
                    part_o, part_ml, q_heads, kv_heads, head_dim, group_size_k, group_size_v,
                    chunk_capacity, num_chunks, res_capacity, res_start, res_len, p.n_units,
-                   p.n_splits, p.units_per_split, softmax_scale * kLog2e};
+                   p.n_splits, p.units_per_split, softmax_scale * kLog2e, res_dtype};
         const dim3 grid(p.n_splits, kv_heads, batch);
         const size_t lds = (size_t)(hg * head_dim + kAttnWaves * (hg * head_dim + hg * kWave)) *
                            sizeof(float);
@@ -495,8 +504,8 @@ static int decode_attention_impl(const float* q, const uint8_t* k_codes, const f
 
 int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const float* k_scale,
                                  const float* k_zero, const uint8_t* v_codes,
-                                 const float* v_scale, const float* v_zero, const float* k_res,
-                                 const float* v_res, float* out, void* workspace,
+                                 const float* v_scale, const float* v_zero, const void* k_res,
+                                 const void* v_res, int32_t res_dtype, float* out, void* workspace,
                                  size_t workspace_bytes, int32_t batch, int32_t q_heads,
                                  int32_t kv_heads, int32_t head_dim, int32_t group_size_k,
                                  int32_t group_size_v, int32_t chunk_capacity,
@@ -504,17 +513,18 @@ int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const f
                                  int32_t res_len, float softmax_scale, int32_t num_splits,
                                  void* stream) {
     return decode_attention_impl(q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
-                                 v_res, out, workspace, workspace_bytes, batch, q_heads,
+                                 v_res, res_dtype, out, workspace, workspace_bytes, batch, q_heads,
                                  kv_heads, head_dim, group_size_k, group_size_v, chunk_capacity,
                                  num_chunks, res_capacity, res_start, res_len, softmax_scale,
                                  num_splits, nullptr, nullptr, 0, 0, stream);
 }
 
 int kivi_packed_decode_attention_append(
-        const float* q, const float* k_new, const float* v_new, int64_t new_batch_stride,
+        const float* q, const void* k_new, const void* v_new, int64_t new_batch_stride,
         int64_t new_head_stride, const uint8_t* k_codes, const float* k_scale,
         const float* k_zero, const uint8_t* v_codes, const float* v_scale, const float* v_zero,
-        float* k_res, float* v_res, float* out, void* workspace, size_t workspace_bytes,
+        void* k_res, void* v_res, int32_t res_dtype, float* out, void* workspace,
+        size_t workspace_bytes,
         int32_t batch, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
         int32_t group_size_k, int32_t group_size_v, int32_t chunk_capacity, int32_t num_chunks,
         int32_t res_capacity, int32_t res_start, int32_t res_len, float softmax_scale,
@@ -524,12 +534,20 @@ int kivi_packed_decode_attention_append(
     if (!k_res || !v_res || res_len < 1)
         return set_error(kErrInvalidArgument,
                          "the window must hold the new token (res_len %d >= 1)", res_len);
-    if (new_batch_stride < 0 || new_head_stride < 0 || new_batch_stride % 4 ||
-        new_head_stride % 4 || (uintptr_t)k_new % 16 || (uintptr_t)v_new % 16)
+    if (res_dtype < kSrcF32 || res_dtype > kSrcF16)
+        return set_error(kErrInvalidArgument, "res_dtype %d is not 0 (f32), 1 (bf16) or 2 (f16)",
+                         res_dtype);
+    // rows of the ring's type, four channels per aligned load
+    const int64_t vb = 4 * src_size(res_dtype);
+    if (new_batch_stride < 0 || new_head_stride < 0 ||
+        (new_batch_stride * src_size(res_dtype)) % vb ||
+        (new_head_stride * src_size(res_dtype)) % vb || (uintptr_t)k_new % vb ||
+        (uintptr_t)v_new % vb)
         return set_error(kErrInvalidArgument,
-                         "new-token rows must be 16-byte aligned (strides multiples of 4)");
+                         "new-token rows must be %d-byte aligned (strides multiples of 4)",
+                         (int)vb);
     return decode_attention_impl(q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
-                                 v_res, out, workspace, workspace_bytes, batch, q_heads,
+                                 v_res, res_dtype, out, workspace, workspace_bytes, batch, q_heads,
                                  kv_heads, head_dim, group_size_k, group_size_v, chunk_capacity,
                                  num_chunks, res_capacity, res_start, res_len, softmax_scale,
                                  num_splits, k_new, v_new, new_batch_stride, new_head_stride,

@@ -15,8 +15,8 @@ struct AttnLaunch {
     const uint8_t* v_codes;  // [B, Hkv, Cmax, G*D/4]
     const float* v_scale;    // [B, Hkv, Cmax, D/Gv, G]
     const float* v_zero;
-    const float* k_res;      // [B, Hkv, Rcap, D] ring
-    const float* v_res;
+    const void* k_res;       // [B, Hkv, Rcap, D] ring of element type res_dt
+    const void* v_res;
     float* out;              // [B, Hq, D]
     float* part_o;           // [B, Hq, n_splits, D] (n_splits > 1 only)
     float* part_ml;          // [B, Hq, n_splits, 2]
@@ -28,23 +28,29 @@ struct AttnLaunch {
     float qscale;            // softmax scale * log2(e)
     // Optional new token, the window's last (index res_len - 1): when k_new
     // is set the kernel reads that token from k_new / v_new (element
-    // (b, h, d) at b*new_sb + h*new_sh + d) and writes it to ring slot
-    // new_slot, so no separate append launch is needed.
-    const float* k_new = nullptr;
-    const float* v_new = nullptr;
+    // (b, h, d) at b*new_sb + h*new_sh + d, of the ring's type) and writes it
+    // to ring slot new_slot, so no separate append launch is needed.
+    const void* k_new = nullptr;
+    const void* v_new = nullptr;
     int64_t new_sb = 0, new_sh = 0;
     int new_slot = 0;
+    int res_dt = 0;          // ring element type: 0 fp32, 1 bf16, 2 fp16
 };
 
 // Launches the matrix-core kernel (kLayoutMfma stores, Hq/Hkv in {1,2,4,8}).
 // With n_splits == 1 it writes `out`; otherwise partials, which the caller
 // merges.  The kernel templates live in kivi_attention_mfma.hpp; each
-// Hq/Hkv ratio is instantiated in its own translation unit
-// (kivi_attention_mfma_hg<N>.hip) so that the build compiles them in parallel.
+// Hq/Hkv ratio and ring width (fp32, or 16-bit: _r16) is instantiated in its
+// own translation unit (kivi_attention_mfma_hg<N>[_r16].hip) so that the
+// build compiles them in parallel.
 int launch_attention_mfma(const AttnLaunch& a, hipStream_t stream);
 int launch_attention_mfma_hg1(const AttnLaunch& a, hipStream_t stream);
 int launch_attention_mfma_hg2(const AttnLaunch& a, hipStream_t stream);
 int launch_attention_mfma_hg4(const AttnLaunch& a, hipStream_t stream);
 int launch_attention_mfma_hg8(const AttnLaunch& a, hipStream_t stream);
+int launch_attention_mfma_hg1_r16(const AttnLaunch& a, hipStream_t stream);
+int launch_attention_mfma_hg2_r16(const AttnLaunch& a, hipStream_t stream);
+int launch_attention_mfma_hg4_r16(const AttnLaunch& a, hipStream_t stream);
+int launch_attention_mfma_hg8_r16(const AttnLaunch& a, hipStream_t stream);
 
 }  // namespace kivi

@@ -36,7 +36,7 @@
 // moved when a chunk exceeds it by more than 8 (probabilities stay <= 256),
 // so rescaling the accumulators is rare.  Workgroups of 4 waves merge their
 // states in LDS; workgroups past the chunk splits take the fp32 residual
-// window with plain fp32 FMAs.  Each workgroup writes a partial (o, m, l)
+// window (fp32, bf16 or fp16 elements, widened) with plain fp32 FMAs.  Each workgroup writes a partial (o, m, l)
 // that kivi_attention.hip's merge kernel combines with log-sum-exp weights.
 #pragma once
 
@@ -418,7 +418,8 @@ __device__ __forceinline__ void stage_meta(const ChunkRegs<S>& r, float* MT, int
 // NGC > 0: the number of value groups per token (D / Gv) is NGC at compile
 // time, so the value operand of every n-block is known statically and its
 // LDS reads can be issued ahead; NGC == 0 reads it from the launch.
-template <class S, int NGC>
+// R16: the residual ring holds bf16 or fp16 (a.res_dt) instead of fp32.
+template <class S, int NGC, bool R16>
 __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, int kvh, int b) {
     constexpr int HG = S::HG, D = S::D, G = S::G, NSUB = S::NSUB, NB = G / 16, NSEG = G / 8;
     // wave-uniform in an SGPR: chunk ranges, ring indices and branches on
@@ -449,14 +450,13 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // The new token (if any) is read from its own tensor by the residual
     // pass below; one wave of the first split also files it in the ring for
     // later launches.  Nothing in this launch reads that ring slot.
-    const float* knew_row = a.k_new ? a.k_new + b * a.new_sb + kvh * a.new_sh : nullptr;
-    const float* vnew_row = a.k_new ? a.v_new + b * a.new_sb + kvh * a.new_sh : nullptr;
-    if (knew_row && split == 0 && threadIdx.x < kWave) {
-        float* kdst = const_cast<float*>(a.k_res) + (bh * a.Rcap + a.new_slot) * D;
-        float* vdst = const_cast<float*>(a.v_res) + (bh * a.Rcap + a.new_slot) * D;
+    const bool has_new = a.k_new != nullptr;
+    const int64_t new_row = (int64_t)b * a.new_sb + (int64_t)kvh * a.new_sh;   // element offset
+    if (has_new && split == 0 && threadIdx.x < kWave) {
+        const int64_t dst = ((int64_t)bh * a.Rcap + a.new_slot) * D;
         for (int e = threadIdx.x; e < D / 4; e += kWave) {
-            reinterpret_cast<float4*>(kdst)[e] = reinterpret_cast<const float4*>(knew_row)[e];
-            reinterpret_cast<float4*>(vdst)[e] = reinterpret_cast<const float4*>(vnew_row)[e];
+            copy4_dt(const_cast<void*>(a.k_res), dst + 4 * e, a.k_new, new_row + 4 * e, a.res_dt);
+            copy4_dt(const_cast<void*>(a.v_res), dst + 4 * e, a.v_new, new_row + 4 * e, a.res_dt);
         }
     }
     __syncthreads();
@@ -760,18 +760,27 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         const int r1 = min(r0 + a.res_per_wave, a.res_len);
         const int tk = lane / 4, qq = lane % 4;
         const int c4 = lane % F4, ts = lane / F4;
+        // Four channels of a ring row widened to fp32.  The ring's width is
+        // a template parameter (a run-time branch here would cost registers
+        // at the kernel's peak, the prefetched chunks being live); bf16 vs
+        // fp16 is a select in the widening.
+        const bool res_half = a.res_dt == kSrcF16;
+        auto load4 = [&](const void* p, int64_t i) {
+            if constexpr (R16) return load4_16(p, i, res_half);
+            else return load4_vec<kSrcF32>(p, i);
+        };
         for (int t0 = r0; t0 < r1; t0 += kResPass) {
             const int n = min(kResPass, r1 - t0);
-            // scores
+            // scores: lane (tk, qq) takes channel quads qq, qq+4, ... of token tk's row
             const int ktok = t0 + min(tk, n - 1);          // index in the window
             int slot = a.res_start + ktok;
             slot = slot >= a.Rcap ? slot - a.Rcap : slot;
-            // lane (tk, qq) takes float4s qq, qq+4, ... of token tk's row
-            const float4* krow = reinterpret_cast<const float4*>(
-                knew_row && ktok == a.res_len - 1 ? knew_row : a.k_res + (bh * a.Rcap + slot) * D) + qq;
+            const bool knew = has_new && ktok == a.res_len - 1;
+            const int64_t krow = (knew ? new_row : ((int64_t)bh * a.Rcap + slot) * D) + 4 * qq;
+            const void* kbase = knew ? a.k_new : a.k_res;
             float4 kv[KQ];
 #pragma unroll
-            for (int j = 0; j < KQ; ++j) kv[j] = krow[4 * j];
+            for (int j = 0; j < KQ; ++j) kv[j] = load4(kbase, krow + 16 * j);
             // the pass's value rows are independent of the scores: load them
             // now so that a pass waits for HBM once
             float4 vv[kResPass / TS];
@@ -780,8 +789,9 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                 const int vtok = t0 + min(ts + TS * j, n - 1);
                 int vs = a.res_start + vtok;
                 vs = vs >= a.Rcap ? vs - a.Rcap : vs;
-                vv[j] = reinterpret_cast<const float4*>(
-                    vnew_row && vtok == a.res_len - 1 ? vnew_row : a.v_res + (bh * a.Rcap + vs) * D)[c4];
+                const bool vnew = has_new && vtok == a.res_len - 1;
+                vv[j] = load4(vnew ? a.v_new : a.v_res,
+                              (vnew ? new_row : ((int64_t)bh * a.Rcap + vs) * D) + 4 * c4);
             }
             float sres[HG];
 #pragma unroll
@@ -950,13 +960,13 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
 template <int HG, int D>
 constexpr int attn_waves_per_eu() { return (D <= 64 || (D <= 128 && HG <= 4)) ? 2 : 1; }
 
-template <int HG, int D, int G, int NGC>
+template <int HG, int D, int G, int NGC, bool R16>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<HG, D>())))
 void attn_mfma_kernel(AttnLaunch a) {
     extern __shared__ __align__(16) unsigned char smem[];
     using S = Shape<HG, D, G>;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    wave_path<S, NGC>(smem, a, split, kvh, b);
+    wave_path<S, NGC, R16>(smem, a, split, kvh, b);
 }
 
 int max_lds_per_block() {
@@ -967,7 +977,7 @@ int max_lds_per_block() {
     return v;
 }
 
-template <int HG, int D, int G, int NGC>
+template <int HG, int D, int G, int NGC, bool R16>
 int launch_shape(const AttnLaunch& a, hipStream_t st) {
     using S = Shape<HG, D, G>;
     static const int lds_limit = max_lds_per_block();
@@ -978,31 +988,32 @@ int launch_shape(const AttnLaunch& a, hipStream_t st) {
                          "group_size_v=%d needs %d bytes of LDS per workgroup; the device "
                          "allows %d", HG, D, G, a.Gv, lds, lds_limit);
     const dim3 grid(a.n_splits, a.Hkv, a.B);
-    attn_mfma_kernel<HG, D, G, NGC><<<grid, kBlock, lds, st>>>(a);
+    attn_mfma_kernel<HG, D, G, NGC, R16><<<grid, kBlock, lds, st>>>(a);
     return check_launch("packed_decode_attention (mfma)");
 }
 
 // Value groups of 32 channels, one group per token, or (head_dim 128/256
 // with 64- or 128-channel groups) the runtime count.
-template <int HG, int D, int G>
+template <int HG, int D, int G, bool R16>
 int launch_ng(const AttnLaunch& a, hipStream_t st) {
-    if (a.Gv == 32) return launch_shape<HG, D, G, D / 32>(a, st);
-    if (a.Gv == D) return launch_shape<HG, D, G, 1>(a, st);
-    if constexpr (D > 64) return launch_shape<HG, D, G, 0>(a, st);
+    if (a.Gv == 32) return launch_shape<HG, D, G, D / 32, R16>(a, st);
+    if (a.Gv == D) return launch_shape<HG, D, G, 1, R16>(a, st);
+    if constexpr (D > 64) return launch_shape<HG, D, G, 0, R16>(a, st);
     return set_error(kErrUnsupported, "group_size_v=%d with head_dim=%d", a.Gv, D);
 }
 
-template <int HG, int D>
+template <int HG, int D, bool R16>
 int launch_g(const AttnLaunch& a, hipStream_t st) {
-    return a.G == 32 ? launch_ng<HG, D, 32>(a, st) : launch_ng<HG, D, 64>(a, st);
+    return a.G == 32 ? launch_ng<HG, D, 32, R16>(a, st) : launch_ng<HG, D, 64, R16>(a, st);
 }
 
-template <int HG>
+// Every kernel shape for one Hq/Hkv ratio and ring width.
+template <int HG, bool R16>
 int launch_d(const AttnLaunch& a, hipStream_t st) {
     switch (a.D) {
-        case 64: return launch_g<HG, 64>(a, st);
-        case 128: return launch_g<HG, 128>(a, st);
-        default: return launch_g<HG, 256>(a, st);
+        case 64: return launch_g<HG, 64, R16>(a, st);
+        case 128: return launch_g<HG, 128, R16>(a, st);
+        default: return launch_g<HG, 256, R16>(a, st);
     }
 }
 

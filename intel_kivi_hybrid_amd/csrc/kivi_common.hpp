@@ -184,6 +184,90 @@ __device__ __forceinline__ uint32_t encode4(float x0, float x1, float x2, float 
     return q0 | (q1 << 2) | (q2 << 4) | (q3 << 6);
 }
 
+// ---------------------------------------------------------------------------
+// K/V element types of new tokens and of the residual ring: 0 fp32, 1 bf16,
+// 2 fp16 (the codes the C ABI takes).  16-bit values are widened exactly.
+// ---------------------------------------------------------------------------
+enum SrcType { kSrcF32 = 0, kSrcBF16 = 1, kSrcF16 = 2 };
+
+__host__ __device__ constexpr int src_size(int dt) { return dt == kSrcF32 ? 4 : 2; }
+
+template <int SRC>
+__device__ __forceinline__ float widen(const void* p, int64_t i) {
+    if constexpr (SRC == kSrcF32) {
+        return static_cast<const float*>(p)[i];
+    } else if constexpr (SRC == kSrcBF16) {
+        return __uint_as_float((uint32_t)static_cast<const uint16_t*>(p)[i] << 16);
+    } else {
+        return (float)static_cast<const _Float16*>(p)[i];
+    }
+}
+
+// Elements i..i+3 widened to fp32 with one 16-byte (fp32) or 8-byte (16-bit)
+// load: the offset must be aligned to that size.
+template <int SRC>
+__device__ __forceinline__ float4 load4_vec(const void* p, int64_t i) {
+    if constexpr (SRC == kSrcF32) {
+        return *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+    } else {
+        const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+        if constexpr (SRC == kSrcBF16) {
+            return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
+                               __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
+        } else {
+            return make_float4((float)__builtin_bit_cast(_Float16, (uint16_t)(u.x & 0xffffu)),
+                               (float)__builtin_bit_cast(_Float16, (uint16_t)(u.x >> 16)),
+                               (float)__builtin_bit_cast(_Float16, (uint16_t)(u.y & 0xffffu)),
+                               (float)__builtin_bit_cast(_Float16, (uint16_t)(u.y >> 16)));
+        }
+    }
+}
+
+// Elements i..i+3 widened to fp32; `vec` selects the aligned single load.
+template <int SRC>
+__device__ __forceinline__ float4 load4_new(const void* p, int64_t i, bool vec) {
+    if (vec) return load4_vec<SRC>(p, i);
+    return make_float4(widen<SRC>(p, i), widen<SRC>(p, i + 1), widen<SRC>(p, i + 2),
+                       widen<SRC>(p, i + 3));
+}
+
+// Elements i..i+3 of a 16-bit array widened to fp32, bf16 or fp16 chosen at
+// run time (`half` true for fp16) by a select after the one 8-byte load.
+__device__ __forceinline__ float4 load4_16(const void* p, int64_t i, bool half) {
+    const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+    auto cvt = [half](uint32_t h) {
+        return half ? (float)__builtin_bit_cast(_Float16, (uint16_t)h) : __uint_as_float(h << 16);
+    };
+    return make_float4(cvt(u.x & 0xffffu), cvt(u.x >> 16), cvt(u.y & 0xffffu), cvt(u.y >> 16));
+}
+
+// The same with the element type known at run time (a uniform branch; used
+// on the residual ring, whose type follows the model's K/V).
+__device__ __forceinline__ float4 load4_dt(const void* p, int64_t i, int dt) {
+    if (dt == kSrcBF16) return load4_vec<kSrcBF16>(p, i);
+    if (dt == kSrcF16) return load4_vec<kSrcF16>(p, i);
+    return load4_vec<kSrcF32>(p, i);
+}
+
+__device__ __forceinline__ float load1_dt(const void* p, int64_t i, int dt) {
+    if (dt == kSrcBF16) return widen<kSrcBF16>(p, i);
+    if (dt == kSrcF16) return widen<kSrcF16>(p, i);
+    return widen<kSrcF32>(p, i);
+}
+
+// Copies four elements of type dt, src[si..si+3] -> dst[di..di+3], bit for
+// bit (offsets aligned as for load4_vec).
+__device__ __forceinline__ void copy4_dt(void* dst, int64_t di, const void* src, int64_t si,
+                                         int dt) {
+    if (dt == kSrcF32) {
+        *reinterpret_cast<float4*>(static_cast<float*>(dst) + di) =
+            *reinterpret_cast<const float4*>(static_cast<const float*>(src) + si);
+    } else {
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(dst) + di) =
+            *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(src) + si);
+    }
+}
+
 // x_hat = fl(fl(q * scale) + zero) (dequantize_kernels.cpp:24).
 __device__ __forceinline__ float decode1(uint32_t q, float scale, float zero) {
     return __fadd_rn(__fmul_rn((float)q, scale), zero);

@@ -31,12 +31,11 @@ namespace kivi {
 namespace {
 
 constexpr int kFlushBlock = 256;
-constexpr int kTileMaxElems = 8192;
-constexpr int kMaxPerBlock = 1;       // chunks per flush_fast_kernel workgroup   // G*D staged in LDS (fp32 tile + u8 codes)
+constexpr int kTileMaxElems = 8192;   // G*D staged in LDS (fp32 tile + u8 codes)
 
 struct FlushArgs {
-    const float* k_res;   // [B, H, Rcap, D] ring
-    const float* v_res;
+    const void* k_res;    // [B, H, Rcap, D] ring of element type res_dt
+    const void* v_res;
     const void* k_new;    // new tokens: element (b, h, t, d) at b*new_sb + h*new_sh + t*new_st + d
     const void* v_new;
     int64_t new_sb, new_sh, new_st;
@@ -56,9 +55,9 @@ struct FlushArgs {
     int n_chunks;         // chunks in this launch: run chunks first .. first+n_chunks-1
     int first;            // (flush_fast_kernel only; flush_kernel starts at 0)
     bool new_vec;         // new rows allow 16-byte (fp32) / 8-byte (16-bit) loads
+    int res_dt;           // element type of the ring (SrcType)
 };
 
-enum SrcType { kSrcF32 = 0, kSrcBF16 = 1, kSrcF16 = 2 };
 // Where a flush_fast_kernel launch's chunks come from: all from the ring, all
 // from the new tokens, or across both.
 enum RunMode { kFromRing = 0, kFromNew = 1, kFromBoth = 2 };
@@ -66,62 +65,6 @@ enum RunMode { kFromRing = 0, kFromNew = 1, kFromBoth = 2 };
 __device__ __forceinline__ int ring(int start, int t, int cap) {
     const int s = start + t;
     return s >= cap ? s - cap : s;
-}
-
-template <int SRC>
-__device__ __forceinline__ float widen(const void* p, int64_t i) {
-    if constexpr (SRC == kSrcF32) {
-        return static_cast<const float*>(p)[i];
-    } else if constexpr (SRC == kSrcBF16) {
-        return __uint_as_float((uint32_t)static_cast<const uint16_t*>(p)[i] << 16);
-    } else {
-        return (float)static_cast<const _Float16*>(p)[i];
-    }
-}
-
-// Four consecutive channels of one new-token row, widened to fp32, with one
-// 16-byte (fp32) or 8-byte (16-bit) load: the row and channel offsets must
-// be aligned to that size.
-template <int SRC>
-__device__ __forceinline__ float4 load4_vec(const void* p, int64_t i) {
-    if constexpr (SRC == kSrcF32) {
-        return *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
-    } else {
-        const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
-        if constexpr (SRC == kSrcBF16) {
-            return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
-                               __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
-        } else {
-            return make_float4((float)__builtin_bit_cast(_Float16, (uint16_t)(u.x & 0xffffu)),
-                               (float)__builtin_bit_cast(_Float16, (uint16_t)(u.x >> 16)),
-                               (float)__builtin_bit_cast(_Float16, (uint16_t)(u.y & 0xffffu)),
-                               (float)__builtin_bit_cast(_Float16, (uint16_t)(u.y >> 16)));
-        }
-    }
-}
-
-// Four consecutive channels of one new-token row, widened to fp32.
-template <int SRC>
-__device__ __forceinline__ float4 load4_new(const void* p, int64_t i, bool vec) {
-    if constexpr (SRC == kSrcF32) {
-        if (vec) return *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
-    } else {
-        if (vec) {
-            const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
-            if constexpr (SRC == kSrcBF16) {
-                return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
-                                   __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
-            } else {
-                return make_float4(
-                    (float)__builtin_bit_cast(_Float16, (uint16_t)(u.x & 0xffffu)),
-                    (float)__builtin_bit_cast(_Float16, (uint16_t)(u.x >> 16)),
-                    (float)__builtin_bit_cast(_Float16, (uint16_t)(u.y & 0xffffu)),
-                    (float)__builtin_bit_cast(_Float16, (uint16_t)(u.y >> 16)));
-            }
-        }
-    }
-    return make_float4(widen<SRC>(p, i), widen<SRC>(p, i + 1), widen<SRC>(p, i + 2),
-                       widen<SRC>(p, i + 3));
 }
 
 // Writes one chunk's codes (u8 per element in `codes`, [G][D]) in the store
@@ -178,7 +121,7 @@ __device__ void write_codes(const uint8_t* codes, uint8_t* out, int G, int D) {
 // One workgroup per (b, kv-head, chunk).  TILE: the chunk's G x D tokens are
 // first staged in LDS as fp32 with coalesced loads (needs G*D <=
 // kTileMaxElems); otherwise elements are read from their source directly.
-// SRC is the element type of the new-token source (the ring is fp32).
+// SRC is the element type of the new-token source; the ring's is a.res_dt.
 template <int LAYOUT, bool TILE, int SRC>
 __global__ __launch_bounds__(kFlushBlock) void flush_kernel(FlushArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -194,15 +137,15 @@ __global__ __launch_bounds__(kFlushBlock) void flush_kernel(FlushArgs a) {
     const int64_t code_bytes = (int64_t)G * D / 4;
     const int64_t hist_row0 = (int64_t)bh * a.hist_cap + (int64_t)chunk * G;
 
-    auto stage = [&](const float* res, const void* nw) {
+    auto stage = [&](const void* res, const void* nw) {
         const int nv = G * (D / 4);
         for (int e = threadIdx.x; e < nv; e += blockDim.x) {
             const int t = e / (D / 4), d4 = e % (D / 4);
             const int vt = vt0 + t;
             float4 x;
             if (vt < a.res_len) {
-                x = reinterpret_cast<const float4*>(
-                    res + res_base + (int64_t)ring(a.res_start, vt, a.Rcap) * D)[d4];
+                x = load4_dt(res, res_base + (int64_t)ring(a.res_start, vt, a.Rcap) * D + 4 * d4,
+                             a.res_dt);
             } else {
                 x = load4_new<SRC>(nw, new_base + (int64_t)(vt - a.res_len) * a.new_st + 4 * d4,
                                    a.new_vec);
@@ -210,10 +153,11 @@ __global__ __launch_bounds__(kFlushBlock) void flush_kernel(FlushArgs a) {
             reinterpret_cast<float4*>(tile)[e] = x;
         }
     };
-    auto elem = [&](const float* res, const void* nw, int t, int d) -> float {
+    auto elem = [&](const void* res, const void* nw, int t, int d) -> float {
         if constexpr (TILE) return tile[t * D + d];
         const int vt = vt0 + t;
-        if (vt < a.res_len) return res[res_base + (int64_t)ring(a.res_start, vt, a.Rcap) * D + d];
+        if (vt < a.res_len)
+            return load1_dt(res, res_base + (int64_t)ring(a.res_start, vt, a.Rcap) * D + d, a.res_dt);
         return widen<SRC>(nw, new_base + (int64_t)(vt - a.res_len) * a.new_st + d);
     };
     // Dequantised tokens go back into the tile (TILE) and are then copied to
@@ -370,9 +314,10 @@ __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
     const int j = a.first + (int)blockIdx.y;   // run chunk of this workgroup
 
     // K or V of run chunk j: float4 slot i*256 + tid of the [G][D] chunk.  The
-    // source is fixed per launch (MODE), so the loads carry no branches and
-    // the compiler's wait counting keeps the next chunk's loads in flight.
-    auto load = [&](float4 (&x)[NV], const float* res, const void* nw, int j) {
+    // source is fixed per launch (MODE), so the loads carry no branches.  SRC
+    // is the element type of that source: the ring's for kFromRing, the new
+    // tokens' otherwise (kFromBoth reads its ring part by a.res_dt).
+    auto load = [&](float4 (&x)[NV], const void* res, const void* nw, int j) {
         const int vt0 = j * G;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
@@ -383,11 +328,11 @@ __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
                 x[i] = load4_vec<SRC>(nw, new_base + (int64_t)(vt - a.res_len) * a.new_st + 4 * d4);
             } else if constexpr (MODE == kFromRing) {
                 const int64_t row = res_base + (int64_t)ring(a.res_start, vt, a.Rcap) * D;
-                x[i] = reinterpret_cast<const float4*>(res + row)[d4];
+                x[i] = load4_vec<SRC>(res, row + 4 * d4);
             } else {
                 if (vt < a.res_len) {
                     const int64_t row = res_base + (int64_t)ring(a.res_start, vt, a.Rcap) * D;
-                    x[i] = reinterpret_cast<const float4*>(res + row)[d4];
+                    x[i] = load4_dt(res, row + 4 * d4, a.res_dt);
                 } else {
                     x[i] = load4_vec<SRC>(nw, new_base + (int64_t)(vt - a.res_len) * a.new_st + 4 * d4);
                 }
@@ -581,7 +526,7 @@ void launch_fast4(const FlushArgs& a, int src, dim3 grid, hipStream_t st) {
 template <int G, int D, int GV>
 void launch_fast3(const FlushArgs& a, int src, int mode, dim3 grid, hipStream_t st) {
     if (mode == kFromNew) launch_fast4<G, D, GV, kFromNew>(a, src, grid, st);
-    else if (mode == kFromRing) launch_fast4<G, D, GV, kFromRing>(a, kSrcF32, grid, st);
+    else if (mode == kFromRing) launch_fast4<G, D, GV, kFromRing>(a, a.res_dt, grid, st);
     else launch_fast4<G, D, GV, kFromBoth>(a, src, grid, st);
 }
 
@@ -628,20 +573,28 @@ void launch_flush(const FlushArgs& a, int src, dim3 grid, size_t lds, hipStream_
 }
 
 // Residual append: token t of the new K/V goes to ring slot (slot + t) % Rcap
-// of every (b, kv-head), one float4 of channels per thread, K and V in the
-// same launch.
+// of every (b, kv-head), four channels per thread, K and V in the same
+// launch.  An fp32 ring (RES == kSrcF32) takes any source type, widened; a
+// 16-bit ring takes its own type only, copied bit for bit.
 struct AppendArgs {
     const void* k_new;
     const void* v_new;
     int64_t sb, sh, st;            // element strides of the new tokens (channels contiguous)
-    float* k_res;                  // [B, H, Rcap, D]
-    float* v_res;
+    void* k_res;                   // [B, H, Rcap, D]
+    void* v_res;
     int64_t total;                 // B * H * n * D/4
     int H, D, n, Rcap, slot;
     bool vec;
 };
 
-template <int SRC>
+// Four raw 16-bit elements at i..i+3 (one 8-byte load when `vec`).
+__device__ __forceinline__ uint2 load4_raw16(const void* p, int64_t i, bool vec) {
+    const uint16_t* h = static_cast<const uint16_t*>(p) + i;
+    if (vec) return *reinterpret_cast<const uint2*>(h);
+    return make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+}
+
+template <int SRC, int RES>
 __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= a.total) return;
@@ -654,8 +607,14 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
     int s = a.slot + t;
     s = s >= a.Rcap ? s - a.Rcap : s;
     const int64_t dst = (bh * a.Rcap + s) * a.D / 4 + d4;
-    reinterpret_cast<float4*>(a.k_res)[dst] = load4_new<SRC>(a.k_new, off, a.vec);
-    reinterpret_cast<float4*>(a.v_res)[dst] = load4_new<SRC>(a.v_new, off, a.vec);
+    if constexpr (RES == kSrcF32) {
+        reinterpret_cast<float4*>(a.k_res)[dst] = load4_new<SRC>(a.k_new, off, a.vec);
+        reinterpret_cast<float4*>(a.v_res)[dst] = load4_new<SRC>(a.v_new, off, a.vec);
+    } else {
+        static_assert(RES == SRC, "a 16-bit ring takes its own element type");
+        reinterpret_cast<uint2*>(a.k_res)[dst] = load4_raw16(a.k_new, off, a.vec);
+        reinterpret_cast<uint2*>(a.v_res)[dst] = load4_raw16(a.v_new, off, a.vec);
+    }
 }
 
 }  // namespace
@@ -669,7 +628,7 @@ extern "C" int kivi_store_code_layout(int32_t head_dim, int32_t group_size_k,
 }
 
 extern "C" int kivi_store_flush_chunks(
-        const float* k_res, const float* v_res, const void* k_new, const void* v_new,
+        const void* k_res, const void* v_res, int32_t res_dtype, const void* k_new, const void* v_new,
         int32_t new_dtype, int64_t new_batch_stride, int64_t new_head_stride,
         int64_t new_token_stride, int32_t new_tokens, uint8_t* k_codes, float* k_scale,
         float* k_zero, uint8_t* v_codes, float* v_scale, float* v_zero, float* k_hist,
@@ -705,6 +664,9 @@ extern "C" int kivi_store_flush_chunks(
     if (new_dtype < kSrcF32 || new_dtype > kSrcF16)
         return set_error(kErrInvalidArgument, "new_dtype %d is not 0 (f32), 1 (bf16) or 2 (f16)",
                          new_dtype);
+    if (res_dtype < kSrcF32 || res_dtype > kSrcF16)
+        return set_error(kErrInvalidArgument, "res_dtype %d is not 0 (f32), 1 (bf16) or 2 (f16)",
+                         res_dtype);
     if (new_batch_stride < 0 || new_head_stride < 0 || new_token_stride < 0)
         return set_error(kErrInvalidArgument, "negative new-token strides");
     if (n_chunks <= 0 || n_chunks > 65535)
@@ -738,7 +700,7 @@ extern "C" int kivi_store_flush_chunks(
                 new_token_stride, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero,
                 k_hist, v_hist, hist_capacity, kv_heads, head_dim, group_size_k,
                 group_size_v, res_capacity, res_start, res_len, chunk_capacity, chunk_index,
-                n_chunks, 0, new_vec};
+                n_chunks, 0, new_vec, res_dtype};
     const dim3 grid(batch * kv_heads, n_chunks);
     hipStream_t st = (hipStream_t)stream;
     const bool fast_gv = group_size_v % 32 == 0 && group_size_v <= head_dim;
@@ -765,7 +727,8 @@ extern "C" int kivi_store_flush_chunks(
     return check_launch("store_flush");
 }
 
-extern "C" int kivi_store_flush(const float* k_res, const float* v_res, uint8_t* k_codes,
+extern "C" int kivi_store_flush(const void* k_res, const void* v_res, int32_t res_dtype,
+                                uint8_t* k_codes,
                                 float* k_scale, float* k_zero, uint8_t* v_codes,
                                 float* v_scale, float* v_zero, float* k_hist, float* v_hist,
                                 int64_t hist_capacity, int32_t batch, int32_t kv_heads,
@@ -773,7 +736,7 @@ extern "C" int kivi_store_flush(const float* k_res, const float* v_res, uint8_t*
                                 int32_t group_size_v, int32_t res_capacity,
                                 int32_t res_start, int32_t chunk_capacity,
                                 int32_t chunk_index, void* stream) {
-    return kivi_store_flush_chunks(k_res, v_res, nullptr, nullptr, kSrcF32, 0, 0, 0, 0,
+    return kivi_store_flush_chunks(k_res, v_res, res_dtype, nullptr, nullptr, kSrcF32, 0, 0, 0, 0,
                                    k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_hist,
                                    v_hist, hist_capacity, batch, kv_heads, head_dim,
                                    group_size_k, group_size_v, res_capacity, res_start,
@@ -782,8 +745,8 @@ extern "C" int kivi_store_flush(const float* k_res, const float* v_res, uint8_t*
 
 extern "C" int kivi_store_append(const void* k_new, const void* v_new, int32_t new_dtype,
                                  int64_t new_batch_stride, int64_t new_head_stride,
-                                 int64_t new_token_stride, int32_t new_tokens, float* k_res,
-                                 float* v_res, int32_t batch, int32_t kv_heads,
+                                 int64_t new_token_stride, int32_t new_tokens, void* k_res,
+                                 void* v_res, int32_t res_dtype, int32_t batch, int32_t kv_heads,
                                  int32_t head_dim, int32_t res_capacity, int32_t slot,
                                  void* stream) {
     if (!k_new || !v_new || !k_res || !v_res)
@@ -795,6 +758,10 @@ extern "C" int kivi_store_append(const void* k_new, const void* v_new, int32_t n
     if (new_dtype < kSrcF32 || new_dtype > kSrcF16)
         return set_error(kErrInvalidArgument, "new_dtype %d is not 0 (f32), 1 (bf16) or 2 (f16)",
                          new_dtype);
+    if (res_dtype != kSrcF32 && res_dtype != new_dtype)
+        return set_error(kErrInvalidArgument,
+                         "res_dtype %d: the ring is f32 (0) or of the new tokens' type (%d)",
+                         res_dtype, new_dtype);
     if (new_batch_stride < 0 || new_head_stride < 0 || new_token_stride < 0)
         return set_error(kErrInvalidArgument, "negative new-token strides");
     if (res_capacity <= 0 || slot < 0 || slot >= res_capacity)
@@ -815,10 +782,16 @@ extern "C" int kivi_store_append(const void* k_new, const void* v_new, int32_t n
                  new_tokens, res_capacity, slot, vec};
     const unsigned grid = (unsigned)((a.total + 255) / 256);
     hipStream_t st = (hipStream_t)stream;
-    switch (new_dtype) {
-        case kSrcBF16: append_kernel<kSrcBF16><<<grid, 256, 0, st>>>(a); break;
-        case kSrcF16: append_kernel<kSrcF16><<<grid, 256, 0, st>>>(a); break;
-        default: append_kernel<kSrcF32><<<grid, 256, 0, st>>>(a); break;
+    if (res_dtype == kSrcBF16) {
+        append_kernel<kSrcBF16, kSrcBF16><<<grid, 256, 0, st>>>(a);
+    } else if (res_dtype == kSrcF16) {
+        append_kernel<kSrcF16, kSrcF16><<<grid, 256, 0, st>>>(a);
+    } else {
+        switch (new_dtype) {
+            case kSrcBF16: append_kernel<kSrcBF16, kSrcF32><<<grid, 256, 0, st>>>(a); break;
+            case kSrcF16: append_kernel<kSrcF16, kSrcF32><<<grid, 256, 0, st>>>(a); break;
+            default: append_kernel<kSrcF32, kSrcF32><<<grid, 256, 0, st>>>(a); break;
+        }
     }
     return check_launch("store_append");
 }

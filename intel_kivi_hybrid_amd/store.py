@@ -5,8 +5,11 @@ CPU and sends one G-token chunk to the device per flush
 (src/kivi_sycl/cache/manager.py:100-118,309-374).  Here everything stays in
 device memory:
 
-* an fp32 residual ring ``[B, Hkv, R, D]`` (``res_start``/``res_len`` track
-  the window; a flush advances ``res_start`` by G instead of moving data);
+* a residual ring ``[B, Hkv, R, D]`` (``res_start``/``res_len`` track the
+  window; a flush advances ``res_start`` by G instead of moving data), fp32
+  like the reference's, or bf16/fp16 for a model whose K/V are of that type
+  (lossless for them: the kernels widen exactly, so results equal those of
+  an fp32 ring holding the same values);
 * the packed store (codes, scales, zeros per chunk of G tokens, layout in
   include/kivi_hip.h), grown geometrically;
 * optionally the dequantised history ``[B, Hkv, T, D]`` that
@@ -122,7 +125,8 @@ class PackedKVStore:
 
     def __init__(self, batch: int, kv_heads: int, head_dim: int, group_size: int,
                  residual_capacity: int, device, group_size_v: Optional[int] = None,
-                 chunk_capacity: int = 0, keep_history: bool = False):
+                 chunk_capacity: int = 0, keep_history: bool = False,
+                 residual_dtype: torch.dtype = torch.float32):
         if group_size <= 0 or group_size % 4:
             raise ValueError(f"group_size ({group_size}) must be >= 4 and divisible by 4")
         gv = group_size if group_size_v is None else group_size_v
@@ -130,14 +134,17 @@ class PackedKVStore:
             raise ValueError(f"head_dim ({head_dim}) must be divisible by group_size_v ({gv})")
         if residual_capacity < group_size:
             raise ValueError("residual capacity must hold at least one group")
+        if residual_dtype not in _SRC_DTYPES:
+            raise ValueError(f"residual_dtype must be float32, bfloat16 or float16, got "
+                             f"{residual_dtype}")
         self.B, self.H, self.D = batch, kv_heads, head_dim
         self.G, self.Gv, self.R = group_size, gv, residual_capacity
         # 1: codes stored in matrix-core operand order, 0: plain byte order
         self.code_layout = int(_lib.kivi_store_code_layout(head_dim, group_size, gv))
         self.device = torch.device(device)
         self.keep_history = keep_history
-        f32 = dict(dtype=torch.float32, device=self.device)
-        self.k_res = torch.zeros(batch, kv_heads, residual_capacity, head_dim, **f32)
+        self.k_res = torch.zeros(batch, kv_heads, residual_capacity, head_dim,
+                                 dtype=residual_dtype, device=self.device)
         self.v_res = torch.zeros_like(self.k_res)
         self.res_start = 0
         self.res_len = 0
@@ -187,12 +194,22 @@ class PackedKVStore:
     def quantized_tokens(self) -> int:
         return self.n_chunks * self.G
 
+    @property
+    def residual_dtype(self) -> torch.dtype:
+        return self.k_res.dtype
+
+    @property
+    def res_dtype_code(self) -> int:
+        """The ring's element type as the C ABI codes it (0 f32, 1 bf16, 2 f16)."""
+        return _SRC_DTYPES[self.k_res.dtype]
+
     def _launch_append(self, k: torch.Tensor, v: torch.Tensor, slot: int) -> None:
         sb, sh, st, _ = k.stride()
         with torch.cuda.device(self.device):
             _native.check(_lib.kivi_store_append(
                 _vp(k), _vp(v), _SRC_DTYPES[k.dtype], sb, sh, st, k.shape[2], _vp(self.k_res),
-                _vp(self.v_res), self.B, self.H, self.D, self.R, slot, _stream(self.device)),
+                _vp(self.v_res), self.res_dtype_code, self.B, self.H, self.D, self.R, slot,
+                _stream(self.device)),
                 "kivi_store_append")
 
     def _commit(self) -> None:
@@ -205,9 +222,10 @@ class PackedKVStore:
     def stage_token(self, k: torch.Tensor, v: torch.Tensor) -> None:
         """Add one new token ``[B, Hkv, 1, D]`` to the window.  It counts at
         once; its K/V are written by the next :meth:`attention` launch
-        itself, which reads them from ``k``/``v`` (fp32 rows 16-byte
-        aligned), or by a separate append when anything else reads the ring
-        first or the layout does not allow the fused path."""
+        itself, which reads them from ``k``/``v`` (rows of the ring's type
+        aligned to four elements), or by a separate append when anything
+        else reads the ring first or the inputs do not allow the fused
+        path."""
         k, v = self._token_source(k, v)
         if k.shape[2] != 1:
             raise ValueError(f"stage_token takes one token, got {k.shape[2]}")
@@ -215,8 +233,9 @@ class PackedKVStore:
         if self.res_len + 1 > self.R:
             raise RuntimeError(f"residual window overflow ({self.res_len} + 1 > {self.R})")
         sb, sh = k.stride(0), k.stride(1)
-        if k.dtype == torch.float32 and sb % 4 == 0 and sh % 4 == 0 and \
-                k.data_ptr() % 16 == 0 and v.data_ptr() % 16 == 0:
+        vb = 4 * k.element_size()
+        if k.dtype == self.k_res.dtype and sb % 4 == 0 and sh % 4 == 0 and \
+                k.data_ptr() % vb == 0 and v.data_ptr() % vb == 0:
             self._pending = (k, v)
             self.res_len += 1
         else:
@@ -224,9 +243,9 @@ class PackedKVStore:
 
     def append(self, k: torch.Tensor, v: torch.Tensor) -> None:
         """Copy new tokens ``[B, Hkv, n, D]`` into the residual window (one
-        launch for K and V; fp32/bf16/fp16 widened exactly, any strides with
-        contiguous channels).  The window must have room (callers flush
-        first)."""
+        launch for K and V; into an fp32 ring fp32/bf16/fp16 are widened
+        exactly; any strides with contiguous channels).  The window must have
+        room (callers flush first)."""
         self._commit()
         k, v = self._token_source(k, v)
         n = k.shape[2]
@@ -239,14 +258,18 @@ class PackedKVStore:
 
     def _token_source(self, k: torch.Tensor, v: torch.Tensor):
         """New tokens as the flush kernel reads them: on the store's device,
-        fp32/bf16/fp16, channels contiguous, K and V with the same strides
-        (copies are made only when the inputs are not already so)."""
+        fp32/bf16/fp16 (for a 16-bit ring: the ring's type, so that every
+        token is quantised from the value the ring would hold), channels
+        contiguous, K and V with the same strides (copies are made only when
+        the inputs are not already so)."""
         if k.shape != v.shape or k.dim() != 4 or tuple(k.shape[:2]) != (self.B, self.H) \
                 or k.shape[3] != self.D:
             raise ValueError(f"new tokens must be [B={self.B}, Hkv={self.H}, n, D={self.D}] for "
                              f"both K and V, got {tuple(k.shape)} and {tuple(v.shape)}")
         k, v = k.to(self.device), v.to(self.device)
-        if k.dtype not in _SRC_DTYPES or v.dtype != k.dtype:
+        if self.k_res.dtype != torch.float32:
+            k, v = k.to(self.k_res.dtype), v.to(self.k_res.dtype)
+        elif k.dtype not in _SRC_DTYPES or v.dtype != k.dtype:
             k, v = k.to(torch.float32), v.to(torch.float32)
         if k.stride(-1) != 1 or v.stride() != k.stride():
             k, v = k.contiguous(), v.contiguous()
@@ -294,7 +317,8 @@ class PackedKVStore:
         sb, sh, st, _ = k.stride()
         with torch.cuda.device(self.device):
             _native.check(_lib.kivi_store_flush_chunks(
-                _vp(self.k_res), _vp(self.v_res), _vp(k), _vp(v), _SRC_DTYPES[k.dtype],
+                _vp(self.k_res), _vp(self.v_res), self.res_dtype_code, _vp(k), _vp(v),
+                _SRC_DTYPES[k.dtype],
                 sb, sh, st, k.shape[2], _vp(self.k_codes), _vp(self.k_scale), _vp(self.k_zero),
                 _vp(self.v_codes), _vp(self.v_scale), _vp(self.v_zero), _vp(self.k_hist),
                 _vp(self.v_hist), hist_cap, self.B, self.H, self.D, self.G, self.Gv, self.R,
@@ -320,7 +344,8 @@ class PackedKVStore:
         hist_cap = self.capacity * self.G if self.keep_history else 0
         with torch.cuda.device(self.device):
             _native.check(_lib.kivi_store_flush(
-                _vp(self.k_res), _vp(self.v_res), _vp(self.k_codes), _vp(self.k_scale),
+                _vp(self.k_res), _vp(self.v_res), self.res_dtype_code, _vp(self.k_codes),
+                _vp(self.k_scale),
                 _vp(self.k_zero), _vp(self.v_codes), _vp(self.v_scale), _vp(self.v_zero),
                 _vp(self.k_hist), _vp(self.v_hist), hist_cap, self.B, self.H, self.D,
                 self.G, self.Gv, self.R, self.res_start, self.capacity, self.n_chunks,
@@ -384,8 +409,9 @@ class PackedKVStore:
           -- keys per channel, groups of G along the T quantised tokens;
         * ``v_codes [B, Hkv, T, D/4]`` u8, ``v_scale``/``v_zero [B, Hkv, T, D/Gv]``
           -- values per token, groups of Gv channels;
-        * ``k_residual``/``v_residual [B, Hkv, r, D]`` fp32, the residual
-          window in token order.
+        * ``k_residual``/``v_residual [B, Hkv, r, D]``, the residual window in
+          token order, in the ring's element type (fp32 unless the store was
+          built with a 16-bit ring).
 
         ``_C.dequantize_keys``/``dequantize_values`` (or the reference's
         own ops) turn the codes back into the served history."""
@@ -411,7 +437,8 @@ class PackedKVStore:
     def from_state(cls, state: dict, group_size: int, residual_capacity: int, device,
                    group_size_v: Optional[int] = None, chunk_capacity: int = 0) -> "PackedKVStore":
         """A store holding what :meth:`export_state` returned (tensors on any
-        device); codes are re-ordered into this build's code layout."""
+        device); codes are re-ordered into this build's code layout and the
+        ring takes the residuals' element type."""
         need = ("k_codes", "k_scale", "k_zero", "v_codes", "v_scale", "v_zero",
                 "k_residual", "v_residual")
         missing = [k for k in need if k not in state]
@@ -437,14 +464,15 @@ class PackedKVStore:
                                  f"{t.dtype} {tuple(t.shape)}")
         kr, vr = state["k_residual"], state["v_residual"]
         if kr.dim() != 4 or tuple(kr.shape[:2]) != (B, H) or kr.shape[3] != D or \
-                kr.shape != vr.shape or kr.dtype != torch.float32 or vr.dtype != torch.float32:
-            raise ValueError(f"residuals must be fp32 [B={B}, Hkv={H}, r, D={D}], got "
-                             f"{tuple(kr.shape)} and {tuple(vr.shape)}")
+                kr.shape != vr.shape or kr.dtype not in _SRC_DTYPES or vr.dtype != kr.dtype:
+            raise ValueError(f"residuals must be fp32, bf16 or fp16 [B={B}, Hkv={H}, r, D={D}] "
+                             f"of one type, got {kr.dtype} {tuple(kr.shape)} and {vr.dtype} "
+                             f"{tuple(vr.shape)}")
         if kr.shape[2] > residual_capacity:
             raise ValueError(f"residual of {kr.shape[2]} tokens exceeds capacity "
                              f"{residual_capacity}")
         st = cls(B, H, D, G, residual_capacity, device, group_size_v=gv,
-                 chunk_capacity=max(n, int(chunk_capacity)))
+                 chunk_capacity=max(n, int(chunk_capacity)), residual_dtype=kr.dtype)
         dev = st.device
         if n:
             kc = _unpack_last(state["k_codes"].to(dev)).reshape(B, H, D, n, G).permute(0, 1, 3, 4, 2)

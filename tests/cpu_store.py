@@ -12,8 +12,11 @@ from oracle.kivi_cache import roundtrip
 
 class CpuPackedStore:
     def __init__(self, batch, kv_heads, head_dim, group_size, residual_capacity, device,
-                 group_size_v=None, chunk_capacity=0, keep_history=False):
+                 group_size_v=None, chunk_capacity=0, keep_history=False,
+                 residual_dtype=torch.float32):
         self.B, self.H, self.D = batch, kv_heads, head_dim
+        # values are held widened to fp32 after rounding to the ring's type
+        self.residual_dtype = residual_dtype
         self.G = group_size
         self.Gv = group_size if group_size_v is None else group_size_v
         self.R = residual_capacity
@@ -39,8 +42,9 @@ class CpuPackedStore:
         n = k.shape[2]
         if self.res_len + n > self.R:
             raise RuntimeError(f"residual window overflow ({self.res_len} + {n} > {self.R})")
-        self.res_k = torch.cat([self.res_k, k.float().cpu()], dim=2)
-        self.res_v = torch.cat([self.res_v, v.float().cpu()], dim=2)
+        rd = self.residual_dtype
+        self.res_k = torch.cat([self.res_k, k.cpu().to(rd).float()], dim=2)
+        self.res_v = torch.cat([self.res_v, v.cpu().to(rd).float()], dim=2)
 
     def stage_token(self, k, v):
         self.append(k, v)

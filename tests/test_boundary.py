@@ -44,7 +44,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_error_string():
     from intel_kivi_hybrid_amd import _native
     lib = _native.load()
-    assert lib.kivi_abi_version() == 2
+    assert lib.kivi_abi_version() == 3
     # invalid arguments are rejected on the host, before any launch
     rc = lib.kivi_quantize_keys_per_channel(None, None, None, None, 4, 32, None)
     assert rc == 1 and "null" in _native.last_error()
@@ -172,27 +172,43 @@ def test_store_entry_points_reject_bad_arguments():
     lib = _native.load()
     buf = (ctypes.c_float * 64)()
     p = ctypes.addressof(buf)
-    # append: slot outside the ring, too many tokens, bad dtype code
-    rc = lib.kivi_store_append(p, p, 0, 0, 0, 0, 1, p, p, 1, 1, 8, 4, 4, None)
+    # append: slot outside the ring, too many tokens, bad dtype codes, a
+    # 16-bit ring fed another type
+    rc = lib.kivi_store_append(p, p, 0, 0, 0, 0, 1, p, p, 0, 1, 1, 8, 4, 4, None)
     assert rc == 1 and "slot 4 outside [0, 4)" in _native.last_error()
-    rc = lib.kivi_store_append(p, p, 0, 0, 0, 0, 5, p, p, 1, 1, 8, 4, 0, None)
+    rc = lib.kivi_store_append(p, p, 0, 0, 0, 0, 5, p, p, 0, 1, 1, 8, 4, 0, None)
     assert rc == 1 and "exceed the ring capacity" in _native.last_error()
-    rc = lib.kivi_store_append(p, p, 7, 0, 0, 0, 1, p, p, 1, 1, 8, 4, 0, None)
+    rc = lib.kivi_store_append(p, p, 7, 0, 0, 0, 1, p, p, 0, 1, 1, 8, 4, 0, None)
     assert rc == 1 and "new_dtype 7" in _native.last_error()
+    rc = lib.kivi_store_append(p, p, 0, 0, 0, 0, 1, p, p, 1, 1, 1, 8, 4, 0, None)
+    assert rc == 1 and "res_dtype 1" in _native.last_error()
     # flush of more chunks than the run holds
-    rc = lib.kivi_store_flush_chunks(p, p, p, p, 0, 0, 0, 8, 3, p, p, p, p, p, p, None, None, 0,
-                                     1, 1, 8, 4, 4, 8, 0, 2, 4, 0, 2, None)
+    rc = lib.kivi_store_flush_chunks(p, p, 0, p, p, 0, 0, 0, 8, 3, p, p, p, p, p, p, None, None,
+                                     0, 1, 1, 8, 4, 4, 8, 0, 2, 4, 0, 2, None)
     assert rc == 1 and "2 chunks of 4 need 8 tokens, 5 available" in _native.last_error()
     # chunk range beyond the capacity
-    rc = lib.kivi_store_flush_chunks(p, p, None, None, 0, 0, 0, 0, 0, p, p, p, p, p, p, None,
+    rc = lib.kivi_store_flush_chunks(p, p, 0, None, None, 0, 0, 0, 0, 0, p, p, p, p, p, p, None,
                                      None, 0, 1, 1, 8, 4, 4, 8, 0, 8, 2, 1, 2, None)
     assert rc == 1 and "outside capacity 2" in _native.last_error()
-    # fused append needs aligned new-token rows and a window holding the token
-    rc = lib.kivi_packed_decode_attention_append(p, p + 4, p, 0, 0, p, p, p, p, p, p, p, p, p,
-                                                 None, 0, 1, 4, 4, 64, 32, 32, 1, 0, 32, 0, 1,
+    # unknown ring type
+    rc = lib.kivi_store_flush_chunks(p, p, 3, None, None, 0, 0, 0, 0, 0, p, p, p, p, p, p, None,
+                                     None, 0, 1, 1, 8, 4, 4, 8, 0, 8, 2, 0, 1, None)
+    assert rc == 1 and "res_dtype 3" in _native.last_error()
+    # fused append needs aligned new-token rows (four elements of the ring's
+    # type) and a window holding the token
+    rc = lib.kivi_packed_decode_attention_append(p, p + 4, p, 0, 0, p, p, p, p, p, p, p, p, 0,
+                                                 p, None, 0, 1, 4, 4, 64, 32, 32, 1, 0, 32, 0, 1,
                                                  ctypes.c_float(0.1), 0, None)
     assert rc == 1 and "16-byte aligned" in _native.last_error()
-    rc = lib.kivi_packed_decode_attention_append(p, p, p, 0, 0, p, p, p, p, p, p, p, p, p,
+    rc = lib.kivi_packed_decode_attention_append(p, p + 4, p, 0, 0, p, p, p, p, p, p, p, p, 1,
+                                                 p, None, 0, 1, 4, 4, 64, 32, 32, 1, 0, 32, 0, 1,
+                                                 ctypes.c_float(0.1), 0, None)
+    assert rc == 1 and "8-byte aligned" in _native.last_error()
+    rc = lib.kivi_packed_decode_attention_append(p, p, p, 0, 0, p, p, p, p, p, p, p, p, 0, p,
                                                  None, 0, 1, 4, 4, 64, 32, 32, 1, 0, 32, 0, 0,
                                                  ctypes.c_float(0.1), 0, None)
     assert rc == 1 and "must hold the new token" in _native.last_error()
+    rc = lib.kivi_packed_decode_attention(p, p, p, p, p, p, p, p, p, 4, p, None, 0, 1, 4, 4,
+                                          64, 32, 32, 1, 0, 32, 0, 1, ctypes.c_float(0.1), 0,
+                                          None)
+    assert rc == 1 and "res_dtype 4" in _native.last_error()
