@@ -154,10 +154,12 @@ def decode_loop(st, Hq, steps, warmup, R, seed, device):
         total_bytes += nb
         total_flushes += fl
     t1.record()
+    submit = time.perf_counter() - wall0     # host time to issue the K steps
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     ms = t0.elapsed_time(t1)
-    return {"ms": ms, "wall_s": wall, "bytes": total_bytes, "flushes": total_flushes,
+    return {"ms": ms, "wall_s": wall, "submit_s": submit, "bytes": total_bytes,
+            "flushes": total_flushes,
             "gbs": total_bytes / (ms * 1e-3) / 1e9, "ms_per_step": ms / steps}
 
 
@@ -375,7 +377,8 @@ def main():
     log(f"[bench] config4 attention: {attn4['avg_us']:.1f} us, {attn4['gbs']:.0f} GB/s")
     loop = decode_loop(st, Hq, args.steps, args.warmup, R, 99, dev)
     log(f"[bench] config4 decode loop: {loop['ms_per_step'] * 1e3:.1f} us/step, "
-        f"{loop['gbs']:.0f} GB/s, {loop['flushes']} flushes")
+        f"{loop['gbs']:.0f} GB/s, {loop['flushes']} flushes (host issues a step in "
+        f"{loop['submit_s'] / args.steps * 1e6:.1f} us)")
     del st
     torch.cuda.empty_cache()
     if args.only == "config4":

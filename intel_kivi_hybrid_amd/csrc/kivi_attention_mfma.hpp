@@ -42,6 +42,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 #include "kivi_common.hpp"
 #include "kivi_attention.hpp"
 
@@ -445,21 +447,48 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // after the merge slots, and the combined residual state at the end.
     float* qres = reinterpret_cast<float*>(smem + S::MERGE_LDS);                // [HG][D]
     float* rstate = reinterpret_cast<float*>(smem + S::lds(NG) - S::RES_LDS);
-    for (int e = threadIdx.x; e < HG * D; e += kBlock)
-        qres[e] = a.q[((int64_t)b * a.Hq + kvh * HG) * D + e] * a.qscale;
     // The new token (if any) is read from its own tensor by the residual
-    // pass below; one wave of the first split also files it in the ring for
-    // later launches.  Nothing in this launch reads that ring slot.
+    // pass below; the first split also files it in the ring for later
+    // launches (nothing in this launch reads that ring slot).  Its loads are
+    // issued before the query's, so that both share one memory round trip
+    // before the barrier.
     const bool has_new = a.k_new != nullptr;
     const int64_t new_row = (int64_t)b * a.new_sb + (int64_t)kvh * a.new_sh;   // element offset
-    if (has_new && split == 0 && threadIdx.x < kWave) {
-        const int64_t dst = ((int64_t)bh * a.Rcap + a.new_slot) * D;
-        for (int e = threadIdx.x; e < D / 4; e += kWave) {
-            copy4_dt(const_cast<void*>(a.k_res), dst + 4 * e, a.k_new, new_row + 4 * e, a.res_dt);
-            copy4_dt(const_cast<void*>(a.v_res), dst + 4 * e, a.v_new, new_row + 4 * e, a.res_dt);
+    // Lane e < D/4 of the first split's last wave moves four elements of
+    // each row.  A wave waits for its stores to complete before it reuses
+    // their data registers (one memory round trip); the last wave has at
+    // most as many chunks as any other (they are dealt from wave 0) and the
+    // smallest residual slice, so the wait mostly stays off the critical path.
+    using Quad = typename std::conditional<R16, uint2, uint4>::type;
+    const bool copy_new = has_new && split == 0 && wave == kWaves - 1 && lane < D / 4;
+    Quad kn{}, vn{};
+    if (copy_new) {
+        kn = static_cast<const Quad*>(a.k_new)[new_row / 4 + lane];
+        vn = static_cast<const Quad*>(a.v_new)[new_row / 4 + lane];
+    }
+    // All of the thread's query loads are issued before any is used, so the
+    // fill costs one memory round trip.
+    {
+        constexpr int QN = (HG * D + kBlock - 1) / kBlock;
+        const float* qg = a.q + ((int64_t)b * a.Hq + kvh * HG) * D;
+        float qt[QN];
+#pragma unroll
+        for (int i = 0; i < QN; ++i) qt[i] = qg[min((int)threadIdx.x + i * kBlock, HG * D - 1)];
+#pragma unroll
+        for (int i = 0; i < QN; ++i) {
+            const int e = threadIdx.x + i * kBlock;
+            if (e < HG * D) qres[e] = qt[i] * a.qscale;
         }
     }
     __syncthreads();
+    // After the barrier: the barrier waits for every outstanding vector
+    // memory operation, stores included, so stores before it would cost a
+    // round trip of their own; here they complete alongside the loads below.
+    if (copy_new) {
+        const int64_t o = ((int64_t)bh * a.Rcap + a.new_slot) * (D / 4) + lane;
+        static_cast<Quad*>(const_cast<void*>(a.k_res))[o] = kn;
+        static_cast<Quad*>(const_cast<void*>(a.v_res))[o] = vn;
+    }
 
     // W-prep lane: head wh, channels [wseg*CPL, +CPL).
     const bool wlane = lane < HG * S::LPH;
@@ -769,6 +798,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             if constexpr (R16) return load4_16(p, i, res_half);
             else return load4_vec<kSrcF32>(p, i);
         };
+
         for (int t0 = r0; t0 < r1; t0 += kResPass) {
             const int n = min(kResPass, r1 - t0);
             // scores: lane (tk, qq) takes channel quads qq, qq+4, ... of token tk's row
@@ -952,16 +982,20 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     merge_and_store<HG, D>(smem, rstate, a, split, kvh, b);
 }
 
-// Occupancy target: two waves per SIMD where the 4-deep prefetch ring fits
-// that register budget without spilling (head_dim 64, or head_dim 128 with
-// up to 4 query heads per kv head); that measured faster than three waves
-// with a 2-deep ring.  Larger shapes keep the full register file (one wave
-// per SIMD).
-template <int HG, int D>
-constexpr int attn_waves_per_eu() { return (D <= 64 || (D <= 128 && HG <= 4)) ? 2 : 1; }
+// Occupancy target: four waves per SIMD for head_dim 64 with G=32 and up to 4
+// query heads per kv head (the kernel fits 128 VGPRs there without spilling;
+// left to itself the compiler's choice lands on either side of 128 as
+// unrelated code changes); two where the 4-deep prefetch ring fits that
+// register budget without spilling (head_dim 64, or head_dim 128 with up to
+// 4 query heads per kv head), which measured faster than three waves with a
+// 2-deep ring.  Larger shapes keep the full register file (one wave per SIMD).
+template <int HG, int D, int G>
+constexpr int attn_waves_per_eu() {
+    return (D <= 64 && G <= 32 && HG <= 4) ? 4 : (D <= 64 || (D <= 128 && HG <= 4)) ? 2 : 1;
+}
 
 template <int HG, int D, int G, int NGC, bool R16>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<HG, D>())))
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<HG, D, G>())))
 void attn_mfma_kernel(AttnLaunch a) {
     extern __shared__ __align__(16) unsigned char smem[];
     using S = Shape<HG, D, G>;

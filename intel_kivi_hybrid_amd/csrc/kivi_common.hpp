@@ -255,19 +255,6 @@ __device__ __forceinline__ float load1_dt(const void* p, int64_t i, int dt) {
     return widen<kSrcF32>(p, i);
 }
 
-// Copies four elements of type dt, src[si..si+3] -> dst[di..di+3], bit for
-// bit (offsets aligned as for load4_vec).
-__device__ __forceinline__ void copy4_dt(void* dst, int64_t di, const void* src, int64_t si,
-                                         int dt) {
-    if (dt == kSrcF32) {
-        *reinterpret_cast<float4*>(static_cast<float*>(dst) + di) =
-            *reinterpret_cast<const float4*>(static_cast<const float*>(src) + si);
-    } else {
-        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(dst) + di) =
-            *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(src) + si);
-    }
-}
-
 // x_hat = fl(fl(q * scale) + zero) (dequantize_kernels.cpp:24).
 __device__ __forceinline__ float decode1(uint32_t q, float scale, float zero) {
     return __fadd_rn(__fmul_rn((float)q, scale), zero);
