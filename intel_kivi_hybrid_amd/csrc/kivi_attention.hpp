@@ -23,7 +23,6 @@ struct AttnLaunch {
     int B, Hq, Hkv, D, G, Gv, Cmax, n_chunks, Rcap, res_start, res_len;
     int n_qsplits;           // workgroups per (b, kv-head)
     int chunks_per_wave;     // packed chunks per wave
-    int res_per_wave;        // residual tokens per wave
     int n_splits;            // partial states per row (= n_qsplits)
     float qscale;            // softmax scale * log2(e)
     // Optional new token, the window's last (index res_len - 1): when k_new

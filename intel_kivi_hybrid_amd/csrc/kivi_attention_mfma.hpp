@@ -784,9 +784,16 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             orr[h][0] = orr[h][1] = orr[h][2] = orr[h][3] = 0.f;
         }
         float* pres = qres + HG * D + wave * HG * kResPass;                      // [HG][16]
-        const int wave_idx = split * kWaves + wave;
-        const int r0 = min(wave_idx * a.res_per_wave, a.res_len);
-        const int r1 = min(r0 + a.res_per_wave, a.res_len);
+        // The window is dealt in whole passes, and in reverse wave order:
+        // chunks are dealt from wave 0 of split 0, so the waves that may hold
+        // one chunk fewer take the extra passes.
+        const int n_waves = a.n_qsplits * kWaves;
+        const int widx = n_waves - 1 - (split * kWaves + wave);
+        const int n_pass = (a.res_len + kResPass - 1) / kResPass;
+        const int pbase = n_pass / n_waves, pextra = n_pass % n_waves;
+        const int p0 = widx * pbase + min(widx, pextra);
+        const int r0 = min(p0 * kResPass, a.res_len);
+        const int r1 = min((p0 + pbase + (widx < pextra ? 1 : 0)) * kResPass, a.res_len);
         const int tk = lane / 4, qq = lane % 4;
         const int c4 = lane % F4, ts = lane / F4;
         // Four channels of a ring row widened to fp32.  The ring's width is
