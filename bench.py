@@ -34,6 +34,14 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0
 
 
+# HBM bytes that one config-4 attention launch (Tq=8096, Tr=96; 583,008,256
+# algorithmic bytes) moves: rocprofv3 --pmc FETCH_SIZE x 2.00 + WRITE_SIZE
+# x 1.00 per dispatch, the factors calibrated on a 512 MiB copy
+# (profiles/attn_mfma_config4.md).  Reported only for that exact workload.
+ATTN4_ALGO_BYTES = 583_008_256
+ATTN4_TRAFFIC_BYTES = 583_480_320
+
+
 def attn_bytes(B, Hq, Hkv, D, Tq, Tr, Gk, Gv):
     per = (D * Tq // 4 + 8 * D * Tq // Gk + Tq * D // 4 + 8 * Tq * D // Gv
            + 8 * Tr * D + 8 * (Hq // Hkv) * D)
@@ -93,22 +101,29 @@ def settle_clocks(fn, seconds=0.05, min_calls=20):
     torch.cuda.synchronize()
 
 
-def time_attention(st, Hq, iters, seed, device):
-    """Average duration of one fused-attention call (HIP events on the launch
-    stream), and its algorithmic bytes."""
+def time_attention(st, Hq, iters, seed, device, blocks=5):
+    """Average duration of one fused-attention call and its algorithmic
+    bytes.  HIP events on the launch stream bracket blocks of back-to-back
+    calls (the host issues a call in a fraction of its GPU time, so the queue
+    never drains): a block's time per call is the kernel's duration plus the
+    launch gap, without the host latency that per-call event pairs add."""
     import torch
     g = torch.Generator(device=device).manual_seed(seed)
     q = torch.randn(st.B, Hq, st.D, generator=g, device=device) * st.D ** -0.5
     out = torch.empty_like(q)
     settle_clocks(lambda: st.attention(q, out=out))
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(iters)]
-    for i in range(iters):
-        starts[i].record()
-        st.attention(q, out=out)
-        ends[i].record()
-    torch.cuda.synchronize()
-    ms = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    per_block = max(1, iters // blocks)
+    ms = []
+    for _ in range(blocks):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(per_block):
+            st.attention(q, out=out)
+        e1.record()
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1) / per_block)
+    ms.sort()
     avg = sum(ms) / len(ms)
     nbytes = attn_bytes(st.B, Hq, st.H, st.D, st.quantized_tokens, st.res_len, st.G, st.Gv)
     return {"avg_us": avg * 1e3, "median_us": ms[len(ms) // 2] * 1e3, "bytes": nbytes,
@@ -443,7 +458,8 @@ def main():
         "quantize_max_err_over_scale": round(qb["max_err_over_scale"], 4),
         "roofline": {"bound": "hbm", "achieved": round(attn4["gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(attn4["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(attn4["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": ATTN4_TRAFFIC_BYTES if attn4["bytes"] == ATTN4_ALGO_BYTES else None,
                      "kernel": "packed decode attention (config 4, one call)",
                      "avg_us": round(attn4["avg_us"], 2), "bytes_per_launch": attn4["bytes"]},
         "cpu_baseline": cpu,
