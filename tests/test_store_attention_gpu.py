@@ -108,6 +108,10 @@ def test_attention_reference_cosine_gate(store_cls, kat):
     (1, 16, 2, 128, 64, 64, 128, 2000),     # GQA 8, G=64
     (2, 4, 4, 256, 64, 256, 64, 700),       # MHA, D=256, one value group per token
     (3, 8, 4, 64, 32, 64, 96, 1500),        # D=64, Gv=64
+    (2, 8, 2, 64, 32, 32, 64, 1200),        # D=64, G=32, GQA 4 (4 waves per SIMD)
+    (2, 4, 2, 64, 32, 32, 64, 900),         # D=64, G=32, GQA 2 (4 waves per SIMD)
+    (1, 4, 4, 64, 32, 32, 48, 700),         # D=64, G=32, MHA (4 waves per SIMD)
+    (1, 16, 2, 64, 32, 32, 64, 800),        # D=64, G=32, GQA 8
 ])
 def test_attention_matrix_core_shapes(store_cls, B, Hq, Hkv, D, G, Gv, R, T):
     """Every matrix-core instantiation family against float64 attention."""

@@ -30,6 +30,7 @@ CASES = [
     (1, 8, 8, 128, 32, 32, 96, 500, 40, 4),     # split partials + merge
     (1, 4, 2, 256, 64, 64, 128, 300, 70, 0),    # untiled generic flush (G*D > tile)
     (2, 4, 2, 128, 16, 16, 32, 90, 40, 0),      # plain code order: generic kernels
+    (2, 8, 2, 64, 32, 32, 64, 150, 70, 0),      # D=64, G=32 (4 waves per SIMD)
 ]
 
 
