@@ -261,16 +261,20 @@ struct Shape {
     static constexpr int RSTATE = HG * D + 2 * HG;
     static constexpr int MERGE_LDS = kWaves * RSTATE * 4;
     // residual pass: scaled q [HG][D] and per-wave probabilities [HG][16].
-    // They are live only before the chunk loop, so they sit in the per-wave
-    // regions, past the merge slots that the residual pass writes.
+    // They sit in the last wave's region, which that wave uses for chunks
+    // only after its residual pass (the last wave takes the whole window when
+    // one wave does), past the merge slots that the passes of all waves may
+    // write.
     static constexpr int QRES_LDS = HG * D * 4 + kWaves * HG * kResPass * 4;
-    static constexpr int SHARED_LDS = MERGE_LDS + QRES_LDS;
+    __host__ __device__ static constexpr int qres_off(int NG) { return (kWaves - 1) * wave_lds(NG); }
     // the combined state of the workgroup's residual slices, kept to the end
     static constexpr int RES_LDS = RSTATE * 4;
     __host__ __device__ static constexpr int lds(int NG) {
-        return (kWaves * wave_lds(NG) > SHARED_LDS ? kWaves * wave_lds(NG) : SHARED_LDS) + RES_LDS;
+        return (kWaves * wave_lds(NG) > MERGE_LDS ? kWaves * wave_lds(NG) : MERGE_LDS) + RES_LDS;
     }
     static_assert(NP >= 1 && LPH * CPL == D && CPL % 2 == 0, "shape");
+    // NG = 1 gives the smallest per-wave region
+    static_assert(QRES_LDS <= wave_lds(1) && MERGE_LDS <= qres_off(1), "residual buffers");
 };
 
 // Writes this wave's state (o unnormalised over D channels, m, l) to the
@@ -445,7 +449,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
 
     // Residual pass buffers (scaled q of the group, per-wave probabilities)
     // after the merge slots, and the combined residual state at the end.
-    float* qres = reinterpret_cast<float*>(smem + S::MERGE_LDS);                // [HG][D]
+    float* qres = reinterpret_cast<float*>(smem + S::qres_off(NG));             // [HG][D]
     float* rstate = reinterpret_cast<float*>(smem + S::lds(NG) - S::RES_LDS);
     // The new token (if any) is read from its own tensor by the residual
     // pass below; the first split also files it in the ring for later
@@ -502,11 +506,22 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // The workgroup's chunks [g_begin, g_end) are dealt to its waves in turn
     // (wave w takes g_begin + w + kWaves*j): the four waves of a workgroup
     // then read neighbouring chunks, which streams from HBM measurably faster
-    // than four separate contiguous ranges.
+    // than four separate contiguous ranges.  When the last wave takes the
+    // whole residual window (res_waves == 1), the first 3*early_chunks chunks
+    // are dealt to the other three waves only, while it works on the window.
+    const bool res_one = a.res_waves == 1;
     const int g_begin = split * kWaves * a.chunks_per_wave;
     const int g_end = min(g_begin + kWaves * a.chunks_per_wave, a.n_chunks);
-    const int n_mine = max(0, (g_end - g_begin - wave + kWaves - 1) / kWaves);
-    auto chunk_of = [&](int j) { return g_begin + wave + kWaves * min(j, n_mine - 1); };
+    const int g_cnt = max(0, g_end - g_begin);
+    const int s_early = res_one ? min((kWaves - 1) * a.early_chunks, g_cnt) : 0;
+    const int n_early = wave < kWaves - 1 ? (s_early - wave + kWaves - 2) / (kWaves - 1) : 0;
+    const int n_mine = n_early + max(0, (g_cnt - s_early - wave + kWaves - 1) / kWaves);
+    const int early_base = g_begin + wave;                               // + 3j
+    const int late_base = g_begin + s_early + wave - kWaves * n_early;   // + 4j
+    auto chunk_of = [&](int j) {
+        const int jj = min(j, n_mine - 1);
+        return jj < n_early ? early_base + (kWaves - 1) * jj : late_base + kWaves * jj;
+    };
 
     f32x4_t O[S::NBV];
 #pragma unroll
@@ -786,9 +801,11 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         float* pres = qres + HG * D + wave * HG * kResPass;                      // [HG][16]
         // The window is dealt in whole passes, and in reverse wave order:
         // chunks are dealt from wave 0 of split 0, so the waves that may hold
-        // one chunk fewer take the extra passes.
-        const int n_waves = a.n_qsplits * kWaves;
-        const int widx = n_waves - 1 - (split * kWaves + wave);
+        // one chunk fewer take the extra passes.  With res_waves == 1 only
+        // the last wave of each split takes passes.
+        const int n_waves = a.n_qsplits * (res_one ? 1 : kWaves);
+        const int widx = res_one ? (wave == kWaves - 1 ? n_waves - 1 - split : n_waves)
+                                 : n_waves - 1 - (split * kWaves + wave);
         const int n_pass = (a.res_len + kResPass - 1) / kResPass;
         const int pbase = n_pass / n_waves, pextra = n_pass % n_waves;
         const int p0 = widx * pbase + min(widx, pextra);
@@ -886,15 +903,19 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                 for (int i = 0; i < 4; ++i) orr[h][i] += __shfl_xor(orr[h][i], sh);
             }
         }
-        float* rst = merge_slot(smem, HG, D, wave);
-        if (lane < F4) {
+        // (res_waves == 1: the last wave's state is the workgroup's residual
+        // state, written straight to rstate; nobody waits for it before the
+        // final merge)
+        float* rst = res_one ? rstate : merge_slot(smem, HG, D, wave);
+        const bool keep = !res_one || wave == kWaves - 1;
+        if (keep && lane < F4) {
 #pragma unroll
             for (int h = 0; h < HG; ++h) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) rst[h * D + 4 * lane + i] = orr[h][i];
             }
         }
-        if (lane == 0) {
+        if (keep && lane == 0) {
 #pragma unroll
             for (int h = 0; h < HG; ++h) {
                 rst[HG * D + h] = mr[h];
@@ -902,7 +923,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             }
         }
     }
-    combine_residual<HG, D>(smem, rstate);
+    if (!res_one) combine_residual<HG, D>(smem, rstate);
 
     // Zero the A operands once: the zero row and correction columns >= LPH
     // are never written and must read as 0.
