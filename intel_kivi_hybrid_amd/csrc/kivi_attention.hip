@@ -312,7 +312,7 @@ __global__ __launch_bounds__(kMaxD) void attn_merge_kernel(const float* __restri
 struct Plan {
     int layout;
     int n_units, n_splits, units_per_split;   // generic kernel
-    int n_qsplits, chunks_per_wave, res_waves, early_chunks;   // matrix-core kernel
+    int n_qsplits, chunks_per_wave, res_waves, early_per_pass_x2;   // matrix-core kernel
 };
 
 Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
@@ -333,8 +333,8 @@ Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
         // The residual window is taken in whole 16-token passes.  With
         // enough chunks per wave, the last wave of each workgroup takes all of
         // its split's passes while the other three start on chunks, taking
-        // about kPassChunks chunks each per pass up front; otherwise every
-        // wave takes passes before its chunks.
+        // 2.5 chunks each per pass up front (measured best at config 4);
+        // otherwise every wave takes passes before its chunks.
         if (n_chunks > 0) {
             S = max(1, min(S, (n_chunks + kWavesPerGroup - 1) / kWavesPerGroup));
             p.chunks_per_wave = (n_chunks + kWavesPerGroup * S - 1) / (kWavesPerGroup * S);
@@ -346,15 +346,13 @@ Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
                                      (res_len + 16 * kWavesPerGroup - 1) / (16 * kWavesPerGroup)));
         }
         constexpr int kMinChunksForOneResWave = 16;
-        constexpr float kPassChunks = 2.5f;       // chunk steps per residual pass (measured)
-        const int n_pass = (res_len + 15) / 16;
-        const int pass_per_split = (n_pass + p.n_qsplits - 1) / p.n_qsplits;
-        if (n_pass > 0 && p.chunks_per_wave >= kMinChunksForOneResWave) {
+        constexpr int kEarlyPerPassX2 = 5;        // 2.5 chunk steps per residual pass
+        if (res_len > 0 && p.chunks_per_wave >= kMinChunksForOneResWave) {
             p.res_waves = 1;
-            p.early_chunks = min((int)(kPassChunks * pass_per_split + 0.5f), p.chunks_per_wave / 2);
+            p.early_per_pass_x2 = kEarlyPerPassX2;
         } else {
             p.res_waves = kWavesPerGroup;
-            p.early_chunks = 0;
+            p.early_per_pass_x2 = 0;
         }
         p.n_splits = p.n_qsplits;
         return p;
@@ -488,7 +486,7 @@ static int decode_attention_impl(const float* q, const uint8_t* k_codes, const f
         AttnLaunch L{q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res, v_res, out,
                      part_o, part_ml, batch, q_heads, kv_heads, head_dim, group_size_k,
                      group_size_v, chunk_capacity, num_chunks, res_capacity, res_start, res_len,
-                     p.n_qsplits, p.chunks_per_wave, p.res_waves, p.early_chunks, p.n_splits,
+                     p.n_qsplits, p.chunks_per_wave, p.res_waves, p.early_per_pass_x2, p.n_splits,
                      softmax_scale * kLog2e, k_new, v_new, new_sb, new_sh, new_slot, res_dtype};
         int rc = launch_attention_mfma(L, st);
         if (rc || !needs_workspace(p)) return rc;

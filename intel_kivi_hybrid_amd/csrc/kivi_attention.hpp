@@ -24,7 +24,7 @@ struct AttnLaunch {
     int n_qsplits;           // workgroups per (b, kv-head)
     int chunks_per_wave;     // packed chunks per wave
     int res_waves;           // waves per workgroup that take residual passes (1: the last)
-    int early_chunks;        // res_waves == 1: chunks each other wave takes first
+    int early_per_pass_x2;   // res_waves == 1: twice the chunks each other wave takes first per residual pass
     int n_splits;            // partial states per row (= n_qsplits)
     float qscale;            // softmax scale * log2(e)
     // Optional new token, the window's last (index res_len - 1): when k_new

@@ -510,10 +510,23 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // whole residual window (res_waves == 1), the first 3*early_chunks chunks
     // are dealt to the other three waves only, while it works on the window.
     const bool res_one = a.res_waves == 1;
+    // Residual passes: the window is dealt in whole passes, and in reverse
+    // wave order (chunks are dealt from wave 0 of split 0, so the waves that
+    // may hold one chunk fewer take the extra passes).  With res_waves == 1
+    // only the last wave of each split takes passes.
+    const int n_res_waves = a.n_qsplits * (res_one ? 1 : kWaves);
+    const int widx = res_one ? (wave == kWaves - 1 ? n_res_waves - 1 - split : n_res_waves)
+                             : n_res_waves - 1 - (split * kWaves + wave);
+    const int n_pass = (a.res_len + kResPass - 1) / kResPass;
+    const int pbase = n_pass / n_res_waves, pextra = n_pass % n_res_waves;
+    // passes of this split's last wave when it alone takes them
+    const int split_passes = pbase + (n_res_waves - 1 - split < pextra ? 1 : 0);
     const int g_begin = split * kWaves * a.chunks_per_wave;
     const int g_end = min(g_begin + kWaves * a.chunks_per_wave, a.n_chunks);
     const int g_cnt = max(0, g_end - g_begin);
-    const int s_early = res_one ? min((kWaves - 1) * a.early_chunks, g_cnt) : 0;
+    // early chunks per other wave: early_per_pass_x2 / 2 per pass, rounded
+    const int early = min((a.early_per_pass_x2 * split_passes + 1) / 2, a.chunks_per_wave / 2);
+    const int s_early = res_one ? min((kWaves - 1) * early, g_cnt) : 0;
     const int n_early = wave < kWaves - 1 ? (s_early - wave + kWaves - 2) / (kWaves - 1) : 0;
     const int n_mine = n_early + max(0, (g_cnt - s_early - wave + kWaves - 1) / kWaves);
     const int early_base = g_begin + wave;                               // + 3j
@@ -799,15 +812,6 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             orr[h][0] = orr[h][1] = orr[h][2] = orr[h][3] = 0.f;
         }
         float* pres = qres + HG * D + wave * HG * kResPass;                      // [HG][16]
-        // The window is dealt in whole passes, and in reverse wave order:
-        // chunks are dealt from wave 0 of split 0, so the waves that may hold
-        // one chunk fewer take the extra passes.  With res_waves == 1 only
-        // the last wave of each split takes passes.
-        const int n_waves = a.n_qsplits * (res_one ? 1 : kWaves);
-        const int widx = res_one ? (wave == kWaves - 1 ? n_waves - 1 - split : n_waves)
-                                 : n_waves - 1 - (split * kWaves + wave);
-        const int n_pass = (a.res_len + kResPass - 1) / kResPass;
-        const int pbase = n_pass / n_waves, pextra = n_pass % n_waves;
         const int p0 = widx * pbase + min(widx, pextra);
         const int r0 = min(p0 * kResPass, a.res_len);
         const int r1 = min((p0 + pbase + (widx < pextra ? 1 : 0)) * kResPass, a.res_len);
