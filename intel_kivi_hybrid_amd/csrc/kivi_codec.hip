@@ -24,7 +24,9 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kUnroll = 4;
-constexpr int kQuantVPL = 2;        // float4s per thread in quantize_vec_kernel
+constexpr int kQuantVPL = 2;        // float4s per segment in quantize_vec_kernel
+constexpr int kQuantIters = 1;      // segments per thread in quantize_vec_kernel (2 and 4
+                                    // measured slower at config 2: 230 and 237 us per pair)
 
 __device__ __forceinline__ void min_max4(const float4& v, float& mn, float& mx) {
     mn = fmin_nan(fmin_nan(v.x, v.y), fmin_nan(v.z, v.w));
@@ -64,45 +66,62 @@ __global__ __launch_bounds__(kBlock) void quantize_seg_kernel(
     }
 }
 
-// Segment kernels: thread t owns VPL consecutive float4s (a "segment") of a
-// group, LANES = G/(4*VPL) adjacent lanes per group.  Larger segments mean
-// fewer cross-lane reduction steps and fewer scale divisions per element;
-// each load instruction then reads 16 bytes per lane at a VPL*16-byte stride.
-template <int LANES, int VPL>
+// Segment kernels: a segment is VPL consecutive float4s of a group, LANES =
+// G/(4*VPL) adjacent lanes per group.  Larger segments mean fewer cross-lane
+// reduction steps and fewer scale divisions per element; each load
+// instruction then reads 16 bytes per lane at a VPL*16-byte stride.  A thread
+// takes ITERS segments one grid stride apart, all loads issued first, so
+// that a wave has more bytes in flight at the same coalescing.
+template <int LANES, int VPL, int ITERS>
 __global__ __launch_bounds__(kBlock) void quantize_vec_kernel(
     const float4* __restrict__ in, uint8_t* __restrict__ packed,
     float* __restrict__ scales, float* __restrict__ zeros, int64_t n_seg) {
-    const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-    if (t >= n_seg) return;              // groups are whole: n_seg % LANES == 0
-    float4 v[VPL];
+    const int64_t t0 = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * kBlock;   // a multiple of LANES
+    // Groups are whole (n_seg % LANES == 0) and a group's lanes share an
+    // iteration, so a group is either wholly in range or wholly past it;
+    // past-the-end lanes reload the last segment and store nothing.
+    float4 v[ITERS][VPL];
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) v[j] = in[t * VPL + j];
-    float mn, mx, scale;
-    min_max4(v[0], mn, mx);
+    for (int u = 0; u < ITERS; ++u) {
+        const int64_t t = min(t0 + u * stride, n_seg - 1);
 #pragma unroll
-    for (int j = 1; j < VPL; ++j) {
-        float a, b;
-        min_max4(v[j], a, b);
-        mn = fmin_nan(mn, a);
-        mx = fmax_nan(mx, b);
+        for (int j = 0; j < VPL; ++j) v[u][j] = in[t * VPL + j];
     }
-    seg_min_max<LANES>(mn, mx);
-    finish_group(mn, mx, scale);
-    uint32_t bytes[VPL];
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) bytes[j] = encode4(v[j].x, v[j].y, v[j].z, v[j].w, mn, scale);
-    if constexpr (VPL % 4 == 0) {
+    for (int u = 0; u < ITERS; ++u) {
+        const int64_t t = t0 + u * stride;
+        float mn, mx, scale;
+        min_max4(v[u][0], mn, mx);
 #pragma unroll
-        for (int j = 0; j < VPL; j += 4)
-            reinterpret_cast<uint32_t*>(packed + t * VPL)[j / 4] =
-                bytes[j] | (bytes[j + 1] << 8) | (bytes[j + 2] << 16) | (bytes[j + 3] << 24);
-    } else {
+        for (int j = 1; j < VPL; ++j) {
+            float a, b;
+            min_max4(v[u][j], a, b);
+            mn = fmin_nan(mn, a);
+            mx = fmax_nan(mx, b);
+        }
+        seg_min_max<LANES>(mn, mx);
+        finish_group(mn, mx, scale);
+        uint32_t bytes[VPL];
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) packed[t * VPL + j] = (uint8_t)bytes[j];
-    }
-    if ((threadIdx.x & (LANES - 1)) == 0) {
-        scales[t / LANES] = scale;
-        zeros[t / LANES] = mn;
+        for (int j = 0; j < VPL; ++j)
+            bytes[j] = encode4(v[u][j].x, v[u][j].y, v[u][j].z, v[u][j].w, mn, scale);
+        if (t >= n_seg) continue;
+        if constexpr (VPL % 4 == 0) {
+#pragma unroll
+            for (int j = 0; j < VPL; j += 4)
+                reinterpret_cast<uint32_t*>(packed + t * VPL)[j / 4] =
+                    bytes[j] | (bytes[j + 1] << 8) | (bytes[j + 2] << 16) | (bytes[j + 3] << 24);
+        } else if constexpr (VPL == 2) {
+            reinterpret_cast<uint16_t*>(packed)[t] = (uint16_t)(bytes[0] | (bytes[1] << 8));
+        } else {
+#pragma unroll
+            for (int j = 0; j < VPL; ++j) packed[t * VPL + j] = (uint8_t)bytes[j];
+        }
+        if ((threadIdx.x & (LANES - 1)) == 0) {
+            scales[t / LANES] = scale;
+            zeros[t / LANES] = mn;
+        }
     }
 }
 
@@ -245,12 +264,12 @@ int launch_quantize_groups(const float* in, uint8_t* packed, float* scales, floa
     const int64_t n_vec = n_groups * lanes;
     const bool pow2 = (lanes & (lanes - 1)) == 0 && lanes <= kWave;
     if (pow2 && aligned16(in) && lanes >= kQuantVPL && kQuantVPL > 1 &&
-        ((uintptr_t)packed % (kQuantVPL >= 4 ? 4 : 1)) == 0) {
+        ((uintptr_t)packed % (kQuantVPL >= 4 ? 4 : kQuantVPL)) == 0) {
         const int64_t n_seg = n_vec / kQuantVPL;
-        const unsigned grid = grid_for(n_seg, kBlock);
+        const unsigned grid = grid_for(n_seg, kBlock * kQuantIters);
         const float4* in4 = reinterpret_cast<const float4*>(in);
         switch (lanes / kQuantVPL) {
-#define KIVI_QV(L) case L: quantize_vec_kernel<L, kQuantVPL><<<grid, kBlock, 0, stream>>>(in4, packed, scales, zeros, n_seg); break;
+#define KIVI_QV(L) case L: quantize_vec_kernel<L, kQuantVPL, kQuantIters><<<grid, kBlock, 0, stream>>>(in4, packed, scales, zeros, n_seg); break;
             KIVI_QV(1) KIVI_QV(2) KIVI_QV(4) KIVI_QV(8) KIVI_QV(16) KIVI_QV(32) KIVI_QV(64)
 #undef KIVI_QV
         }
