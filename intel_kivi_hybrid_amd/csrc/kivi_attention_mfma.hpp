@@ -951,8 +951,17 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         if (has_next) wprep(Int<nslot>{});
         pprep(Int<slot>{}, any_cur);
         wave_sync();
+        // A wave in its matrix-core phase (value MFMAs, then the next chunk's
+        // scores and softmax) runs at a raised priority, so that when both
+        // waves of a SIMD are ready the one whose MFMA chain and softmax gate
+        // the next step goes first and the other's operand prep fills in.
+        // Measured 3.3 % faster at config 4 and 5.5 % at config 5 (in-process
+        // A/B); raising it around the ring loads, or over the prep phase
+        // instead, did not help.
+        __builtin_amdgcn_s_setprio(2);
         vside(cur);
         if (has_next) any_cur = kside(nxt, Int<nslot>{});
+        __builtin_amdgcn_s_setprio(0);
     };
     static_assert(PF % 2 == 0, "the slot parity of a ring step must be static");
     for (int c0 = 0; c0 < n_full; c0 += PF) {
