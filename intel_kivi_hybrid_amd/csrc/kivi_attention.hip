@@ -333,7 +333,7 @@ Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
         // The residual window is taken in whole 16-token passes.  With
         // enough chunks per wave, the last wave of each workgroup takes all of
         // its split's passes while the other three start on chunks, taking
-        // 2.5 chunks each per pass up front (measured best at config 4);
+        // 3 chunks each per pass up front (measured best at config 4);
         // otherwise every wave takes passes before its chunks.
         if (n_chunks > 0) {
             S = max(1, min(S, (n_chunks + kWavesPerGroup - 1) / kWavesPerGroup));
@@ -346,7 +346,7 @@ Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
                                      (res_len + 16 * kWavesPerGroup - 1) / (16 * kWavesPerGroup)));
         }
         constexpr int kMinChunksForOneResWave = 16;
-        constexpr int kEarlyPerPassX2 = 5;        // 2.5 chunk steps per residual pass
+        constexpr int kEarlyPerPassX2 = 6;        // 3 chunk steps per residual pass
         if (res_len > 0 && p.chunks_per_wave >= kMinChunksForOneResWave) {
             p.res_waves = 1;
             p.early_per_pass_x2 = kEarlyPerPassX2;
