@@ -39,7 +39,7 @@ HBM_PEAK_GBS = 8000.0
 # x 1.00 per dispatch, the factors calibrated on a 512 MiB copy
 # (profiles/attn_mfma_config4.md).  Reported only for that exact workload.
 ATTN4_ALGO_BYTES = 583_008_256
-ATTN4_TRAFFIC_BYTES = 583_543_680
+ATTN4_TRAFFIC_BYTES = 583_457_664
 
 
 def attn_bytes(B, Hq, Hkv, D, Tq, Tr, Gk, Gv):
