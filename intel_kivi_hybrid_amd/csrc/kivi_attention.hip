@@ -311,6 +311,7 @@ __global__ __launch_bounds__(kMaxD) void attn_merge_kernel(const float* __restri
 
 struct Plan {
     int layout;
+    bool mfma;                                // matrix-core kernel (else the generic one)
     int n_units, n_splits, units_per_split;   // generic kernel
     int n_qsplits, chunks_per_wave, res_waves, early_per_pass_x2;   // matrix-core kernel
 };
@@ -319,7 +320,11 @@ Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
                int splits_hint) {
     Plan p{};
     p.layout = code_layout_for(D, G, Gv);
-    if (p.layout == kLayoutMfma) {
+    // The matrix-core kernel needs at least one chunk per workgroup (its
+    // prefetch ring is filled unconditionally); a residual-only context of a
+    // matrix-core store goes to the generic kernel, which reads the ring only.
+    p.mfma = p.layout == kLayoutMfma && n_chunks > 0;
+    if (p.mfma) {
         // Aim for ~2048 chunk waves in flight (8 per CU) with >= 8 chunks per
         // wave; the residual window gets its own workgroups.
         constexpr int kWavesPerGroup = 4, kTargetWaves = 2048, kMinChunksPerWave = 8;
@@ -335,16 +340,11 @@ Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
         // its split's passes while the other three start on chunks, taking
         // 3 chunks each per pass up front (measured best at config 4);
         // otherwise every wave takes passes before its chunks.
-        if (n_chunks > 0) {
-            S = max(1, min(S, (n_chunks + kWavesPerGroup - 1) / kWavesPerGroup));
-            p.chunks_per_wave = (n_chunks + kWavesPerGroup * S - 1) / (kWavesPerGroup * S);
-            p.n_qsplits = (n_chunks + kWavesPerGroup * p.chunks_per_wave - 1) /
-                          (kWavesPerGroup * p.chunks_per_wave);
-        } else {
-            p.chunks_per_wave = 0;
-            p.n_qsplits = max(1, min(splits_hint > 0 ? splits_hint : 1,
-                                     (res_len + 16 * kWavesPerGroup - 1) / (16 * kWavesPerGroup)));
-        }
+        // every split gets at least one chunk
+        S = max(1, min(S, (n_chunks + kWavesPerGroup - 1) / kWavesPerGroup));
+        p.chunks_per_wave = (n_chunks + kWavesPerGroup * S - 1) / (kWavesPerGroup * S);
+        p.n_qsplits = (n_chunks + kWavesPerGroup * p.chunks_per_wave - 1) /
+                      (kWavesPerGroup * p.chunks_per_wave);
         constexpr int kMinChunksForOneResWave = 16;
         constexpr int kEarlyPerPassX2 = 6;        // 3 chunk steps per residual pass
         if (res_len > 0 && p.chunks_per_wave >= kMinChunksForOneResWave) {
@@ -376,6 +376,13 @@ bool needs_workspace(const Plan& p) { return p.n_splits > 1; }
 }  // namespace
 
 int launch_attention_mfma(const AttnLaunch& a, hipStream_t st) {
+    // every workgroup's prefetch ring reads at least one real chunk
+    if (a.n_chunks <= 0 || a.chunks_per_wave <= 0 ||
+        (int64_t)(a.n_qsplits - 1) * 4 * a.chunks_per_wave >= a.n_chunks)
+        return set_error(kErrInvalidArgument,
+                         "matrix-core attention needs a chunk in every split (chunks %d, "
+                         "splits %d, chunks per wave %d)", a.n_chunks, a.n_qsplits,
+                         a.chunks_per_wave);
     const bool r16 = a.res_dt != kSrcF32;
     switch (a.Hq / a.Hkv) {
         case 1: return r16 ? launch_attention_mfma_hg1_r16(a, st) : launch_attention_mfma_hg1(a, st);
@@ -474,7 +481,7 @@ static int decode_attention_impl(const float* q, const uint8_t* k_codes, const f
     }
     hipStream_t st = (hipStream_t)stream;
     const int new_slot = k_new ? (res_start + res_len - 1) % res_capacity : 0;
-    if (k_new && layout != kLayoutMfma) {
+    if (k_new && !p.mfma) {
         // the generic kernel reads the ring only: file the token there first
         const int rc = kivi_store_append(k_new, v_new, res_dtype, new_sb, new_sh, 0, 1,
                                          const_cast<void*>(k_res), const_cast<void*>(v_res),
@@ -482,7 +489,7 @@ static int decode_attention_impl(const float* q, const uint8_t* k_codes, const f
                                          new_slot, stream);
         if (rc) return rc;
     }
-    if (layout == kLayoutMfma) {
+    if (p.mfma) {
         AttnLaunch L{q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res, v_res, out,
                      part_o, part_ml, batch, q_heads, kv_heads, head_dim, group_size_k,
                      group_size_v, chunk_capacity, num_chunks, res_capacity, res_start, res_len,

@@ -272,6 +272,7 @@ struct Shape {
     __host__ __device__ static constexpr int lds(int NG) {
         return (kWaves * wave_lds(NG) > MERGE_LDS ? kWaves * wave_lds(NG) : MERGE_LDS) + RES_LDS;
     }
+    __host__ __device__ static constexpr int res_off(int NG) { return lds(NG) - RES_LDS; }
     static_assert(NP >= 1 && LPH * CPL == D && CPL % 2 == 0, "shape");
     // NG = 1 gives the smallest per-wave region
     static_assert(QRES_LDS <= wave_lds(1) && MERGE_LDS <= qres_off(1), "residual buffers");
@@ -450,19 +451,24 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // Residual pass buffers (scaled q of the group, per-wave probabilities)
     // after the merge slots, and the combined residual state at the end.
     float* qres = reinterpret_cast<float*>(smem + S::qres_off(NG));             // [HG][D]
-    float* rstate = reinterpret_cast<float*>(smem + S::lds(NG) - S::RES_LDS);
-    // The new token (if any) is read from its own tensor by the residual
-    // pass below; the first split also files it in the ring for later
-    // launches (nothing in this launch reads that ring slot).  Its loads are
-    // issued before the query's, so that both share one memory round trip
-    // before the barrier.
+    float* rstate = reinterpret_cast<float*>(smem + S::res_off(NG));
+    // ---- launch prologue -----------------------------------------------------
+    // Every load the prologue needs is issued up front, in the order of use:
+    // the new token (if any), the query, this lane's query channels for the
+    // key operand builds, then the first PF chunks of the wave's prefetch
+    // ring.  The barrier fences LDS only, so the ring's loads stay in flight
+    // across it: the prologue costs one memory round trip, shared with the
+    // first chunks.
+    //
+    // The new token is read from its own tensor by the residual pass below;
+    // the first split also files it in the ring for later launches (nothing
+    // in this launch reads that ring slot).  Lane e < D/4 of the first
+    // split's last wave moves four elements of each row.  A wave waits for
+    // its stores to complete before it reuses their data registers (one
+    // memory round trip); the last wave holds the fewest chunks, so the wait
+    // mostly stays off the critical path.
     const bool has_new = a.k_new != nullptr;
     const int64_t new_row = (int64_t)b * a.new_sb + (int64_t)kvh * a.new_sh;   // element offset
-    // Lane e < D/4 of the first split's last wave moves four elements of
-    // each row.  A wave waits for its stores to complete before it reuses
-    // their data registers (one memory round trip); the last wave has at
-    // most as many chunks as any other (they are dealt from wave 0) and the
-    // smallest residual slice, so the wait mostly stays off the critical path.
     using Quad = typename std::conditional<R16, uint2, uint4>::type;
     const bool copy_new = has_new && split == 0 && wave == kWaves - 1 && lane < D / 4;
     Quad kn{}, vn{};
@@ -470,50 +476,26 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         kn = static_cast<const Quad*>(a.k_new)[new_row / 4 + lane];
         vn = static_cast<const Quad*>(a.v_new)[new_row / 4 + lane];
     }
-    // All of the thread's query loads are issued before any is used, so the
-    // fill costs one memory round trip.
-    {
-        constexpr int QN = (HG * D + kBlock - 1) / kBlock;
-        const float* qg = a.q + ((int64_t)b * a.Hq + kvh * HG) * D;
-        float qt[QN];
+    constexpr int QN = (HG * D + kBlock - 1) / kBlock;
+    const float* qg = a.q + ((int64_t)b * a.Hq + kvh * HG) * D;
+    float qt[QN];
 #pragma unroll
-        for (int i = 0; i < QN; ++i) qt[i] = qg[min((int)threadIdx.x + i * kBlock, HG * D - 1)];
-#pragma unroll
-        for (int i = 0; i < QN; ++i) {
-            const int e = threadIdx.x + i * kBlock;
-            if (e < HG * D) qres[e] = qt[i] * a.qscale;
-        }
-    }
-    __syncthreads();
-    // After the barrier: the barrier waits for every outstanding vector
-    // memory operation, stores included, so stores before it would cost a
-    // round trip of their own; here they complete alongside the loads below.
-    if (copy_new) {
-        const int64_t o = ((int64_t)bh * a.Rcap + a.new_slot) * (D / 4) + lane;
-        static_cast<Quad*>(const_cast<void*>(a.k_res))[o] = kn;
-        static_cast<Quad*>(const_cast<void*>(a.v_res))[o] = vn;
-    }
-
+    for (int i = 0; i < QN; ++i) qt[i] = qg[min((int)threadIdx.x + i * kBlock, HG * D - 1)];
     // W-prep lane: head wh, channels [wseg*CPL, +CPL).
     const bool wlane = lane < HG * S::LPH;
     const int wh = lane / S::LPH, wseg = lane % S::LPH;
     float qv[S::CPL];
 #pragma unroll
-    for (int i = 0; i < S::CPL; ++i)
-        qv[i] = wlane ? a.q[((int64_t)b * a.Hq + kvh * HG + wh) * D + wseg * S::CPL + i] * a.qscale
-                      : 0.f;
+    for (int i = 0; i < S::CPL; ++i) qv[i] = wlane ? qg[wh * D + wseg * S::CPL + i] : 0.f;
+    // Keeps the query loads ahead of the ring's: the query's LDS stores then
+    // wait for the query alone.
+    asm volatile("" ::: "memory");
 
-    // The workgroup's chunks [g_begin, g_end) are dealt to its waves in turn
-    // (wave w takes g_begin + w + kWaves*j): the four waves of a workgroup
-    // then read neighbouring chunks, which streams from HBM measurably faster
-    // than four separate contiguous ranges.  When the last wave takes the
-    // whole residual window (res_waves == 1), the first 3*early_chunks chunks
-    // are dealt to the other three waves only, while it works on the window.
+    // Residual passes are dealt whole, in reverse wave order (chunks are
+    // dealt from wave 0, so the waves that may hold one chunk fewer take the
+    // extra passes).  With res_waves == 1 the last wave of each workgroup
+    // takes all of its split's passes while the other three stream chunks.
     const bool res_one = a.res_waves == 1;
-    // Residual passes: the window is dealt in whole passes, and in reverse
-    // wave order (chunks are dealt from wave 0 of split 0, so the waves that
-    // may hold one chunk fewer take the extra passes).  With res_waves == 1
-    // only the last wave of each split takes passes.
     const int n_res_waves = a.n_qsplits * (res_one ? 1 : kWaves);
     const int widx = res_one ? (wave == kWaves - 1 ? n_res_waves - 1 - split : n_res_waves)
                              : n_res_waves - 1 - (split * kWaves + wave);
@@ -521,9 +503,18 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     const int pbase = n_pass / n_res_waves, pextra = n_pass % n_res_waves;
     // passes of this split's last wave when it alone takes them
     const int split_passes = pbase + (n_res_waves - 1 - split < pextra ? 1 : 0);
+
+    // The workgroup's chunks [g_begin, g_end) are dealt to its waves in turn
+    // (wave w takes g_begin + w + kWaves*j): the four waves then read
+    // neighbouring chunks, which streams from HBM measurably faster than four
+    // separate contiguous ranges.  When the last wave takes the whole
+    // residual window (res_waves == 1), the first 3*early chunks are dealt to
+    // the other three waves only, while it works on the window.  The dealing
+    // is fixed per launch shape, so results are bit-for-bit reproducible.
     const int g_begin = split * kWaves * a.chunks_per_wave;
     const int g_end = min(g_begin + kWaves * a.chunks_per_wave, a.n_chunks);
     const int g_cnt = max(0, g_end - g_begin);
+    const int c_last = g_end - 1;
     // early chunks per other wave: early_per_pass_x2 / 2 per pass, rounded
     const int early = min((a.early_per_pass_x2 * split_passes + 1) / 2, a.chunks_per_wave / 2);
     const int s_early = res_one ? min((kWaves - 1) * early, g_cnt) : 0;
@@ -531,10 +522,38 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     const int n_mine = n_early + max(0, (g_cnt - s_early - wave + kWaves - 1) / kWaves);
     const int early_base = g_begin + wave;                               // + 3j
     const int late_base = g_begin + s_early + wave - kWaves * n_early;   // + 4j
+    // the wave's j-th chunk, or -1 past its last
     auto chunk_of = [&](int j) {
-        const int jj = min(j, n_mine - 1);
-        return jj < n_early ? early_base + (kWaves - 1) * jj : late_base + kWaves * jj;
+        return j >= n_mine ? -1
+                           : j < n_early ? early_base + (kWaves - 1) * j : late_base + kWaves * j;
     };
+    constexpr int PF = S::PF;
+    ChunkRegs<S> buf[PF];
+    int cid[PF];     // the chunk in each ring slot; -1 past the end (its load re-reads c_last)
+    const ChunkSrc<S> src = chunk_src<S>(a, bh * a.Cmax, lane, NG);
+    // (the launch gives every workgroup at least one chunk, so c_last is a
+    // valid chunk and these loads need no branch: a branch here would make the
+    // compiler wait for them before the query's LDS stores)
+#pragma unroll
+    for (int k = 0; k < PF; ++k) {
+        cid[k] = chunk_of(k);
+        load_chunk<S>(buf[k], src, cid[k] >= 0 ? cid[k] : c_last);
+    }
+    int next_j = PF;     // the wave's next chunk to load
+#pragma unroll
+    for (int i = 0; i < QN; ++i) {
+        const int e = threadIdx.x + i * kBlock;
+        if (e < HG * D) qres[e] = qt[i] * a.qscale;
+    }
+    lds_barrier();
+    // After the barrier, so that no wave waits for these stores before it.
+    if (copy_new) {
+        const int64_t o = ((int64_t)bh * a.Rcap + a.new_slot) * (D / 4) + lane;
+        static_cast<Quad*>(const_cast<void*>(a.k_res))[o] = kn;
+        static_cast<Quad*>(const_cast<void*>(a.v_res))[o] = vn;
+    }
+#pragma unroll
+    for (int i = 0; i < S::CPL; ++i) qv[i] *= a.qscale;
 
     f32x4_t O[S::NBV];
 #pragma unroll
@@ -777,23 +796,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         }
     };
 
-    // ---- software-pipelined chunk loop ----------------------------------------
-    // Step i finishes chunk i (value operands and o update) while it starts
-    // chunk i+1 (metadata, key operands, scores, softmax): the two halves are
-    // independent, so their latencies overlap, and each chunk costs two
-    // wave-level LDS syncs.  Chunk data come from a ring of PF register
-    // buffers filled PF chunks ahead (clamped indices, so no load is inside a
-    // branch and the compiler waits only for the chunk about to be used).
-    constexpr int PF = S::PF;
-    ChunkRegs<S> buf[PF];
-    const int n_full = n_mine / PF * PF;
-    const ChunkSrc<S> src = chunk_src<S>(a, bh * a.Cmax, lane, NG);
     bool any_cur = false;
-    if (n_mine > 0) {
-#pragma unroll
-        for (int k = 0; k < PF; ++k)
-            load_chunk<S>(buf[k], src, chunk_of(k));
-    }
 
     // ---- this wave's slice of the fp32 residual window ------------------------
     // Its own online-softmax state (mr, lr, orr), merged with the chunk state
@@ -933,7 +936,15 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // are never written and must read as 0.
     for (int e = lane; e < S::off_pl(NG) / 4; e += kWave) reinterpret_cast<uint32_t*>(wl)[e] = 0u;
 
-    if (n_mine > 0) {
+    // ---- software-pipelined chunk loop ----------------------------------------
+    // Step i finishes chunk i (value operands and o update) while it starts
+    // chunk i+1 (metadata, key operands, scores, softmax): the two halves are
+    // independent, so their latencies overlap, and each chunk costs two
+    // wave-level LDS syncs.  Chunk data come from the ring of PF register
+    // buffers, refilled PF chunks ahead (a slot past the end re-reads a valid
+    // chunk, so no load is inside a branch and the compiler waits only for
+    // the chunk about to be used).
+    if (cid[0] >= 0) {
         stage_meta<S>(buf[0], MT, lane, NG, meta_floats);
         wave_sync();
         wprep(Int<0>{});
@@ -943,9 +954,8 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // Step i (of the wave's chunks, counted from 0) uses double-buffer
     // slot i & 1; PF is even, so within the unrolled ring the slot of step k
     // is k & 1, a compile-time constant.
-    auto step = [&](const ChunkRegs<S>& cur, const ChunkRegs<S>& nxt, int i, auto slot_c) {
+    auto step = [&](const ChunkRegs<S>& cur, const ChunkRegs<S>& nxt, bool has_next, auto slot_c) {
         constexpr int slot = decltype(slot_c)::value, nslot = slot ^ 1;
-        const bool has_next = i + 1 < n_mine;
         if (has_next) stage_meta<S>(nxt, MT + nslot * meta_stride, lane, NG, meta_floats);
         wave_sync();
         if (has_next) wprep(Int<nslot>{});
@@ -964,18 +974,22 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         __builtin_amdgcn_s_setprio(0);
     };
     static_assert(PF % 2 == 0, "the slot parity of a ring step must be static");
-    for (int c0 = 0; c0 < n_full; c0 += PF) {
+    // The ring holds the wave's chunks in order, valid ones first.  The main
+    // loop runs whole rings while every slot holds a chunk (no branch inside,
+    // so the compiler schedules across the steps); the last partial ring is
+    // the tail, which loads nothing.
+    while (cid[PF - 1] >= 0) {
         static_for<0, PF>([&](auto kc) {
             constexpr int k = decltype(kc)::value;
-            step(buf[k], buf[(k + 1) % PF], c0 + k, Int<k & 1>{});
-            load_chunk<S>(buf[k], src, chunk_of(c0 + k + PF));
+            step(buf[k], buf[(k + 1) % PF], k + 1 < PF || cid[0] >= 0, Int<k & 1>{});
+            cid[k] = chunk_of(next_j++);
+            load_chunk<S>(buf[k], src, cid[k] >= 0 ? cid[k] : c_last);
         });
     }
-    static_for<0, PF>([&](auto kc) {
+    static_for<0, PF - 1>([&](auto kc) {
         constexpr int k = decltype(kc)::value;
-        if (k < n_mine - n_full) step(buf[k], buf[(k + 1) % PF], n_full + k, Int<k & 1>{});
+        if (cid[k] >= 0) step(buf[k], buf[k + 1], cid[k + 1] >= 0, Int<k & 1>{});
     });
-
     // ---- wave state -> merge slot --------------------------------------------
     wave_sync();
 #pragma unroll

@@ -269,4 +269,15 @@ __device__ __forceinline__ float4 decode4(uint32_t byte, float scale, float zero
     return o;
 }
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also
+// waits for every outstanding global load and store (s_waitcnt vmcnt(0)),
+// which would drain a prefetch issued before the barrier.  Only for kernels
+// where no thread reads global memory that another thread of the workgroup
+// wrote.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 }  // namespace kivi

@@ -246,16 +246,6 @@ __global__ __launch_bounds__(kFlushBlock) void flush_kernel(FlushArgs a) {
     write_codes<LAYOUT, false>(codes, a.v_codes + chunk_id * code_bytes, G, D);
 }
 
-// Workgroup barrier that orders LDS accesses only.  __syncthreads() also
-// waits for every outstanding global load (s_waitcnt vmcnt(0)), which would
-// drain the next chunk's prefetch at each barrier; no thread here reads
-// global memory another thread of the workgroup wrote.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // 1/scale for code_rcp, or NaN when the scale is outside the range where
 // v_rcp_f32 is accurate, so that code_rcp flags every element of that group.
 __device__ __forceinline__ float rcp_or_nan(float scale) {
