@@ -12,6 +12,8 @@ are chosen so that it holds.
     split taking fewer, so the up-front chunks differ per split.
   * A window of one token, the fused append (bit-identical to a separate
     append), and GQA ratios 1, 4 and 8.
+  * A decode that starts with the whole context in the window (generic
+    kernel) and crosses its first flush onto the matrix-core kernel.
 Bar: 1e-3 relative (max |o - o_ref| / max |o_ref| per (batch, head))."""
 
 import pytest
@@ -119,3 +121,38 @@ def test_residual_wave_16bit_ring(store_cls):
     b.stage_token(kh[:, :, T:], vh[:, :, T:])
     q = seeded_q(B, Hq, D, seed=9).cuda()
     assert torch.equal(a.attention(q, num_splits=1), b.attention(q, num_splits=1))
+
+
+def test_decode_from_window_only_into_first_flush(store_cls):
+    """A context held entirely in the residual window has no quantised chunk,
+    so its launches take the generic kernel (the matrix-core kernel needs a
+    chunk in every workgroup); the first flush moves the same decode onto the
+    matrix-core kernel.  Each step: the fused append equals a separate append
+    bit for bit, and the output matches the oracle."""
+    B, Hq, Hkv, D, G, Gv, R = 2, 8, 2, 128, 32, 32, 64
+    T, steps = 40, 40
+    print(f"[reswave] window-only decode T={T} R={R} steps={steps}", flush=True)
+    k, v = make_kv(B, Hkv, T + steps, D, seed=91)
+    a = store_cls(B, Hkv, D, G, R, "cuda:0", group_size_v=Gv)
+    b = store_cls(B, Hkv, D, G, R, "cuda:0", group_size_v=Gv)
+    fill_store(a, k[:, :, :T], v[:, :, :T], R)
+    fill_store(b, k[:, :, :T], v[:, :, :T], R)
+    assert a.n_chunks == 0
+    seen_chunks = set()
+    for step in range(steps):
+        t = T + step
+        kn, vn = k[:, :, t:t + 1].cuda(), v[:, :, t:t + 1].cuda()
+        q = seeded_q(B, Hq, D, seed=300 + step).cuda()
+        a.stage_token(kn, vn)
+        oa = a.attention(q).clone()
+        b.append(kn, vn)
+        ob = b.attention(q).clone()
+        assert torch.equal(oa, ob), f"step {step}: fused append differs"
+        err = _check(a, k, v, q, oa, G, Gv)
+        seen_chunks.add(a.n_chunks)
+        assert err <= ATTN_TOL, f"step {step}: chunks={a.n_chunks} rel_err={err:.2e}"
+        while a.res_len >= R:
+            a.flush()
+            b.flush()
+    print(f"[reswave]   chunk counts seen: {sorted(seen_chunks)}", flush=True)
+    assert 0 in seen_chunks and max(seen_chunks) >= 1
