@@ -960,6 +960,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         wave_sync();
         if (has_next) wprep(Int<nslot>{});
         pprep(Int<slot>{}, any_cur);
+        any_cur = false;            // vb now follows the current running max
         wave_sync();
         // A wave in its matrix-core phase (value MFMAs, then the next chunk's
         // scores and softmax) runs at a raised priority, so that when both
@@ -974,10 +975,51 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         __builtin_amdgcn_s_setprio(0);
     };
     static_assert(PF % 2 == 0, "the slot parity of a ring step must be static");
+
+    // O accumulates (p vs)(8 + c), which carries a bias of 8 sum_t p vs
+    // beside the output itself; the per-item correction sum_t p (vz - 8 vs)
+    // in vb cancels it.  Cancelled only at the end, that bias lets O's
+    // rounding grow with the whole context: each chunk adds ~2^-24 of the
+    // biased sum, which over long contexts of near-uniform weights reaches
+    // the size of the output itself (3e-3 relative at 1025 chunks per wave).
+    // Folding vb into O every kFoldChunks chunks keeps the bias in O to that
+    // of at most kFoldChunks chunks.  Called after a whole ring, where the
+    // pending rescale (if the last scores moved the running max) is in AL
+    // slot 0 and has not reached vb yet: it is applied here, and the next
+    // pprep then scales zeros.
+    constexpr int kFoldChunks = 16;
+    constexpr int kFoldRings = kFoldChunks / PF > 0 ? kFoldChunks / PF : 1;
+    auto fold_vcorr = [&]() {
+        wave_sync();
+#pragma unroll
+        for (int it = 0; it < S::NEV; ++it) {
+            if (it_valid[it]) {
+                const float x = any_cur ? vb[it] * AL[it_h[it]] : vb[it];
+                VB[ilane + 64 * it] = x;          // [h][g][seg]
+            }
+            vb[it] = 0.f;
+        }
+        wave_sync();
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int h = 2 * gq + e;
+            if (h < HG) {
+#pragma unroll
+                for (int nb = 0; nb < S::NBV; ++nb) {
+                    const float* pv = VB + (h * NG + (16 * nb + col) / Gv) * NSEG;
+                    float v = 0.f;
+#pragma unroll
+                    for (int sg = 0; sg < NSEG; ++sg) v += pv[sg];
+                    O[nb][2 * e] += v;
+                }
+            }
+        }
+    };
     // The ring holds the wave's chunks in order, valid ones first.  The main
     // loop runs whole rings while every slot holds a chunk (no branch inside,
     // so the compiler schedules across the steps); the last partial ring is
     // the tail, which loads nothing.
+    int rings = 0;
     while (cid[PF - 1] >= 0) {
         static_for<0, PF>([&](auto kc) {
             constexpr int k = decltype(kc)::value;
@@ -985,6 +1027,10 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             cid[k] = chunk_of(next_j++);
             load_chunk<S>(buf[k], src, cid[k] >= 0 ? cid[k] : c_last);
         });
+        if (++rings == kFoldRings) {
+            rings = 0;
+            fold_vcorr();
+        }
     }
     static_for<0, PF - 1>([&](auto kc) {
         constexpr int k = decltype(kc)::value;
@@ -1081,11 +1127,27 @@ int launch_shape(const AttnLaunch& a, hipStream_t st) {
     return check_launch("packed_decode_attention (mfma)");
 }
 
+// gfx950 LDS per workgroup.  Shapes whose fixed LDS need exceeds it are
+// not instantiated (they could never launch).
+constexpr int kMaxLdsBytes = 160 * 1024;
+
+template <int HG, int D, int G, int NG>
+constexpr bool lds_fits() {
+    return Shape<HG, D, G>::lds(NG) <= kMaxLdsBytes;
+}
+
 // Value groups of 32 channels, one group per token, or (head_dim 128/256
 // with 64- or 128-channel groups) the runtime count.
 template <int HG, int D, int G, bool R16>
 int launch_ng(const AttnLaunch& a, hipStream_t st) {
-    if (a.Gv == 32) return launch_shape<HG, D, G, D / 32, R16>(a, st);
+    if (a.Gv == 32) {
+        if constexpr (lds_fits<HG, D, G, D / 32>())
+            return launch_shape<HG, D, G, D / 32, R16>(a, st);
+        return set_error(kErrUnsupported,
+                         "decode attention with q_heads/kv_heads=%d, head_dim=%d, G=%d, "
+                         "group_size_v=32 needs %d bytes of LDS per workgroup (at most %d)",
+                         HG, D, G, Shape<HG, D, G>::lds(D / 32), kMaxLdsBytes);
+    }
     if (a.Gv == D) return launch_shape<HG, D, G, 1, R16>(a, st);
     if constexpr (D > 64) return launch_shape<HG, D, G, 0, R16>(a, st);
     return set_error(kErrUnsupported, "group_size_v=%d with head_dim=%d", a.Gv, D);
