@@ -61,30 +61,39 @@ def fill_store(store, k, v, R):
 
 
 def oracle_history(k, v, n_chunks, G, Gv):
-    """Dequantised history [B,H,n_chunks*G,D] for keys and values."""
-    ks, vs = [], []
-    for c in range(n_chunks):
-        o = oracle_chunk(k[:, :, c * G:(c + 1) * G], v[:, :, c * G:(c + 1) * G], G, Gv)
-        ks.append(o["k_deq"])
-        vs.append(o["v_deq"])
+    """Dequantised history [B,H,n_chunks*G,D] for keys and values.
+
+    One oracle round-trip call per tensor over the whole history (the
+    round-trip is pinned bit-identical to quantise + dequantise): keys as
+    [B,H,n,D,G] (each channel of each chunk one group of G tokens), values as
+    [B,H,n*G,D] (each token's channels in groups of Gv)."""
     B, H, _, D = k.shape
-    if not ks:
+    T = n_chunks * G
+    if T == 0:
         return np.zeros((B, H, 0, D), np.float32), np.zeros((B, H, 0, D), np.float32)
-    return np.concatenate(ks, axis=2), np.concatenate(vs, axis=2)
+    k, v = torch.as_tensor(k), torch.as_tensor(v)
+    # layout changes in torch (threaded copies), the arithmetic in the oracle
+    kt = k[:, :, :T].reshape(B, H, n_chunks, G, D).transpose(3, 4).contiguous()
+    k_deq = torch.from_numpy(codec.roundtrip_groups(kt.numpy(), G)).reshape(B, H, n_chunks, D, G)
+    del kt
+    k_deq = k_deq.transpose(3, 4).contiguous().reshape(B, H, T, D).numpy()
+    v_deq = codec.roundtrip_groups(v[:, :, :T].contiguous().numpy(), Gv).reshape(B, H, T, D)
+    return k_deq, v_deq
 
 
 def _u32(t):
     return t.detach().cpu().numpy().view(np.uint32)
 
 
-def check_store_bit_exact(st, k, v):
-    """Every flushed chunk of store ``st`` (codes through the documented byte
-    transposes, scales, zeros and, if kept, the dequantised history) equals
-    the oracle's quantisation of tokens [c*G, (c+1)*G) of ``k``/``v``
-    ([B,H,T,D] fp32, CPU), and the residual window holds the tokens after
-    the last chunk."""
+def check_store_bit_exact(st, k, v, chunks=None):
+    """Every flushed chunk of store ``st`` (or those listed in ``chunks``:
+    codes through the documented byte transposes, scales, zeros and, if
+    kept, the dequantised history) equals the oracle's quantisation of
+    tokens [c*G, (c+1)*G) of ``k``/``v`` ([B,H,T,D] fp32, CPU), and the
+    residual window holds the tokens after the last chunk (up to T)."""
     G, Gv = st.G, st.Gv
-    for c in range(st.n_chunks):
+    for c in (range(st.n_chunks) if chunks is None else chunks):
+        assert 0 <= c < st.n_chunks, f"chunk {c} not flushed ({st.n_chunks} chunks)"
         o = oracle_chunk(k[:, :, c * G:(c + 1) * G], v[:, :, c * G:(c + 1) * G], G, Gv)
         assert np.array_equal(st.unpermuted_k_codes(c).cpu().numpy(), o["k_codes"]), \
             f"k codes chunk {c}"
@@ -101,7 +110,8 @@ def check_store_bit_exact(st, k, v):
             assert np.array_equal(_u32(vh), o["v_deq"].view(np.uint32)), f"v history chunk {c}"
     rk, rv = st.residual()
     q0 = st.n_chunks * G
-    assert torch.equal(rk.cpu(), k[:, :, q0:]) and torch.equal(rv.cpu(), v[:, :, q0:])
+    q1 = q0 + st.res_len
+    assert torch.equal(rk.cpu(), k[:, :, q0:q1]) and torch.equal(rv.cpu(), v[:, :, q0:q1])
 
 
 def rel_err(out, ref):

@@ -1,0 +1,150 @@
+"""Pins the float64 attention oracle (oracle/attention.py) on the CPU.
+
+The reference has no attention kernel; the math it states is
+``softmax(Q K^T * D^-0.5) V`` over the dequantised cache
+(tests/integration/test_attention_fix.py:40-43,91-93), run by the HF model
+with GQA ``repeat_kv`` (query head h reads kv head h // (Hq / Hkv)).  The
+oracle is checked here against:
+  * torch's scaled_dot_product_attention in float64 (an independent library
+    routine), with K/V repeated per query head, on shapes with and without a
+    quantised history and a residual window;
+  * closed forms: identical keys or a zero query give the mean of V, a
+    one-token context gives that token's V, a two-token context the
+    two-term softmax written out by hand;
+  * mutants: each plausible mistake planted in a copy of the oracle's own
+    source (wrong scale, wrong head map, a dropped history or residual, V
+    swapped for K, normalisation over the wrong axis) must fail the library
+    comparison, so the comparison above pins those parts.
+It also pins the vectorised history builder of the GPU tests against the
+per-chunk oracle quantise + dequantise.
+"""
+
+import os
+import types
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oracle_attention
+from oracle.attention import decode_attention
+from tests.kv_helpers import make_kv, oracle_chunk, oracle_history
+
+SHAPES = [
+    # B, Hq, Hkv, D, Tq, Tr
+    (2, 8, 2, 64, 96, 17),     # GQA 4, history + residual
+    (1, 4, 4, 128, 0, 40),     # MHA, residual only (no flush yet)
+    (2, 6, 3, 32, 64, 0),      # GQA 2, residual empty right after a flush
+    (1, 8, 1, 16, 32, 1),      # GQA 8, one residual token
+]
+
+
+def _inputs(B, Hq, Hkv, D, Tq, Tr, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hq, D, generator=g, dtype=torch.float64)
+    kh = torch.randn(B, Hkv, Tq, D, generator=g, dtype=torch.float64)
+    vh = torch.randn(B, Hkv, Tq, D, generator=g, dtype=torch.float64)
+    kr = torch.randn(B, Hkv, Tr, D, generator=g, dtype=torch.float64)
+    vr = torch.randn(B, Hkv, Tr, D, generator=g, dtype=torch.float64)
+    kh[..., 3] *= 10.0                          # a channel outlier
+    return q, kh, vh, kr, vr
+
+
+def _sdpa(q, kh, vh, kr, vr):
+    """torch float64 SDPA over [history ; residual], K/V repeated per query head."""
+    Hq, Hkv = q.shape[1], kh.shape[1]
+    K = torch.cat([kh, kr], dim=2).repeat_interleave(Hq // Hkv, dim=1)
+    V = torch.cat([vh, vr], dim=2).repeat_interleave(Hq // Hkv, dim=1)
+    o = torch.nn.functional.scaled_dot_product_attention(q[:, :, None], K, V)
+    return o[:, :, 0]
+
+
+def _max_err(fn, shape, seed):
+    q, kh, vh, kr, vr = _inputs(*shape, seed=seed)
+    out = fn(q.numpy(), kh.numpy(), vh.numpy(), kr.numpy(), vr.numpy())
+    return float(np.abs(out - _sdpa(q, kh, vh, kr, vr).numpy()).max())
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_oracle_matches_sdpa_float64(shape):
+    assert _max_err(decode_attention, shape, seed=sum(shape)) < 1e-12
+
+
+def test_closed_forms():
+    rng = np.random.default_rng(3)
+    B, Hq, Hkv, D, T = 2, 8, 2, 32, 20
+    q = rng.standard_normal((B, Hq, D))
+    v = rng.standard_normal((B, Hkv, T, D))
+    # identical keys: uniform weights, the mean of V
+    k = np.broadcast_to(rng.standard_normal((B, Hkv, 1, D)), (B, Hkv, T, D))
+    mean_v = np.repeat(v.mean(axis=2), Hq // Hkv, axis=1)
+    o = decode_attention(q, k[:, :, :12], v[:, :, :12], k[:, :, 12:], v[:, :, 12:])
+    assert np.allclose(o, mean_v, rtol=0, atol=1e-13)
+    # zero query: uniform weights whatever the keys
+    kk = rng.standard_normal((B, Hkv, T, D))
+    o = decode_attention(np.zeros_like(q), kk[:, :, :5], v[:, :, :5], kk[:, :, 5:], v[:, :, 5:])
+    assert np.allclose(o, mean_v, rtol=0, atol=1e-13)
+    # one-token context (history only, or residual only): that token's V
+    v1 = np.repeat(v[:, :, :1], Hq // Hkv, axis=1)[:, :, 0]
+    o = decode_attention(q, kk[:, :, :1], v[:, :, :1], None, None)
+    assert np.array_equal(o, v1)
+    o = decode_attention(q, None, None, kk[:, :, :1], v[:, :, :1])
+    assert np.array_equal(o, v1)
+    # two tokens, written out: o = (e^s0 v0 + e^s1 v1) / (e^s0 + e^s1),
+    # s = q.k / sqrt(D), query head h on kv head h // 4
+    o = decode_attention(q, kk[:, :, :1], v[:, :, :1], kk[:, :, 1:2], v[:, :, 1:2])
+    for b in range(B):
+        for h in range(Hq):
+            j = h // (Hq // Hkv)
+            s0 = q[b, h] @ kk[b, j, 0] / np.sqrt(D)
+            s1 = q[b, h] @ kk[b, j, 1] / np.sqrt(D)
+            w0, w1 = np.exp(s0), np.exp(s1)
+            ref = (w0 * v[b, j, 0] + w1 * v[b, j, 1]) / (w0 + w1)
+            assert np.allclose(o[b, h], ref, rtol=1e-13, atol=1e-13)
+
+
+MUTANTS = {
+    "softmax scale": ("D ** -0.5", "D ** -1.0"),
+    "head map": ("kh * g:(kh + 1) * g]", "kh::Hkv]"),
+    "history dropped": ("if k_hist is not None and k_hist.shape[2]:", "if False:"),
+    "residual dropped": ("if k_res is not None and k_res.shape[2]:", "if False:"),
+    "V swapped for K": ("p @ V", "p @ K"),
+    "normalised over heads": ("p.sum(axis=1, keepdims=True)", "p.sum(axis=0, keepdims=True)"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(MUTANTS))
+def test_planted_mistakes_fail_the_library_comparison(name):
+    """A mistake planted in a copy of the oracle's source fails the SDPA
+    comparison on at least one shape (so that comparison pins the part the
+    mistake touches)."""
+    old, new = MUTANTS[name]
+    path = os.path.abspath(oracle_attention.__file__)
+    with open(path) as f:
+        src = f.read()
+    assert old in src, f"mutation site for '{name}' not found"
+    mutant = types.ModuleType(f"oracle_attention_mutant_{name.replace(' ', '_')}")
+    exec(compile(src.replace(old, new), path, "exec"), mutant.__dict__)
+    worst = 0.0
+    for shape in SHAPES:
+        try:
+            worst = max(worst, _max_err(mutant.decode_attention, shape, seed=sum(shape)))
+        except (ValueError, IndexError):
+            worst = np.inf                # the mutant cannot even run this shape
+    assert worst > 1e-6, f"mutant '{name}' passes the comparison (max err {worst:.2e})"
+
+
+@pytest.mark.parametrize("B,H,D,G,Gv,n", [(2, 3, 64, 32, 32, 5), (1, 2, 128, 32, 128, 3),
+                                          (2, 2, 8, 4, 4, 6), (1, 4, 64, 64, 16, 2)])
+def test_vectorised_history_matches_per_chunk_oracle(B, H, D, G, Gv, n):
+    """The GPU tests' one-call history builder equals quantise + dequantise
+    chunk by chunk (the store's definition of a chunk), bit for bit."""
+    k, v = make_kv(B, H, n * G + 5, D, seed=D + n)
+    kh, vh = oracle_history(k, v, n, G, Gv)
+    assert kh.shape == (B, H, n * G, D) and vh.shape == (B, H, n * G, D)
+    for c in range(n):
+        o = oracle_chunk(k[:, :, c * G:(c + 1) * G], v[:, :, c * G:(c + 1) * G], G, Gv)
+        assert np.array_equal(o["k_deq"].view(np.uint32), kh[:, :, c * G:(c + 1) * G].view(np.uint32))
+        assert np.array_equal(o["v_deq"].view(np.uint32), vh[:, :, c * G:(c + 1) * G].view(np.uint32))
+    kh0, vh0 = oracle_history(k, v, 0, G, Gv)
+    assert kh0.shape == (B, H, 0, D) and vh0.shape == (B, H, 0, D)
