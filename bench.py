@@ -1,22 +1,29 @@
 """KIVI hot-path benchmark on one MI355X.
 
 Headline (``value``): packed-KV decode throughput at benchmark config 4
-(Llama-3-8B GQA shape: B=64, 32 q heads / 8 kv heads, D=128, 8K context,
-R=128, G=32).  One step = append the new token's K/V to the HBM residual
-ring, flush 32 tokens into the packed store whenever the residual reaches R,
-and run the fused packed decode attention for one query token per sequence.
-``value`` is algorithmic bytes moved by those steps / wall time of the K timed
-steps, in GB/s.
+(Llama-3-8B GQA shape: B=64, 32 q heads / 8 kv heads, D=128, context 8192,
+R=128, G=32).  One step = the fused packed decode attention for one query
+token per sequence, which also files the step's new K/V into the HBM
+residual ring, then a flush of the 32 oldest residual tokens into the packed
+store whenever the window reaches R.  ``value`` is algorithmic bytes moved by
+those steps / GPU time of the K timed steps, in GB/s.  The first timed step
+is a flush step, so K steps hold ceil(K / 32) flushes (reported).
 
 Also reported: the attention kernel alone against the 8 TB/s HBM roofline
-(``roofline``), configs 3 and 5, the quantise microbench of config 2
-(Mtokens/s), and CPU baselines of the reference path timed on the host.
+(``roofline``: context 8192 = 8064 quantised + a full window of 128; HBM
+traffic from two rocprofv3 counter passes in the same run), configs 3 and 5
+at their stated token counts, the config-2 codec ops through ``_C``
+(quantise, dequantise, round-trip), the batched prefill flush, and CPU
+baselines of the reference path timed on the host over the same K/V bits.
 
 Algorithmic bytes (per (batch, kv-head)):
   attention : D*Tq/4 + 8*D*Tq/Gk + Tq*D/4 + 8*Tq*D/Gv + 8*Tr*D + 8*(Hq/Hkv)*D
+              (the step's new token is read as part of Tr)
+  append    : 4*D*2 written (the new token's K and V into the ring)
   flush     : 8*G*D (read residual) + G*D/4 + 8*D + G*D/4 + 8*G*D/Gv (write)
-  append    : 8*D read + 8*D write
   quantise  : per tensor of N fp32: 4N read + N/4 + 8N/G written
+  dequantise: per tensor: N/4 + 8N/G read + 4N written
+  round-trip: per tensor: 4N read + 4N written
 """
 
 from __future__ import annotations
@@ -34,14 +41,6 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0
 
 
-# HBM bytes that one config-4 attention launch (Tq=8096, Tr=96; 583,008,256
-# algorithmic bytes) moves: rocprofv3 --pmc FETCH_SIZE x 2.00 + WRITE_SIZE
-# x 1.00 per dispatch, the factors calibrated on a 512 MiB copy
-# (profiles/attn_mfma_config4.md).  Reported only for that exact workload.
-ATTN4_ALGO_BYTES = 583_008_256
-ATTN4_TRAFFIC_BYTES = 583_457_664
-
-
 def attn_bytes(B, Hq, Hkv, D, Tq, Tr, Gk, Gv):
     per = (D * Tq // 4 + 8 * D * Tq // Gk + Tq * D // 4 + 8 * Tq * D // Gv
            + 8 * Tr * D + 8 * (Hq // Hkv) * D)
@@ -52,37 +51,65 @@ def flush_bytes(B, Hkv, D, G, Gv):
     return B * Hkv * (8 * G * D + G * D // 4 + 8 * D + G * D // 4 + 8 * G * D // Gv)
 
 
-def append_bytes(B, Hkv, D, n=1):
-    return B * Hkv * 16 * D * n
+def fused_append_bytes(B, Hkv, D):
+    return B * Hkv * 8 * D
 
 
 def quant_bytes(N, G):
     return 4 * N + N // 4 + 8 * N // G
 
 
+def dequant_bytes(N, G):
+    return N // 4 + 8 * N // G + 4 * N
+
+
+def roundtrip_bytes(N):
+    return 8 * N
+
+
 # --------------------------------------------------------------------------
 # GPU workloads
 # --------------------------------------------------------------------------
-def synth_kv(B, H, T, D, seed, device):
-    """N(0,1) K/V with 4 key channels x10 per head and 2% value tokens x8."""
+def synth_kv(B, H, T, D, seed):
+    """Seeded synthetic K/V ``[B, H, T, D]`` fp32, made on the CPU (so that
+    the GPU runs, the CPU baseline and the parity tests see identical bits):
+    N(0,1); keys with 4 fixed channels per kv head x10 (channel outliers);
+    values with round(2% of T) token positions per (b, kv head) x8 (token
+    outliers)."""
     import torch
-    g = torch.Generator(device=device).manual_seed(seed)
-    k = torch.randn(B, H, T, D, generator=g, device=device)
-    v = torch.randn(B, H, T, D, generator=g, device=device)
-    ch = torch.randperm(D, generator=g, device=device)[:4]
-    k[..., ch] *= 10.0
-    tok = torch.randperm(T, generator=g, device=device)[:max(1, round(0.02 * T))]
-    v[:, :, tok, :] *= 8.0
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(B, H, T, D, generator=g)
+    v = torch.randn(B, H, T, D, generator=g)
+    for h in range(H):
+        ch = torch.randperm(D, generator=g)[:min(4, D)]
+        k[:, h, :, ch] *= 10.0
+    n = max(1, round(0.02 * T))
+    for b in range(B):
+        for h in range(H):
+            tok = torch.randperm(T, generator=g)[:n]
+            v[b, h, tok] *= 8.0
     return k, v
 
 
-def build_store(B, Hkv, D, G, Gv, R, T, seed, device, extra_chunks=16):
+def store_tokens(Tq, Tr, G, R):
+    """Tokens to feed an empty store through ``extend(flush_at=R)`` (the
+    KiviCache rule: flush the G oldest while the residual holds >= R) so
+    that it ends with Tq quantised and Tr residual tokens; Tr must lie in
+    [R - G, R - 1] (what that rule leaves) and Tq be a multiple of G."""
+    if Tq % G or not R - G <= Tr < R:
+        raise ValueError(f"Tq={Tq}, Tr={Tr} is not a state extend(flush_at={R}) leaves")
+    return Tq + Tr
+
+
+def make_store(k, v, G, Gv, R, device, extra_chunks=16):
+    """A PackedKVStore fed with CPU K/V ``[B, Hkv, T, D]`` by one batched
+    ``extend`` (one flush launch for every chunk owed, then the residual
+    copy), as a prompt would be."""
     from intel_kivi_hybrid_amd.store import PackedKVStore
+    B, Hkv, T, D = k.shape
     st = PackedKVStore(B, Hkv, D, G, R, device, group_size_v=Gv,
                        chunk_capacity=T // G + extra_chunks)
-    k, v = synth_kv(B, Hkv, T, D, seed, device)
-    st.extend(k, v, flush_at=R)
-    del k, v
+    st.extend(k.to(device), v.to(device), flush_at=R)
     return st
 
 
@@ -101,17 +128,14 @@ def settle_clocks(fn, seconds=0.05, min_calls=20):
     torch.cuda.synchronize()
 
 
-def time_attention(st, Hq, iters, seed, device, blocks=5):
-    """Average duration of one fused-attention call and its algorithmic
-    bytes.  HIP events on the launch stream bracket blocks of back-to-back
-    calls (the host issues a call in a fraction of its GPU time, so the queue
-    never drains): a block's time per call is the kernel's duration plus the
-    launch gap, without the host latency that per-call event pairs add."""
+def time_calls(fn, iters, blocks=5):
+    """Average GPU time of one ``fn()`` call, in microseconds.  HIP events on
+    torch's current stream (the stream every launch here goes to) bracket
+    blocks of back-to-back calls: the host issues a call in a fraction of its
+    GPU time, so the queue never drains, and a block's time per call is the
+    kernels' duration plus the launch gaps, without host latency."""
     import torch
-    g = torch.Generator(device=device).manual_seed(seed)
-    q = torch.randn(st.B, Hq, st.D, generator=g, device=device) * st.D ** -0.5
-    out = torch.empty_like(q)
-    settle_clocks(lambda: st.attention(q, out=out))
+    settle_clocks(fn)
     per_block = max(1, iters // blocks)
     ms = []
     for _ in range(blocks):
@@ -119,34 +143,64 @@ def time_attention(st, Hq, iters, seed, device, blocks=5):
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(per_block):
-            st.attention(q, out=out)
+            fn()
         e1.record()
         torch.cuda.synchronize()
         ms.append(e0.elapsed_time(e1) / per_block)
     ms.sort()
-    avg = sum(ms) / len(ms)
+    return {"avg_us": 1e3 * sum(ms) / len(ms), "median_us": 1e3 * ms[len(ms) // 2]}
+
+
+def time_attention(st, q, iters):
+    """One fused-attention call over the store as it stands."""
+    import torch
+    out = torch.empty_like(q)
+    r = time_calls(lambda: st.attention(q, out=out), iters)
+    Hq = q.shape[1]
     nbytes = attn_bytes(st.B, Hq, st.H, st.D, st.quantized_tokens, st.res_len, st.G, st.Gv)
-    return {"avg_us": avg * 1e3, "median_us": ms[len(ms) // 2] * 1e3, "bytes": nbytes,
-            "gbs": nbytes / (avg * 1e-3) / 1e9, "Tq": st.quantized_tokens, "Tr": st.res_len}
+    ws = st.workspace_bytes(Hq)
+    r.update({"bytes": nbytes, "gbs": nbytes / (r["avg_us"] * 1e-6) / 1e9,
+              "Tq": st.quantized_tokens, "Tr": st.res_len,
+              "splits": ws // (st.B * Hq * (st.D + 2) * 4) if ws else 1})
+    return r
 
 
-def decode_loop(st, Hq, steps, warmup, R, seed, device):
-    """The timed decode loop: fused append + attention, then the flush when
-    the window reaches R."""
+def time_flush(st, iters=50):
+    """One decode-time flush (the G oldest residual tokens of every (b, kv
+    head) into a new chunk).  A flush moves no ring data, so undoing its
+    bookkeeping re-arms the same flush; the store is left as it was."""
+    if st.res_len < st.G:
+        raise ValueError("time_flush needs a window of at least G tokens")
+    st.reserve(st.n_chunks + 1)
+
+    def one():
+        st.flush()
+        st.n_chunks -= 1
+        st.res_start = (st.res_start - st.G) % st.R
+        st.res_len += st.G
+
+    r = time_calls(one, iters)
+    nbytes = flush_bytes(st.B, st.H, st.D, st.G, st.Gv)
+    r.update({"bytes": nbytes, "gbs": nbytes / (r["avg_us"] * 1e-6) / 1e9})
+    return r
+
+
+def decode_loop(st, q_all, k_new, v_new, steps, warmup, R):
+    """The timed decode loop.  Step i: the new token is staged (the attention
+    launch writes it into the ring itself), the fused attention runs for one
+    query token per sequence, and the G oldest residual tokens are quantised
+    once the window holds R.  The caller sets the store up so that the first
+    timed step is a flush step: K timed steps then hold ceil(K / G) flushes
+    (exactly K / G when G divides K)."""
     import torch
     B, Hkv, D, G, Gv = st.B, st.H, st.D, st.G, st.Gv
-    n = steps + warmup
-    g = torch.Generator(device=device).manual_seed(seed)
-    k_new, v_new = synth_kv(B, Hkv, n, D, seed + 1, device)
-    q_all = torch.randn(n, B, Hq, D, generator=g, device=device) * D ** -0.5
-    out = torch.empty(B, Hq, D, device=device)
+    Hq = q_all.shape[2]
+    out = torch.empty(B, Hq, D, device=q_all.device)
 
     def step(i):
-        # the new token is written by the attention launch itself; the G
-        # oldest residual tokens are quantised once the window holds R
         st.stage_token(k_new[:, :, i:i + 1], v_new[:, :, i:i + 1])
-        nb = append_bytes(B, Hkv, D)
-        nb += attn_bytes(B, Hq, Hkv, D, st.quantized_tokens, st.res_len, G, Gv)
+        nb = attn_bytes(B, Hq, Hkv, D, st.quantized_tokens, st.res_len, G, Gv)
+        nb += fused_append_bytes(B, Hkv, D)
         st.attention(q_all[i], out=out)
         flushes = 0
         while st.res_len >= R:
@@ -162,95 +216,90 @@ def decode_loop(st, Hq, steps, warmup, R, seed, device):
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     total_bytes = total_flushes = 0
+    ctx0 = st.quantized_tokens + st.res_len + 1
     wall0 = time.perf_counter()
     t0.record()
-    for i in range(warmup, n):
+    for i in range(warmup, warmup + steps):
         nb, fl = step(i)
         total_bytes += nb
         total_flushes += fl
     t1.record()
     submit = time.perf_counter() - wall0     # host time to issue the K steps
     torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
     ms = t0.elapsed_time(t1)
-    return {"ms": ms, "wall_s": wall, "submit_s": submit, "bytes": total_bytes,
-            "flushes": total_flushes,
+    return {"ms": ms, "submit_s": submit, "bytes": total_bytes, "flushes": total_flushes,
+            "context": [ctx0, st.quantized_tokens + st.res_len],
             "gbs": total_bytes / (ms * 1e-3) / 1e9, "ms_per_step": ms / steps}
 
 
-def quantize_bench(device, iters=10):
-    """Config 2: keys [8,32,128,4096] (G=32 along tokens) + values
-    [8,32,4096,128] (G=32 along D); Mtokens/s where a token is one (b, t)
-    position with all 32 heads of K and V."""
+def codec_bench(kt, v, G, iters=10):
+    """Config 2 through the ``_C`` ops on device-resident inputs: keys
+    ``kt [B,H,D,Seq]`` quantised per channel along tokens, values
+    ``v [B,H,Seq,D]`` per token along channels, both in groups of G.  Times
+    the K+V pair of each op the reference exposes: quantise, dequantise and
+    the fused round-trip (the op KiviCache's flush calls,
+    src/kivi_sycl/cache/manager.py:338,345).  Mtokens/s counts (b, t)
+    positions with all heads of K and V."""
     import torch
     from intel_kivi_hybrid_amd import _C
-    B, H, D, S, G = 8, 32, 128, 4096, 32
-    N = B * H * D * S
-    k, v = synth_kv(B, H, S, D, 1236, device)
-    kt = k.transpose(2, 3).contiguous()
-    del k
-    kp = torch.empty(N // 4, dtype=torch.uint8, device=device)
-    ks = torch.empty(N // G, device=device)
-    kz = torch.empty(N // G, device=device)
+    B, H, D, S = kt.shape
+    N = kt.numel()
+    kp = torch.empty(N // 4, dtype=torch.uint8, device=kt.device)
+    ks = torch.empty(N // G, device=kt.device)
+    kz = torch.empty(N // G, device=kt.device)
     vp, vs, vz = torch.empty_like(kp), torch.empty_like(ks), torch.empty_like(kz)
+    kd = torch.empty_like(kt)
+    vd = torch.empty_like(v)
 
-    def one():
+    def quant():
         _C.quantize_keys_async(kt, kp, ks, kz, G)
         _C.quantize_values_async(v, vp, vs, vz, D, G)
 
-    for _ in range(2):
-        one()
-    torch.cuda.synchronize()
-    a = torch.cuda.Event(enable_timing=True)
-    b = torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(iters):
-        one()
-    b.record()
-    torch.cuda.synchronize()
-    us = a.elapsed_time(b) * 1e3 / iters
-    nbytes = 2 * quant_bytes(N, G)
+    def dequant():
+        _C.dequantize_keys_async(kp, ks, kz, kd, G)
+        _C.dequantize_values_async(vp, vs, vz, vd, D, G)
+
+    def roundtrip():
+        _C.quant_dequant_roundtrip_keys_async(kt, kd, G)
+        _C.quant_dequant_roundtrip_values_async(v, vd, D, G)
+
     tokens = B * S
-    res = {"us_per_pair": us, "gbs": nbytes / (us * 1e-6) / 1e9,
-           "mtokens_s": tokens / us, "bytes": nbytes, "tokens": tokens}
+    algo = {"quantize": 2 * quant_bytes(N, G), "dequantize": 2 * dequant_bytes(N, G),
+            "roundtrip": 2 * roundtrip_bytes(N)}
+    res = {}
+    for name, fn in (("quantize", quant), ("dequantize", dequant), ("roundtrip", roundtrip)):
+        r = time_calls(fn, iters)
+        us = r["avg_us"]
+        res[name] = {"us_per_pair": round(us, 1), "gbs": round(algo[name] / (us * 1e-6) / 1e9, 1),
+                     "mtokens_s": round(tokens / us, 2), "bytes": algo[name]}
     # round-trip error / scale (reported, not gated)
-    rt = torch.empty_like(v)
-    _C.quant_dequant_roundtrip_values(v, rt, D, G)
-    err = (rt - v).abs().reshape(-1, G).amax(dim=1)
+    _C.quant_dequant_roundtrip_values(v, vd, D, G)
+    _C.quantize_values(v, vp, vs, vz, D, G)
+    err = (vd - v).abs().reshape(-1, G).amax(dim=1)
     res["max_err_over_scale"] = float((err / vs).max())
     return res
 
 
-def prefill_bench(device, iters=20):
-    """Batched prefill flush: a 4096-token prompt of config 2's shape
-    (B=8, 32 kv heads, D=128) appended to an empty PackedKVStore (R=128,
-    G=32), which quantises its 125 owed chunks per (b, head) in one launch
-    reading the [B,H,T,D] K/V in place; fp32 and bf16 inputs.  Algorithmic
-    bytes: the flushed tokens' K/V read once plus the codes, scales and
-    zeros written; Mtokens/s counts (b, t) positions with all heads of K and
-    V."""
+def prefill_bench(k, v, device, iters=20):
+    """Batched prefill flush: a prompt ``k``/``v [B, H, T, D]`` appended to an
+    empty PackedKVStore (R=128, G=32), which quantises every chunk it owes in
+    one launch reading the K/V in place; fp32 and bf16 inputs.  Algorithmic
+    bytes: the flushed tokens' K/V read once plus the codes, scales and zeros
+    written; Mtokens/s counts (b, t) positions with all heads of K and V."""
     import torch
     from intel_kivi_hybrid_amd.store import PackedKVStore
-    B, H, T, D, G, R = 8, 32, 4096, 128, 32, 128
-    k, v = synth_kv(B, H, T, D, 1237, device)
+    B, H, T, D = k.shape
+    G, R = 32, 128
     out = {}
     for name, dt in (("fp32", torch.float32), ("bf16", torch.bfloat16)):
-        kk, vv = k.to(dt), v.to(dt)
+        kk, vv = k.to(device, dt), v.to(device, dt)
         st = PackedKVStore(B, H, D, G, R, device, chunk_capacity=T // G + 1)
 
         def one():
             st.reset()
             st.extend(kk, vv, flush_at=R)
 
-        settle_clocks(one)
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(iters):
-            one()
-        b.record()
-        torch.cuda.synchronize()
-        us = a.elapsed_time(b) * 1e3 / iters
+        us = time_calls(one, iters)["avg_us"]
         n_tok = st.n_chunks * G
         nbytes = (2 * B * H * n_tok * D * kk.element_size()       # K/V read
                   + 2 * B * H * n_tok * D // 4                     # codes
@@ -264,23 +313,107 @@ def prefill_bench(device, iters=20):
 
 
 # --------------------------------------------------------------------------
+# HBM traffic of the headline kernel (rocprofv3 counters, measured in the run)
+# --------------------------------------------------------------------------
+ATTN_KERNEL = "attn_mfma_kernel"
+COPY_BYTES = 512 << 20
+
+
+def traffic_workload(dev):
+    """Child-process workload for the counter passes: a 512 MiB device copy
+    (calibration: it reads and writes COPY_BYTES) and the config-4 attention
+    at the roofline state.  Counters do not depend on the values, so the
+    store is filled from the GPU's own generator here (fast)."""
+    import torch
+    from intel_kivi_hybrid_amd.store import PackedKVStore
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(7)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    del src, dst
+    B, Hq, Hkv, D, T, R, G = CONFIG4
+    g = torch.Generator(device=dev).manual_seed(11)
+    st = PackedKVStore(B, Hkv, D, G, R, dev, chunk_capacity=T // G + 1)
+    st.extend(torch.randn(B, Hkv, T - 1, D, generator=g, device=dev),
+              torch.randn(B, Hkv, T - 1, D, generator=g, device=dev), flush_at=R)
+    st.append(torch.randn(B, Hkv, 1, D, generator=g, device=dev),
+              torch.randn(B, Hkv, 1, D, generator=g, device=dev))
+    q = torch.randn(B, Hq, D, generator=g, device=dev) * D ** -0.5
+    for _ in range(3):
+        st.attention(q)
+    torch.cuda.synchronize()
+
+
+def _counter_means(outdir, counter):
+    """Mean value of ``counter`` per dispatch for the copy kernel and the
+    attention kernel, from rocprofv3's counter-collection CSV."""
+    import csv
+    import glob
+    vals = {"copy": [], "attn": []}
+    for path in glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True):
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != counter:
+                    continue
+                name = row.get("Kernel_Name", "")
+                key = "attn" if ATTN_KERNEL in name else "copy" if "copyBuffer" in name else None
+                if key:
+                    vals[key].append(float(row["Counter_Value"]))
+    if not vals["copy"] or not vals["attn"]:
+        raise RuntimeError(f"no {counter} rows for the copy and attention kernels in {outdir}")
+    return {k: sum(v) / len(v) for k, v in vals.items()}
+
+
+def measure_traffic(algo_bytes, log):
+    """HBM bytes per config-4 attention launch from two rocprofv3 --pmc passes
+    (FETCH_SIZE, then WRITE_SIZE, in KiB per dispatch) over a child process
+    running traffic_workload(), each scaled by what the counter reads for the
+    512 MiB copy in the same pass.  Returns the roofline's traffic fields, or
+    null traffic with the reason when the profiler is unavailable."""
+    import shutil
+    import subprocess
+    import tempfile
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
+        return {"traffic": None, "traffic_note": "rocprofv3 not found"}
+    means = {}
+    try:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            outdir = tempfile.mkdtemp(prefix=f"kivi_pmc_{counter}_")
+            cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", outdir, "-o", "p",
+                   "--", sys.executable, os.path.abspath(__file__), "--only", "traffic"]
+            log(f"[bench] traffic pass: rocprofv3 --pmc {counter}")
+            subprocess.run(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                           timeout=150, check=False)
+            means[counter] = _counter_means(outdir, counter)
+            shutil.rmtree(outdir, ignore_errors=True)
+    except Exception as e:             # the bench line must not depend on the profiler
+        return {"traffic": None, "traffic_note": f"counter pass failed: {e}"}
+    f_scale = COPY_BYTES / (means["FETCH_SIZE"]["copy"] * 1024)
+    w_scale = COPY_BYTES / (means["WRITE_SIZE"]["copy"] * 1024)
+    traffic = 1024 * (means["FETCH_SIZE"]["attn"] * f_scale + means["WRITE_SIZE"]["attn"] * w_scale)
+    return {"traffic": int(round(traffic)),
+            "traffic_note": (f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE in this run: "
+                             f"{means['FETCH_SIZE']['attn']:.1f} / {means['WRITE_SIZE']['attn']:.1f} "
+                             f"KiB per dispatch, scaled x{f_scale:.3f} / x{w_scale:.3f} (512 MiB copy); "
+                             f"{traffic / algo_bytes:.4f} x algorithmic bytes")}
+
+
+# --------------------------------------------------------------------------
 # CPU baselines (the reference's CPU path, restated; test infrastructure)
 # --------------------------------------------------------------------------
-def cpu_attention_baseline(B, Hq, Hkv, D, T, R, G, Gv, budget_s=10.0):
+def cpu_attention_baseline(k, v, Hq, Tq, G, Gv, B_total, budget_s=10.0):
     """What the reference does per decode step on the CPU: HF-style fp32
     attention (repeat_kv, QK^T*scale, softmax, PV) over the dequantised
     history + fp32 residual served by get_full_cache()
-    (src/kivi_sycl/cache/manager.py:251-290).  Timed on a sample of the batch
-    with all host threads; reported in the same algorithmic-bytes unit."""
+    (src/kivi_sycl/cache/manager.py:251-290).  ``k``/``v [nb, Hkv, T, D]``
+    are the first nb sequences of the GPU workload (the same bits); the
+    first Tq tokens are served through the oracle round-trip.  Timed with
+    all host threads, reported in the same algorithmic-bytes unit."""
     import torch
-    from oracle import codec  # noqa: F401  (the oracle codec builds the history below)
-    n_flush = (T - R) // G + 1
-    Tq, Tr = n_flush * G, T - n_flush * G
-    nb = max(1, min(B, 4))
-    g = torch.Generator().manual_seed(7)
-    k = torch.randn(nb, Hkv, T, D, generator=g)
-    v = torch.randn(nb, Hkv, T, D, generator=g)
-    # the served history is the mirror round-trip of each flushed chunk
+    from oracle import codec
+    nb, Hkv, T, D = k.shape
+    Tr = T - Tq
     kh = k[:, :, :Tq].reshape(nb, Hkv, Tq // G, G, D).transpose(3, 4).contiguous()
     kh = torch.from_numpy(codec.roundtrip_groups(kh.numpy(), G).reshape(kh.shape))
     kh = kh.transpose(3, 4).reshape(nb, Hkv, Tq, D)
@@ -288,7 +421,7 @@ def cpu_attention_baseline(B, Hq, Hkv, D, T, R, G, Gv, budget_s=10.0):
                           .reshape(nb, Hkv, Tq, D))
     K = torch.cat([kh, k[:, :, Tq:]], dim=2)
     V = torch.cat([vh, v[:, :, Tq:]], dim=2)
-    q = torch.randn(nb, Hq, 1, D, generator=g) * D ** -0.5
+    q = torch.randn(nb, Hq, 1, D, generator=torch.Generator().manual_seed(7)) * D ** -0.5
     rep = Hq // Hkv
 
     def step():
@@ -307,34 +440,41 @@ def cpu_attention_baseline(B, Hq, Hkv, D, T, R, G, Gv, budget_s=10.0):
     nbytes = attn_bytes(nb, Hq, Hkv, D, Tq, Tr, G, Gv)
     return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"{nb} of {B} sequences x {Hkv} kv heads, context {T} (Tq={Tq}, Tr={Tr}), "
-                      f"{n} steps in {n * dt:.1f}s; torch fp32 attention over the dequantised "
-                      f"history as the reference's HF model computes it on the CPU"}
+            "sample": f"{nb} of {B_total} sequences x {Hkv} kv heads of the same K/V, context "
+                      f"{T} (Tq={Tq}, Tr={Tr}), {n} steps in {n * dt:.1f}s; torch fp32 "
+                      f"attention over the dequantised history as the reference's HF model "
+                      f"computes it on the CPU"}
 
 
-def cpu_quantize_baseline(budget_s=8.0):
+def cpu_quantize_baseline(kt, v, G, B_total, budget_s=8.0):
     """The C oracle (one group per iteration, OpenMP over groups, the
-    reference kernels' loop structure) on 1/8 of config 2."""
-    import numpy as np
+    reference kernels' loop structure) on the first sequences of config 2's
+    own K/V (``kt [nb,H,D,Seq]``, ``v [nb,H,Seq,D]``)."""
     from oracle import codec
-    B, H, D, S, G = 1, 32, 128, 4096, 32
-    rng = np.random.default_rng(0)
-    k = rng.standard_normal((B, H, D, S), dtype=np.float32)
-    v = rng.standard_normal((B, H, S, D), dtype=np.float32)
-    codec.quantize_groups(k, G)
+    kn = kt.contiguous().numpy()
+    vn = v.contiguous().numpy()
+    nb, _, _, S = kt.shape
+    codec.quantize_groups(kn, G)
     n, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < budget_s and n < 1000:
-        codec.quantize_groups(k, G)
-        codec.quantize_groups(v, G)
+        codec.quantize_groups(kn, G)
+        codec.quantize_groups(vn, G)
         n += 1
     dt = (time.perf_counter() - t0) / n
-    return {"value": B * S / dt / 1e6, "unit": "Mtokens/s", "cores": codec.num_threads(),
+    return {"value": nb * S / dt / 1e6, "unit": "Mtokens/s", "cores": codec.num_threads(),
             "kind": "port",
-            "sample": f"keys [1,32,128,4096] + values [1,32,4096,128] (1/8 of config 2), "
-                      f"{n} passes in {n * dt:.1f}s"}
+            "sample": f"keys {list(kt.shape)} + values {list(v.shape)} ({nb} of {B_total} "
+                      f"sequences of config 2's K/V), {n} passes in {n * dt:.1f}s"}
 
 
 # --------------------------------------------------------------------------
+CONFIG4 = (64, 32, 8, 128, 8192, 128, 32)      # B, Hq, Hkv, D, context, R, G
+PRECISION = ("fp32 inputs and outputs; 2-bit codes with fp32 scales/zeros, bit-exact to the "
+             "reference codec; attention products on bf16 matrix cores with each fp32 factor "
+             "split into bf16 hi+lo (~2^-17 relative) and fp32 accumulation; softmax and "
+             "residual window in fp32")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -342,10 +482,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--attn-iters", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["config4", "attention", "quantize", "prefill", "copy"],
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 counter passes behind roofline.traffic")
+    ap.add_argument("--only", choices=["config4", "attention", "config3", "config5", "codec",
+                                       "prefill", "copy", "traffic"],
                     default=None,
                     help="run one workload (for profiling); 'copy' is a plain 512 MiB device "
-                         "copy used to calibrate the FETCH_SIZE / WRITE_SIZE counters")
+                         "copy for calibrating the FETCH_SIZE / WRITE_SIZE counters; "
+                         "'traffic' is the workload of the counter passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the KIVI hot path here is built and "
@@ -357,110 +501,179 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     dev = torch.device("cuda:0")
     log = lambda *a: print(*a, file=sys.stderr, flush=True)      # noqa: E731
+    only = args.only
+    W, K = args.warmup, args.steps
 
-    if args.only == "copy":
-        n = 512 << 20
-        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(7)
+    if only == "copy":
+        src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(7)
         dst = torch.empty_like(src)
         for _ in range(5):
             dst.copy_(src)
         torch.cuda.synchronize()
-        log(f"[bench] copy: {n} bytes read and {n} bytes written per launch, 5 launches")
+        log(f"[bench] copy: {COPY_BYTES} bytes read and written per launch, 5 launches")
         return
-
-    if args.only == "prefill":
-        for name, r in prefill_bench(dev).items():
-            log(f"[bench] prefill flush ({name}): {r}")
-        return
-    if args.only == "quantize":
-        qb = quantize_bench(dev)
-        log(f"[bench] config2 quantize K+V: {qb['us_per_pair']:.1f} us, {qb['gbs']:.0f} GB/s, "
-            f"{qb['mtokens_s']:.1f} Mtokens/s")
-        return
-
-    # ---- config 4: the headline decode loop -------------------------------
-    B, Hq, Hkv, D, T, R, G = 64, 32, 8, 128, 8192, 128, 32
-    log(f"[bench] config4 store: B={B} Hq={Hq} Hkv={Hkv} D={D} T={T} R={R} G={G}")
-    st = build_store(B, Hkv, D, G, G, R, T, 1234 + 4, dev,
-                     extra_chunks=(args.steps + args.warmup) // G + 2)
-    torch.cuda.synchronize()
-    if args.only == "attention":
-        r = time_attention(st, Hq, args.attn_iters, 5, dev)
-        log(f"[bench] attention only: {r}")
-        return
-    attn4 = time_attention(st, Hq, args.attn_iters, 5, dev)
-    log(f"[bench] config4 attention: {attn4['avg_us']:.1f} us, {attn4['gbs']:.0f} GB/s")
-    loop = decode_loop(st, Hq, args.steps, args.warmup, R, 99, dev)
-    log(f"[bench] config4 decode loop: {loop['ms_per_step'] * 1e3:.1f} us/step, "
-        f"{loop['gbs']:.0f} GB/s, {loop['flushes']} flushes (host issues a step in "
-        f"{loop['submit_s'] / args.steps * 1e6:.1f} us)")
-    del st
-    torch.cuda.empty_cache()
-    if args.only == "config4":
+    if only == "traffic":
+        traffic_workload(dev)
         return
 
     extra = {}
-    if args.only is None:
-        # ---- config 3 (MHA) and config 5 (long context, Gv=128) ------------
-        st3 = build_store(16, 32, 128, 32, 32, 128, 4096 + 128, 1234 + 3, dev)
-        a3 = time_attention(st3, 32, args.attn_iters, 6, dev)
+    loop = attn4 = None
+    # ---- config 4: the headline decode loop -------------------------------
+    if only in (None, "config4", "attention"):
+        B, Hq, Hkv, D, T, R, G = CONFIG4
+        Tq = T - R
+        # the store starts Tr0 tokens into its window so that the first timed
+        # step fills it to R and flushes
+        Tr0 = (R - 1) - (W % G)
+        n_new = W + K
+        log(f"[bench] config4: B={B} Hq={Hq} Hkv={Hkv} D={D} context {T} R={R} G={G}; "
+            f"making K/V on the CPU")
+        k, v = synth_kv(B, Hkv, store_tokens(Tq, Tr0, G, R) + n_new, D, 1234 + 4)
+        st = make_store(k[:, :, :Tq + Tr0], v[:, :, :Tq + Tr0], G, G, R, dev,
+                        extra_chunks=n_new // G + 2)
+        k_new = k[:, :, Tq + Tr0:].to(dev)
+        v_new = v[:, :, Tq + Tr0:].to(dev)
+        cpu_k4 = k[:4, :, :T].clone()
+        cpu_v4 = v[:4, :, :T].clone()
+        del k, v
+        gq = torch.Generator().manual_seed(5)
+        q_all = (torch.randn(n_new, B, Hq, D, generator=gq) * D ** -0.5).to(dev)
+        q4 = (torch.randn(B, Hq, D, generator=gq) * D ** -0.5).to(dev)
+        # roofline: the attention kernel alone at context T (Tq = T - R
+        # quantised, a full window of R), the first tokens of the loop filling it
+        m = R - Tr0
+        st.append(k_new[:, :, :m], v_new[:, :, :m])
+        attn4 = time_attention(st, q4, args.attn_iters)
+        st.rollback(m)
+        log(f"[bench] config4 attention: {attn4['avg_us']:.1f} us, {attn4['gbs']:.0f} GB/s "
+            f"(Tq={attn4['Tq']}, Tr={attn4['Tr']}, splits={attn4['splits']})")
+        if only == "attention":
+            return
+        flush4 = time_flush(st)
+        log(f"[bench] config4 flush: {flush4['avg_us']:.1f} us, {flush4['gbs']:.0f} GB/s")
+        loop = decode_loop(st, q_all, k_new, v_new, K, W, R)
+        log(f"[bench] config4 decode loop: {loop['ms_per_step'] * 1e3:.1f} us/step, "
+            f"{loop['gbs']:.0f} GB/s, {loop['flushes']} flushes in {K} steps, context "
+            f"{loop['context'][0]}..{loop['context'][1]} (host issues a step in "
+            f"{loop['submit_s'] / K * 1e6:.1f} us)")
+        extra["flush_config4"] = {k_: round(flush4[k_], 2) for k_ in ("avg_us", "gbs")}
+        del st, k_new, v_new, q_all
+        torch.cuda.empty_cache()
+        if only == "config4":
+            return
+
+    if only in (None, "config3"):
+        # ---- config 3: MHA, 4096 quantised + 128 residual tokens -----------
+        B3, H3, D3, R3, G3 = 16, 32, 128, 128, 32
+        k, v = synth_kv(B3, H3, 4096 + R3, D3, 1234 + 3)
+        st = make_store(k[:, :, :4096 + R3 - 1], v[:, :, :4096 + R3 - 1], G3, G3, R3, dev)
+        st.append(k[:, :, -1:].to(dev), v[:, :, -1:].to(dev))
+        del k, v
+        q = (torch.randn(B3, H3, D3, generator=torch.Generator().manual_seed(6))
+             * D3 ** -0.5).to(dev)
+        a3 = time_attention(st, q, args.attn_iters)
         log(f"[bench] config3 attention: {a3['avg_us']:.1f} us, {a3['gbs']:.0f} GB/s "
             f"(Tq={a3['Tq']}, Tr={a3['Tr']})")
-        del st3
+        extra["attention_config3"] = {k_: a3[k_] for k_ in ("avg_us", "gbs", "Tq", "Tr", "splits")}
+        del st
         torch.cuda.empty_cache()
-        st5 = build_store(4, 8, 128, 32, 128, 128, 131072 + 128, 1234 + 5, dev)
-        a5 = time_attention(st5, 32, args.attn_iters, 7, dev)
+
+    if only in (None, "config5"):
+        # ---- config 5: 131072 quantised tokens, Gv=128, split-K + merge ----
+        B5, Hq5, H5, D5, R5, G5, Gv5 = 4, 32, 8, 128, 128, 32, 128
+        k, v = synth_kv(B5, H5, 131072 + R5, D5, 1234 + 5)
+        st = make_store(k[:, :, :131072 + R5 - 1], v[:, :, :131072 + R5 - 1], G5, Gv5, R5, dev)
+        st.append(k[:, :, -1:].to(dev), v[:, :, -1:].to(dev))
+        del k, v
+        q = (torch.randn(B5, Hq5, D5, generator=torch.Generator().manual_seed(7))
+             * D5 ** -0.5).to(dev)
+        a5 = time_attention(st, q, args.attn_iters)
+        f5 = time_flush(st)
+        step_us = a5["avg_us"] + f5["avg_us"]
         log(f"[bench] config5 attention: {a5['avg_us']:.1f} us, {a5['gbs']:.0f} GB/s "
-            f"(Tq={a5['Tq']}, Tr={a5['Tr']})")
-        del st5
+            f"(Tq={a5['Tq']}, Tr={a5['Tr']}, {a5['splits']} splits + merge); flush "
+            f"{f5['avg_us']:.1f} us; decode step {step_us:.1f} us")
+        extra["attention_config5"] = {k_: a5[k_] for k_ in ("avg_us", "gbs", "Tq", "Tr", "splits")}
+        extra["attention_config5"].update({
+            "flush_us": round(f5["avg_us"], 2), "step_us": round(step_us, 2),
+            "step_gbs": round((a5["bytes"] + f5["bytes"]) / (step_us * 1e-6) / 1e9, 1)})
+        del st
         torch.cuda.empty_cache()
-        extra["attention_config3"] = {k: a3[k] for k in ("avg_us", "gbs", "Tq", "Tr")}
-        extra["attention_config5"] = {k: a5[k] for k in ("avg_us", "gbs", "Tq", "Tr")}
 
-    qb = quantize_bench(dev)
-    log(f"[bench] config2 quantize K+V: {qb['us_per_pair']:.1f} us, {qb['gbs']:.0f} GB/s, "
-        f"{qb['mtokens_s']:.1f} Mtokens/s")
-    if args.only is None:
-        pf = prefill_bench(dev)
-        for name, r in pf.items():
-            log(f"[bench] prefill flush ({name} K/V, 4096-token prompt, B=8, 32 heads): "
-                f"{r['us']:.1f} us, {r['gbs']:.0f} GB/s, {r['mtokens_s']:.1f} Mtokens/s")
-        extra["prefill_flush"] = pf
+    qb = None
+    cpu_kt2 = cpu_v2 = None
+    if only in (None, "codec", "prefill"):
+        # ---- config 2: the _C codec ops and the batched prefill flush -------
+        B2, H2, S2, D2, G2 = 8, 32, 4096, 128, 32
+        k, v = synth_kv(B2, H2, S2, D2, 1234 + 2)
+        if only in (None, "codec"):
+            kt = k.transpose(2, 3).contiguous()
+            cpu_kt2, cpu_v2 = kt[:1].clone(), v[:1].clone()
+            qb = codec_bench(kt.to(dev), v.to(dev), G2)
+            del kt
+            for name in ("quantize", "dequantize", "roundtrip"):
+                r = qb[name]
+                log(f"[bench] config2 {name} K+V: {r['us_per_pair']:.1f} us, {r['gbs']:.0f} GB/s, "
+                    f"{r['mtokens_s']:.1f} Mtokens/s")
+            torch.cuda.empty_cache()
+        if only in (None, "prefill"):
+            pf = prefill_bench(k, v, dev)
+            for name, r in pf.items():
+                log(f"[bench] prefill flush ({name} K/V, {S2}-token prompt, B={B2}, {H2} heads): "
+                    f"{r['us']:.1f} us, {r['gbs']:.0f} GB/s, {r['mtokens_s']:.1f} Mtokens/s")
+            extra["prefill_flush"] = pf
+        del k, v
+        torch.cuda.empty_cache()
+    if only is not None:
+        return
 
+    B, Hq, Hkv, D, T, R, G = CONFIG4
     cpu = cpu_q = None
     if not args.no_cpu_baseline:
-        cpu = cpu_attention_baseline(B, Hq, Hkv, D, T, R, G, G)
+        cpu = cpu_attention_baseline(cpu_k4, cpu_v4, Hq, T - R, G, G, B)
         log(f"[bench] cpu baseline attention: {cpu}")
-        cpu_q = cpu_quantize_baseline()
+        cpu_q = cpu_quantize_baseline(cpu_kt2, cpu_v2, 32, 8)
         log(f"[bench] cpu baseline quantize: {cpu_q}")
+    traffic = {"traffic": None, "traffic_note": "not measured (--no-traffic)"}
+    if not args.no_traffic:
+        traffic = measure_traffic(attn4["bytes"], log)
+        log(f"[bench] traffic: {traffic}")
 
     line = {
         "metric": "packed-KV decode attention GB/s (% HBM peak) + quantize Mtokens/s, 1 GPU",
         "value": round(loop["gbs"], 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": K,
+        "warmup": W,
         "ms_per_step": round(loop["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": "synthetic (seeded N(0,1) K/V with channel/token outliers, made on the GPU)",
+        "precision": PRECISION,
+        "data": "synthetic: seeded N(0,1) K/V made on the CPU (4 key channels x10 per kv "
+                "head, 2% of value tokens x8 per sequence and head), copied to HBM before "
+                "timing; the CPU baselines use the same bits",
         "config": {"workload": "config4 Llama-3-8B GQA packed-KV decode loop",
                    "batch": B, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D,
                    "context": T, "residual": R, "group_size": G,
-                   "step": "attention with the new token appended in the same launch + flush when residual >= R"},
+                   "step": "attention with the new token appended in the same launch + flush "
+                           "of the 32 oldest residual tokens when the window reaches R",
+                   "flushes": loop["flushes"],
+                   "context_range": loop["context"]},
         "pct_hbm_peak": round(100 * loop["gbs"] / HBM_PEAK_GBS, 2),
-        "quantize_mtokens_s": round(qb["mtokens_s"], 2),
-        "quantize_gbs": round(qb["gbs"], 1),
+        "quantize_mtokens_s": qb["quantize"]["mtokens_s"],
+        "quantize_gbs": qb["quantize"]["gbs"],
         "quantize_config": "config2 keys [8,32,128,4096] G=32 + values [8,32,4096,128] G=32",
+        "codec_config2": {k_: qb[k_] for k_ in ("quantize", "dequantize", "roundtrip")},
         "quantize_max_err_over_scale": round(qb["max_err_over_scale"], 4),
         "roofline": {"bound": "hbm", "achieved": round(attn4["gbs"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(attn4["gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": ATTN4_TRAFFIC_BYTES if attn4["bytes"] == ATTN4_ALGO_BYTES else None,
-                     "kernel": "packed decode attention (config 4, one call)",
+                     "traffic": traffic["traffic"], "traffic_note": traffic["traffic_note"],
+                     "kernel": "attn_mfma_kernel<4,128,32,4,false>, config 4, one call "
+                               f"(Tq={attn4['Tq']}, Tr={attn4['Tr']})",
                      "avg_us": round(attn4["avg_us"], 2), "bytes_per_launch": attn4["bytes"]},
         "cpu_baseline": cpu,
         "cpu_baseline_quantize": cpu_q,

@@ -120,6 +120,15 @@ def encode_codes(codes: torch.Tensor, G: int, D: int, layout: int, key: bool) ->
     return b.to(torch.uint8).reshape(*lead, G * D // 4)
 
 
+def decode_geometry_error(q_heads: int, kv_heads: int, head_dim: int, group_size: int,
+                          group_size_v: int) -> Optional[str]:
+    """None if the fused decode attention runs stores of this geometry (any
+    context length), else the reason it would refuse them."""
+    rc = _lib.kivi_packed_decode_attention_supported(q_heads, kv_heads, head_dim, group_size,
+                                                     group_size_v)
+    return None if rc == 0 else _native.last_error()
+
+
 class PackedKVStore:
     """Residual ring + packed chunks for one layer (all on ``device``)."""
 
@@ -357,6 +366,18 @@ class PackedKVStore:
     def reset(self) -> None:
         self.res_start = self.res_len = self.n_chunks = 0
         self._pending = None
+
+    def rollback(self, n: int) -> None:
+        """Drop the newest ``n`` tokens of the residual window, e.g. draft
+        tokens that a speculative decode rejects (HF ``Cache.crop``).  Only
+        tokens not yet quantised can be dropped: a flushed chunk is final."""
+        n = int(n)
+        if n < 0 or n > self.res_len:
+            raise ValueError(f"cannot roll back {n} tokens: the residual window holds "
+                             f"{self.res_len} (quantised tokens cannot be rolled back)")
+        if n and self._pending is not None:
+            self._pending = None          # the staged token is the newest
+        self.res_len -= n
 
     _TENSORS = ("k_res", "v_res", "k_codes", "k_scale", "k_zero", "v_codes", "v_scale",
                 "v_zero", "k_hist", "v_hist")
