@@ -187,6 +187,14 @@ int kivi_store_code_layout(int32_t head_dim, int32_t group_size_k, int32_t group
  * {1,2,4,8}, head_dim % 16 == 0 and <= 256; plain-layout stores also need
  * group_size_k % 16 == 0 and <= 64.  Matrix-core-layout stores run on the
  * bf16 MFMA units with fp32 accumulation (relative error ~1e-5). */
+/* 0 if kivi_packed_decode_attention can run a store of this geometry (for
+ * any context length), else the KIVI_ERR_* code its launch would return, with
+ * the message in kivi_last_error().  No reference counterpart; it lets a
+ * cache refuse a geometry when it is built instead of at its first decode. */
+int kivi_packed_decode_attention_supported(int32_t q_heads, int32_t kv_heads,
+                                           int32_t head_dim, int32_t group_size_k,
+                                           int32_t group_size_v);
+
 size_t kivi_packed_decode_attention_workspace_size(int32_t batch, int32_t q_heads,
                                                    int32_t kv_heads, int32_t head_dim,
                                                    int32_t group_size_k, int32_t group_size_v,

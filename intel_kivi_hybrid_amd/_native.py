@@ -44,6 +44,7 @@ SIGNATURES = {
     "kivi_store_append": [_vp, _vp, _i32, _i64, _i64, _i64, _i32, _vp, _vp, _i32, _i32, _i32,
                           _i32, _i32, _i32, _vp],
     "kivi_store_code_layout": [_i32, _i32, _i32],
+    "kivi_packed_decode_attention_supported": [_i32, _i32, _i32, _i32, _i32],
     "kivi_packed_decode_attention_workspace_size": [_i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                                     _i32, _i32],
     "kivi_packed_decode_attention_append": [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp,

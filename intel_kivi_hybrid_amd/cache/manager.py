@@ -61,7 +61,14 @@ def _build_cache(layers):
 
 def _resolve_device(device) -> torch.device:
     """The store lives on a HIP device ("cuda" on ROCm torch).  The
-    reference's "xpu" spelling is accepted as an alias for it."""
+    reference's "xpu" spelling is accepted as an alias for it.
+
+    The reference also runs its cache with ``device="cpu"`` behind a stubbed
+    ``_C`` (tests/unit/test_manager_bookkeeping.py:72-80,166-170), because its
+    flush only crosses to the device for the round-trip op.  Here the whole
+    state (residual ring, packed chunks, served history) is device memory
+    written by the HIP kernels, so a CPU cache is refused; the CPU restatement
+    of that bookkeeping is the test oracle (oracle/kivi_cache.py)."""
     name = str(device)
     if name.startswith("xpu"):
         name = "cuda" + name[3:]
@@ -69,7 +76,10 @@ def _resolve_device(device) -> torch.device:
     if dev.type != "cuda":
         raise ValueError(
             f"KiviCache keeps its packed store and residual window in GPU memory; "
-            f"device must be a HIP device ('cuda' or 'cuda:N'), got {device!r}")
+            f"device must be a HIP device ('cuda' or 'cuda:N'), got {device!r}. "
+            f"(The reference's CPU cache with a stubbed _C, as in its "
+            f"test_manager_bookkeeping.py, has no counterpart here: every flush "
+            f"and append runs a HIP kernel.)")
     return dev
 
 

@@ -40,7 +40,7 @@ from transformers.modeling_utils import AttentionInterface
 
 from ..config.model_config import detect_model_config
 from ..extension.loader import kivi_native  # noqa: F401  (fails loudly without the HIP library)
-from ..store import PackedKVStore
+from ..store import PackedKVStore, decode_geometry_error
 from .manager import _resolve_device
 
 __all__ = ["KIVI_ATTENTION", "FORMAT_NAME", "FORMAT_VERSION", "KiviPackedCache",
@@ -252,6 +252,16 @@ class KiviPackedCache(Cache):
             f"head_dim ({head_dim}) must be divisible by value group size ({gv})"
         assert group_size <= residual_length, (
             f"group_size ({group_size}) must not exceed residual_length ({residual_length})")
+        # Refuse a geometry the decode kernel cannot run now, not at the first
+        # decode step after the prompt (the query-head ratio is checked at the
+        # first attention call, where the query's head count is known).
+        err = decode_geometry_error(num_kv_heads or 1, num_kv_heads or 1, head_dim, group_size,
+                                    gv)
+        if err:
+            raise ValueError(f"KiviPackedCache: the packed decode attention does not support "
+                             f"head_dim={head_dim}, group_size={group_size}, "
+                             f"value_group_size={gv}: {err}")
+        self._heads_checked = False
         register_packed_attention()
         self.device = _resolve_device(device)
         self.head_dim = head_dim
@@ -384,6 +394,15 @@ def kivi_packed_attention_forward(module, query, key, value, attention_mask, sca
     if layer is None:
         raise RuntimeError(f"the '{KIVI_ATTENTION}' attention needs past_key_values to be a "
                            f"KiviPackedCache and use_cache=True")
+    owner = layer.owner
+    if not owner._heads_checked:
+        err = decode_geometry_error(query.shape[1], key.shape[1], owner.head_dim, owner.G,
+                                    owner.Gv)
+        if err:
+            raise ValueError(f"KiviPackedCache: {query.shape[1]} query heads over "
+                             f"{key.shape[1]} kv heads cannot be decoded from the packed "
+                             f"store: {err}")
+        owner._heads_checked = True
     if layer._prompt or query.shape[2] > 1:
         return sdpa_attention_forward(module, query, key, value, attention_mask,
                                       dropout=dropout, scaling=scaling, **kwargs)

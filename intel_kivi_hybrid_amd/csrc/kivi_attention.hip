@@ -373,6 +373,28 @@ Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
 // workgroup covers a row.
 bool needs_workspace(const Plan& p) { return p.n_splits > 1; }
 
+// Head and group geometry every decode launch needs, whatever its context.
+int check_geometry(int q_heads, int kv_heads, int head_dim, int group_size_k,
+                   int group_size_v) {
+    if (kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads)
+        return set_error(kErrInvalidArgument,
+                         "q_heads (%d) must be a positive multiple of kv_heads (%d)",
+                         q_heads, kv_heads);
+    const int hg = q_heads / kv_heads;
+    if (hg != 1 && hg != 2 && hg != 4 && hg != 8)
+        return set_error(kErrUnsupported, "q_heads / kv_heads = %d (supported: 1, 2, 4, 8)", hg);
+    if (head_dim <= 0 || head_dim % 16 || head_dim > kMaxD)
+        return set_error(kErrUnsupported, "head_dim %d (supported: multiple of 16, <= %d)",
+                         head_dim, kMaxD);
+    if (group_size_k <= 0 || group_size_k % 4 || group_size_v <= 0 || group_size_v % 4 ||
+        head_dim % group_size_v)
+        return set_error(kErrInvalidArgument,
+                         "group sizes must be positive multiples of 4 and group_size_v must "
+                         "divide head_dim (got %d, %d, head_dim %d)", group_size_k,
+                         group_size_v, head_dim);
+    return kOk;
+}
+
 }  // namespace
 
 int launch_attention_mfma(const AttnLaunch& a, hipStream_t st) {
@@ -396,6 +418,35 @@ int launch_attention_mfma(const AttnLaunch& a, hipStream_t st) {
 using namespace kivi;
 
 extern "C" {
+
+int kivi_packed_decode_attention_supported(int32_t q_heads, int32_t kv_heads,
+                                           int32_t head_dim, int32_t group_size_k,
+                                           int32_t group_size_v) {
+    int rc = check_geometry(q_heads, kv_heads, head_dim, group_size_k, group_size_v);
+    if (rc) return rc;
+    if (code_layout_for(head_dim, group_size_k, group_size_v) == kLayoutPlain) {
+        if (group_size_k % 16 || group_size_k > kWave)
+            return set_error(kErrUnsupported,
+                             "group_size_k %d (supported: multiple of 16, <= 64)", group_size_k);
+        return kOk;
+    }
+    const int lds = attention_mfma_lds_bytes(q_heads / kv_heads, head_dim, group_size_k,
+                                             head_dim / group_size_v);
+    int dev = 0, limit = 160 * 1024;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) ==
+                hipSuccess && v > 0)
+            limit = v;
+    }
+    if (lds < 0 || lds > limit)
+        return set_error(kErrUnsupported,
+                         "decode attention with q_heads/kv_heads=%d, head_dim=%d, G=%d, "
+                         "group_size_v=%d needs %d bytes of LDS per workgroup; the device "
+                         "allows %d", q_heads / kv_heads, head_dim, group_size_k,
+                         group_size_v, lds, limit);
+    return kOk;
+}
 
 size_t kivi_packed_decode_attention_workspace_size(int32_t batch, int32_t q_heads,
                                                    int32_t kv_heads, int32_t head_dim,
@@ -424,22 +475,11 @@ static int decode_attention_impl(const float* q, const uint8_t* k_codes, const f
                                  int64_t new_sh, void* stream) {
     if (!q || !out)
         return set_error(kErrInvalidArgument, "null q/out pointer");
-    if (batch <= 0 || kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads)
-        return set_error(kErrInvalidArgument,
-                         "q_heads (%d) must be a positive multiple of kv_heads (%d)",
-                         q_heads, kv_heads);
+    if (batch <= 0)
+        return set_error(kErrInvalidArgument, "batch %d must be positive", batch);
+    int rc = check_geometry(q_heads, kv_heads, head_dim, group_size_k, group_size_v);
+    if (rc) return rc;
     const int hg = q_heads / kv_heads;
-    if (hg != 1 && hg != 2 && hg != 4 && hg != 8)
-        return set_error(kErrUnsupported, "q_heads / kv_heads = %d (supported: 1, 2, 4, 8)", hg);
-    if (head_dim <= 0 || head_dim % 16 || head_dim > kMaxD)
-        return set_error(kErrUnsupported, "head_dim %d (supported: multiple of 16, <= %d)",
-                         head_dim, kMaxD);
-    if (group_size_k <= 0 || group_size_k % 4 || group_size_v <= 0 || group_size_v % 4 ||
-        head_dim % group_size_v)
-        return set_error(kErrInvalidArgument,
-                         "group sizes must be positive multiples of 4 and group_size_v must "
-                         "divide head_dim (got %d, %d, head_dim %d)", group_size_k,
-                         group_size_v, head_dim);
     if (num_chunks < 0 || res_len < 0 || num_chunks + res_len == 0)
         return set_error(kErrInvalidArgument, "empty context (num_chunks=%d, res_len=%d)",
                          num_chunks, res_len);
@@ -483,7 +523,7 @@ static int decode_attention_impl(const float* q, const uint8_t* k_codes, const f
     const int new_slot = k_new ? (res_start + res_len - 1) % res_capacity : 0;
     if (k_new && !p.mfma) {
         // the generic kernel reads the ring only: file the token there first
-        const int rc = kivi_store_append(k_new, v_new, res_dtype, new_sb, new_sh, 0, 1,
+        rc = kivi_store_append(k_new, v_new, res_dtype, new_sb, new_sh, 0, 1,
                                          const_cast<void*>(k_res), const_cast<void*>(v_res),
                                          res_dtype, batch, kv_heads, head_dim, res_capacity,
                                          new_slot, stream);
@@ -495,7 +535,7 @@ static int decode_attention_impl(const float* q, const uint8_t* k_codes, const f
                      group_size_v, chunk_capacity, num_chunks, res_capacity, res_start, res_len,
                      p.n_qsplits, p.chunks_per_wave, p.res_waves, p.early_per_pass_x2, p.n_splits,
                      softmax_scale * kLog2e, k_new, v_new, new_sb, new_sh, new_slot, res_dtype};
-        int rc = launch_attention_mfma(L, st);
+        rc = launch_attention_mfma(L, st);
         if (rc || !needs_workspace(p)) return rc;
     } else {
         AttnArgs a{q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res, v_res, out,
@@ -511,7 +551,7 @@ static int decode_attention_impl(const float* q, const uint8_t* k_codes, const f
             case 4: attn_generic_kernel<4><<<grid, kAttnBlock, lds, st>>>(a); break;
             case 8: attn_generic_kernel<8><<<grid, kAttnBlock, lds, st>>>(a); break;
         }
-        int rc = check_launch("packed_decode_attention");
+        rc = check_launch("packed_decode_attention");
         if (rc || !needs_workspace(p)) return rc;
     }
     attn_merge_kernel<<<dim3(q_heads, batch), head_dim, 0, st>>>(part_o, part_ml, out,

@@ -54,4 +54,9 @@ int launch_attention_mfma_hg2_r16(const AttnLaunch& a, hipStream_t stream);
 int launch_attention_mfma_hg4_r16(const AttnLaunch& a, hipStream_t stream);
 int launch_attention_mfma_hg8_r16(const AttnLaunch& a, hipStream_t stream);
 
+// LDS bytes per workgroup of the matrix-core kernel for HG query heads per
+// kv head, head_dim D, key group G and NG value groups per token (-1 for a
+// shape it has no instance of).
+int attention_mfma_lds_bytes(int HG, int D, int G, int NG);
+
 }  // namespace kivi

@@ -36,6 +36,10 @@ def test_device_rules():
     assert KiviCache(1, 8, group_size=4, residual_length=8, device="xpu:1").device == torch.device("cuda:1")
     with pytest.raises(ValueError, match="HIP device"):
         KiviCache(1, 8, group_size=4, residual_length=8, device="cpu")
+    # the reference's own unit tests build a CPU cache behind a stubbed _C
+    # (tests/unit/test_manager_bookkeeping.py:72-80); the error names that use
+    with pytest.raises(ValueError, match="stubbed _C"):
+        KiviCache(1, 8, group_size=4, residual_length=8, device="cpu")
 
 
 def test_signatures_match_reference():

@@ -210,3 +210,19 @@ def test_gqa_model(cpu_store, monkeypatch):
     ref = gen_mod.generate(model, tok, "grouped query heads", max_new_tokens=60,
                            group_size=32, residual_length=32)
     assert ours.split() == ref.split()
+
+
+def test_unsupported_geometry_refused_up_front(cpu_store):
+    """Geometries the decode kernel cannot run are refused when the cache is
+    built, not at the first decode step after the prompt has been stored."""
+    from intel_kivi_hybrid_amd.store import decode_geometry_error
+    with pytest.raises(ValueError, match="group_size_k 8"):
+        pc.KiviPackedCache(2, 64, 2, group_size=8, residual_length=32)
+    with pytest.raises(ValueError, match="head_dim 72"):
+        pc.KiviPackedCache(2, 72, 2, group_size=8, residual_length=32)
+    with pytest.raises(ValueError, match="head_dim 512"):
+        pc.KiviPackedCache(2, 512, 2, group_size=32, residual_length=32)
+    assert decode_geometry_error(8, 2, 128, 32, 32) is None
+    assert decode_geometry_error(4, 4, 64, 32, 64) is None
+    assert "q_heads / kv_heads = 3" in decode_geometry_error(6, 2, 64, 32, 32)
+    assert "needs" in decode_geometry_error(8, 1, 256, 64, 32)     # LDS beyond the device's
