@@ -212,6 +212,30 @@ int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const f
                                  int32_t res_len, float softmax_scale, int32_t num_splits,
                                  void* stream);
 
+/* Size of the device-resident scratch array behind
+ * kivi_packed_decode_attention_noalloc: 8 MiB per GPU, held until the process
+ * ends. */
+#define KIVI_NOALLOC_SCRATCH_BYTES (8u << 20)
+
+/* kivi_packed_decode_attention without a workspace argument and without any
+ * allocation: no reference counterpart; it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments (minus workspace), same
+ * kernels and the same result bit for bit.  The split partials live in a
+ * library-owned device array of KIVI_NOALLOC_SCRATCH_BYTES per GPU, whose
+ * address is resolved on the first call made with that GPU current.  A launch
+ * whose partials exceed that size (kivi_packed_decode_attention_workspace_size)
+ * is rejected with KIVI_ERR_INVALID_ARGUMENT before anything runs.  Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (on
+ * different streams, unordered) race and must not be issued. */
+int kivi_packed_decode_attention_noalloc(
+    const float* q, const uint8_t* k_codes, const float* k_scale, const float* k_zero,
+    const uint8_t* v_codes, const float* v_scale, const float* v_zero, const void* k_res,
+    const void* v_res, int32_t res_dtype, float* out, int32_t batch, int32_t q_heads,
+    int32_t kv_heads, int32_t head_dim, int32_t group_size_k, int32_t group_size_v,
+    int32_t chunk_capacity, int32_t num_chunks, int32_t res_capacity, int32_t res_start,
+    int32_t res_len, float softmax_scale, int32_t num_splits, void* stream);
+
 /* kivi_packed_decode_attention with this step's new token appended in the
  * same launch: the window (res_start, res_len) already counts the new token
  * as its last (index res_len - 1, ring slot (res_start + res_len - 1) %

@@ -21,6 +21,8 @@
 // log2 domain (q is pre-scaled by scale * log2(e)) so exp is a single v_exp_f32.
 #include <math.h>
 
+#include <mutex>
+
 #include "kivi_attention.hpp"
 #include "kivi_common.hpp"
 #include "../../include/kivi_hip.h"
@@ -415,6 +417,43 @@ int launch_attention_mfma(const AttnLaunch& a, hipStream_t st) {
 }
 }  // namespace kivi
 
+// Split partials of the allocation-free entry point: one copy of this array
+// per GPU, held until the process ends.  Host code never passes `scratch`
+// itself (in host code its name is a host-side stand-in, not a device
+// address); it resolves the device address once per device and uses that.
+static __device__ __align__(256) unsigned char scratch[KIVI_NOALLOC_SCRATCH_BYTES];
+
+namespace kivi {
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The device address of `scratch` on the current device, resolved with
+// hipGetSymbolAddress on the first call made with that device current.
+int scratch_for_current_device(void** out) {
+    int dev = -1;
+    int rc = check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (rc) return rc;
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        return set_error(kErrUnsupported, "device %d: the allocation-free entry point supports "
+                         "devices 0..%d", dev, kMaxScratchDevices - 1);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                       "hipGetSymbolAddress(scratch)");
+        if (rc) return rc;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return kOk;
+}
+
+}  // namespace
+}  // namespace kivi
+
 using namespace kivi;
 
 extern "C" {
@@ -575,6 +614,34 @@ int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const f
                                  kv_heads, head_dim, group_size_k, group_size_v, chunk_capacity,
                                  num_chunks, res_capacity, res_start, res_len, softmax_scale,
                                  num_splits, nullptr, nullptr, 0, 0, stream);
+}
+
+int kivi_packed_decode_attention_noalloc(
+        const float* q, const uint8_t* k_codes, const float* k_scale, const float* k_zero,
+        const uint8_t* v_codes, const float* v_scale, const float* v_zero, const void* k_res,
+        const void* v_res, int32_t res_dtype, float* out, int32_t batch, int32_t q_heads,
+        int32_t kv_heads, int32_t head_dim, int32_t group_size_k, int32_t group_size_v,
+        int32_t chunk_capacity, int32_t num_chunks, int32_t res_capacity, int32_t res_start,
+        int32_t res_len, float softmax_scale, int32_t num_splits, void* stream) {
+    const size_t need = kivi_packed_decode_attention_workspace_size(
+        batch, q_heads, kv_heads, head_dim, group_size_k, group_size_v, num_chunks, res_len,
+        num_splits);
+    if (need > (size_t)KIVI_NOALLOC_SCRATCH_BYTES)
+        return set_error(kErrInvalidArgument,
+                         "this launch needs %zu bytes of split partials; the allocation-free "
+                         "entry point holds at most %zu (pass fewer splits, or use "
+                         "kivi_packed_decode_attention with a workspace)", need,
+                         (size_t)KIVI_NOALLOC_SCRATCH_BYTES);
+    // The scratch address of this device is resolved on the first call made
+    // with it current, and kept.
+    void* ws = nullptr;
+    const int rc = scratch_for_current_device(&ws);
+    if (rc) return rc;
+    return decode_attention_impl(q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
+                                 v_res, res_dtype, out, ws, KIVI_NOALLOC_SCRATCH_BYTES, batch,
+                                 q_heads, kv_heads, head_dim, group_size_k, group_size_v,
+                                 chunk_capacity, num_chunks, res_capacity, res_start, res_len,
+                                 softmax_scale, num_splits, nullptr, nullptr, 0, 0, stream);
 }
 
 int kivi_packed_decode_attention_append(

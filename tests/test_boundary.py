@@ -212,3 +212,18 @@ def test_store_entry_points_reject_bad_arguments():
                                           64, 32, 32, 1, 0, 32, 0, 1, ctypes.c_float(0.1), 0,
                                           None)
     assert rc == 1 and "res_dtype 4" in _native.last_error()
+
+
+def test_noalloc_rejects_oversize_partials_on_host():
+    """The allocation-free attention entry point refuses a launch whose split
+    partials exceed its static scratch array, on the host, before it touches
+    a device (64 rows x 32 heads x 64 splits x (128 + 2) floats = 68 MB >
+    8 MiB)."""
+    from intel_kivi_hybrid_amd import _native
+    lib = _native.load()
+    rc = lib.kivi_packed_decode_attention_noalloc(
+        None, None, None, None, None, None, None, None, None, 0, None,
+        64, 32, 8, 128, 32, 32, 2000, 1000, 128, 0, 0, 0.088, 64, None)
+    assert rc == 1
+    msg = _native.last_error()
+    assert "allocation-free entry point holds at most 8388608" in msg, msg
