@@ -33,6 +33,7 @@ namespace {
 constexpr int kAttnWaves = 4;
 constexpr int kAttnBlock = kAttnWaves * kWave;
 constexpr int kMaxD = 256;
+constexpr int kMaxSplits = 4096;       // the merge kernel keeps 2 floats per split in LDS
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
@@ -290,22 +291,56 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
     }
 }
 
-// Merge split partials: grid (Hq, B), one thread per channel.
+// Merge split partials: grid (Hq, B), one thread per channel, dynamic LDS of
+// 2*S floats.  The S (m, l) pairs are read in parallel (one per thread) and
+// turned into weights f_s = 2^(m_s - M) in LDS; each thread then sums its
+// channel over the S partial rows with every load in flight at once (the
+// loop is unrolled), so the kernel costs about two memory round trips
+// however many splits there are.  The sums run in split order with fmaf, as
+// a plain sequential merge would.
 __global__ __launch_bounds__(kMaxD) void attn_merge_kernel(const float* __restrict__ part_o,
                                                            const float* __restrict__ part_ml,
                                                            float* __restrict__ out, int Hq,
                                                            int D, int S) {
+    extern __shared__ float wl[];                 // [S] weights, then [S] l
+    __shared__ float red[kMaxD / kWave];
     const int64_t row = (int64_t)blockIdx.y * Hq + blockIdx.x;
     const float* ml = part_ml + row * S * 2;
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, ml[2 * s]);
-    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    const int tid = threadIdx.x, nt = blockDim.x;
+    float mloc = -INFINITY;
+    for (int s = tid; s < S; s += nt) {
+        const float m = ml[2 * s];
+        wl[s] = m;
+        wl[S + s] = ml[2 * s + 1];
+        mloc = fmaxf(mloc, m);
+    }
+    mloc = wave_max(mloc);
+    if (tid % kWave == 0) red[tid / kWave] = mloc;
+    __syncthreads();
+    float M = red[0];
+    for (int w = 1; w < (nt + kWave - 1) / kWave; ++w) M = fmaxf(M, red[w]);
+    for (int s = tid; s < S; s += nt) {
+        const float m = wl[s];
+        wl[s] = m == -INFINITY ? 0.f : exp2f(m - M);
+    }
+    __syncthreads();
+    for (int d = tid; d < D; d += nt) {
+        const float* po = part_o + row * S * D + d;
         float acc = 0.f, L = 0.f;
-        for (int s = 0; s < S; ++s) {
-            const float ms = ml[2 * s];
-            const float f = ms == -INFINITY ? 0.f : exp2f(ms - M);
-            acc = fmaf(f, part_o[(row * S + s) * D + d], acc);
-            L = fmaf(f, ml[2 * s + 1], L);
+        int s = 0;
+        for (; s + 8 <= S; s += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = po[(int64_t)(s + j) * D];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                acc = fmaf(wl[s + j], v[j], acc);
+                L = fmaf(wl[s + j], wl[S + s + j], L);
+            }
+        }
+        for (; s < S; ++s) {
+            acc = fmaf(wl[s], po[(int64_t)s * D], acc);
+            L = fmaf(wl[s], wl[S + s], L);
         }
         out[row * D + d] = acc / L;
     }
@@ -343,7 +378,7 @@ Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
         // 3 chunks each per pass up front (measured best at config 4);
         // otherwise every wave takes passes before its chunks.
         // every split gets at least one chunk
-        S = max(1, min(S, (n_chunks + kWavesPerGroup - 1) / kWavesPerGroup));
+        S = max(1, min(min(S, kMaxSplits), (n_chunks + kWavesPerGroup - 1) / kWavesPerGroup));
         p.chunks_per_wave = (n_chunks + kWavesPerGroup * S - 1) / (kWavesPerGroup * S);
         p.n_qsplits = (n_chunks + kWavesPerGroup * p.chunks_per_wave - 1) /
                       (kWavesPerGroup * p.chunks_per_wave);
@@ -365,7 +400,7 @@ Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
         const int target_groups = 2048;
         S = (target_groups + B * Hkv - 1) / (B * Hkv);
     }
-    S = max(1, min(S, (p.n_units + kAttnWaves - 1) / kAttnWaves));
+    S = max(1, min(min(S, kMaxSplits), (p.n_units + kAttnWaves - 1) / kAttnWaves));
     p.units_per_split = (p.n_units + S - 1) / S;
     p.n_splits = (p.n_units + p.units_per_split - 1) / p.units_per_split;
     return p;
@@ -593,9 +628,8 @@ static int decode_attention_impl(const float* q, const uint8_t* k_codes, const f
         rc = check_launch("packed_decode_attention");
         if (rc || !needs_workspace(p)) return rc;
     }
-    attn_merge_kernel<<<dim3(q_heads, batch), head_dim, 0, st>>>(part_o, part_ml, out,
-                                                                  q_heads, head_dim,
-                                                                  p.n_splits);
+    attn_merge_kernel<<<dim3(q_heads, batch), head_dim, 2 * p.n_splits * sizeof(float), st>>>(
+        part_o, part_ml, out, q_heads, head_dim, p.n_splits);
     return check_launch("packed_decode_attention_merge");
 }
 

@@ -246,39 +246,69 @@ __global__ __launch_bounds__(kFlushBlock) void flush_kernel(FlushArgs a) {
     write_codes<LAYOUT, false>(codes, a.v_codes + chunk_id * code_bytes, G, D);
 }
 
-// 1/scale for code_rcp, or NaN when the scale is outside the range where
-// v_rcp_f32 is accurate, so that code_rcp flags every element of that group.
-__device__ __forceinline__ float rcp_or_nan(float scale) {
-    return (scale >= 1e-10f) && (scale <= 0x1.0p120f) ? __builtin_amdgcn_rcpf(scale)
-                                                       : __builtin_nanf("");
+// RN(1/scale) (this library is built with correctly rounded division), or
+// NaN when the scale lies outside [1e-10, 2^120], so that code_fast flags
+// every element of that group for the exact path.
+__device__ __forceinline__ float crcp_or_nan(float scale) {
+    return (scale >= 1e-10f) && (scale <= 0x1.0p120f) ? 1.0f / scale : __builtin_nanf("");
 }
 
-// Code of one element from its group's min and rcp_or_nan(scale): the
-// reciprocal path of encode4.  `bad` collects the elements that need the
-// exact divide (near a rounding tie, NaN input, or a flagged scale).
-__device__ __forceinline__ uint32_t code_rcp(float x, float mn, float r, bool& bad) {
-    const float u = fmaf(x - mn, r, 0.5f);
-    bad |= !(fabsf(__builtin_amdgcn_fractf(u) - 0.5f) < 0.5f - kTieGuard);
-    return (uint32_t)fminf(fmaxf(u, 0.0f), 3.0f);
+// Code of one element from its group's min and y = crcp_or_nan(scale).
+// u = fma(x - mn, y, 0.5 + kTieGuard) is within ~2 ulp of q + 0.5 +
+// kTieGuard, where q = RN((x - mn) / scale); whenever fract(u) >= 2 kTieGuard,
+// floor(u) = floor(q + 0.5), the code rounded half away from zero.  Otherwise
+// (q within kTieGuard of a rounding tie, NaN input, flagged scale) `bad` is
+// set and the caller recomputes the element with code_slow.  u <= 3.5 + 2
+// kTieGuard when the code is kept, so no clamp is needed.
+__device__ __forceinline__ uint32_t code_fast(float x, float mn, float y, bool& bad) {
+    const float u = fmaf(x - mn, y, 0.5f + kTieGuard);
+    bad |= !(__builtin_amdgcn_fractf(u) >= 2.0f * kTieGuard);
+    return (uint32_t)u;
+}
+
+// Slow path of code_fast, exact without a divide for every accepted scale:
+// with y = RN(1/s), q = RN(d*y) is within one ulp of d/s, the remainder
+// d - q*s is exact under an FMA, and RN(q + (d - q*s)*y) = RN(d/s)
+// (Markstein's theorem; d and s are normal and far from overflow for every
+// scale crcp_or_nan accepts).  For that quotient q1 in [0, 3],
+// (uint)(q1 + 0.5f) rounds half away from zero for every float except
+// 0.5 - 2^-25, where adding 0.5 rounds up to 1.0; that one value is
+// corrected.  A NaN input gives code 0, as code_exact does; a flagged scale
+// (NaN y) goes to code_exact.  Bit-exact with code_exact
+// (quantize_kernels.cpp:46-48, quant_tile.hpp:53-70) at about half its cost:
+// bf16-grid inputs sit on rounding ties in ~40% of 64-lane waves.
+__device__ __forceinline__ uint32_t code_slow(float x, float mn, float s, float y) {
+    if (__builtin_isnan(y)) return code_exact(x, mn, s);
+    const float d = x - mn;
+    const float q = d * y;
+    const float q1 = fmaf(fmaf(-q, s, d), y, q);
+    const uint32_t c = (uint32_t)fmaxf(q1 + 0.5f, 0.0f);
+    return c - (__float_as_uint(q1) == 0x3effffffu ? 1u : 0u);
 }
 
 // Matrix-core layout with compile-time shapes (G*D <= kTileMaxElems).  One
 // workgroup of 256 threads per (b, kv-head, chunk) loads the chunk's K and V
 // at once (V waits in registers while K is quantised).  Per tensor:
 //  1. the [G][D] tokens go to an fp32 LDS tile whose rows are padded by four
-//     floats (bank spread for the column and 8-channel reads below);
+//     floats; for values, rows 8..15 (mod 16) also hold their columns XORed
+//     with 16, which makes the column reads of step 3 bank-conflict free (rows
+//     8 apart would otherwise share banks) and keeps float4 groups whole;
 //  2. group statistics: keys -- thread (segment s, channel d) scans tokens
 //     [s*E, (s+1)*E) of channel d, segments combine through LDS; values --
 //     thread (token t, group g, segment s) scans channels [g*GV + s*E, +E),
 //     segments are adjacent lanes and combine with DPP.  Each group's
-//     (min, scale, rcp_or_nan(scale)) is published in LDS (scale and zero
+//     (min, scale, crcp_or_nan(scale)) is published in LDS (scale and zero
 //     also go to HBM);
 //  3. each thread builds whole output dwords of the matrix-core code order
 //     (16 codes: two tiles x 8 elements) from the tile and the group
 //     parameters and stores them straight to HBM, so codes never pass
-//     through LDS as bytes.
+//     through LDS as bytes.  Consecutive threads take consecutive lanes of
+//     the same code word (64 lanes, then the next word), which spreads a
+//     wave's tile reads over the banks.
+// HIST: the dequantised history is also written (a template parameter, so
+// that its test is not a branch per element).
 // Same codes, scales, zeros and history as flush_kernel.
-template <int G, int D, int GV, int SRC, int MODE>
+template <int G, int D, int GV, int SRC, int MODE, bool HIST>
 __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
     constexpr int N = G * D;
     constexpr int E = N / kFlushBlock;        // elements per thread in step 2
@@ -329,20 +359,24 @@ __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
             }
         }
     };
-    auto put = [&](const float4 (&x)[NV]) {
+    // Tile offset of (token t, channel c): keys plain, values with the
+    // channel XORed with 16 in rows 8..15 (mod 16).
+    auto kat = [](int t, int c) { return t * LD + c; };
+    auto vat = [](int t, int c) { return t * LD + (c ^ (16 * ((t >> 3) & 1))); };
+    auto put = [&](const float4 (&x)[NV], auto at) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int e = i * kFlushBlock + tid;
             const int t = e / (D / 4), d4 = e % (D / 4);
-            *reinterpret_cast<float4*>(tile + t * LD + 4 * d4) = x[i];
+            *reinterpret_cast<float4*>(tile + at(t, 4 * d4)) = x[i];
         }
     };
     // Dequantised tokens (written back into the tile) -> history rows.
-    auto copy_hist = [&](float* hist, int64_t row0) {
+    auto copy_hist = [&](float* hist, int64_t row0, auto at) {
         for (int e = tid; e < N / 4; e += kFlushBlock) {
             const int t = e / (D / 4), d4 = e % (D / 4);
             reinterpret_cast<float4*>(hist + (row0 + t) * D)[d4] =
-                *reinterpret_cast<const float4*>(tile + t * LD + 4 * d4);
+                *reinterpret_cast<const float4*>(tile + at(t, 4 * d4));
         }
     };
 
@@ -357,7 +391,7 @@ __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
         uint32_t* const vout = reinterpret_cast<uint32_t*>(a.v_codes + chunk_id * (N / 4));
 
         // ================================ keys ================================
-        put(kx);
+        put(kx, kat);
         lds_barrier();
         {
             const int d = tid % D, sg = tid / D;
@@ -385,7 +419,7 @@ __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
                 a.k_zero[chunk_id * D + d] = mn;
                 kpar[0][d] = mn;
                 kpar[1][d] = scale;
-                kpar[2][d] = rcp_or_nan(scale);
+                kpar[2][d] = crcp_or_nan(scale);
             }
         }
         lds_barrier();
@@ -395,7 +429,7 @@ __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
         for (int it = 0; it < NW; ++it) {
             const int e = it * kFlushBlock + tid;
             if (e < 64 * NP) {
-                const int l = e / NP, w = e % NP;
+                const int l = e % 64, w = e / 64;
                 uint32_t word = 0;
 #pragma unroll
                 for (int m = 0; m < 2; ++m) {
@@ -416,28 +450,29 @@ __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
                     bool bad = false;
                     uint32_t q[8];
 #pragma unroll
-                    for (int jj = 0; jj < 8; ++jj) q[jj] = code_rcp(x[jj], mnv[jj], rcv[jj], bad);
+                    for (int jj = 0; jj < 8; ++jj) q[jj] = code_fast(x[jj], mnv[jj], rcv[jj], bad);
                     if (__builtin_expect(bad, 0)) {
 #pragma unroll
-                        for (int jj = 0; jj < 8; ++jj) q[jj] = code_exact(x[jj], mnv[jj], scv[jj]);
+                        for (int jj = 0; jj < 8; ++jj)
+                            q[jj] = code_slow(x[jj], mnv[jj], scv[jj], rcv[jj]);
                     }
 #pragma unroll
                     for (int jj = 0; jj < 8; ++jj) {
                         word |= q[jj] << mfma_code_bit(m, jj);
-                        if (a.k_hist) tile[t * LD + d0 + jj] = decode1(q[jj], scv[jj], mnv[jj]);
+                        if constexpr (HIST) tile[t * LD + d0 + jj] = decode1(q[jj], scv[jj], mnv[jj]);
                     }
                 }
-                kout[e] = word;
+                kout[l * NP + w] = word;
             }
         }
-        if (a.k_hist) {
+        if constexpr (HIST) {
             lds_barrier();
-            copy_hist(a.k_hist, hist_row0);
+            copy_hist(a.k_hist, hist_row0, kat);
         }
 
         // =============================== values ===============================
         lds_barrier();
-        put(vx);
+        put(vx, vat);
         lds_barrier();
         {
             const int sg = tid % NSV, grp = tid / NSV;
@@ -446,7 +481,7 @@ __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
             float mn = 1e30f, mx = -1e30f;
 #pragma unroll
             for (int q4 = 0; q4 < E / 4; ++q4) {
-                const float4 f = *reinterpret_cast<const float4*>(tile + t * LD + c0 + 4 * q4);
+                const float4 f = *reinterpret_cast<const float4*>(tile + vat(t, c0 + 4 * q4));
                 mn = fmin_nan(fmin_nan(mn, f.x), fmin_nan(f.y, fmin_nan(f.z, f.w)));
                 mx = fmax_nan(fmax_nan(mx, f.x), fmax_nan(f.y, fmax_nan(f.z, f.w)));
             }
@@ -456,7 +491,7 @@ __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
             if (sg == 0) {
                 a.v_scale[(chunk_id * NG + gi) * G + t] = scale;
                 a.v_zero[(chunk_id * NG + gi) * G + t] = mn;
-                vpar[t * NG + gi] = make_float4(mn, scale, rcp_or_nan(scale), 0.0f);
+                vpar[t * NG + gi] = make_float4(mn, scale, crcp_or_nan(scale), 0.0f);
             }
         }
         lds_barrier();
@@ -466,7 +501,7 @@ __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
         for (int it = 0; it < NW; ++it) {
             const int e = it * kFlushBlock + tid;
             if (e < 64 * NP) {
-                const int l = e / NP, w = e % NP;
+                const int l = e % 64, w = e / 64;
                 uint32_t word = 0;
 #pragma unroll
                 for (int m = 0; m < 2; ++m) {
@@ -476,41 +511,48 @@ __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
                     float4 par[8];
 #pragma unroll
                     for (int jj = 0; jj < 8; ++jj) {
-                        x[jj] = tile[(t0 + jj) * LD + c];
+                        x[jj] = tile[vat(t0 + jj, c)];
                         par[jj] = vpar[(t0 + jj) * NG + c / GV];
                     }
                     bool bad = false;
                     uint32_t q[8];
 #pragma unroll
                     for (int jj = 0; jj < 8; ++jj)
-                        q[jj] = code_rcp(x[jj], par[jj].x, par[jj].z, bad);
+                        q[jj] = code_fast(x[jj], par[jj].x, par[jj].z, bad);
                     if (__builtin_expect(bad, 0)) {
 #pragma unroll
-                        for (int jj = 0; jj < 8; ++jj) q[jj] = code_exact(x[jj], par[jj].x, par[jj].y);
+                        for (int jj = 0; jj < 8; ++jj)
+                            q[jj] = code_slow(x[jj], par[jj].x, par[jj].y, par[jj].z);
                     }
 #pragma unroll
                     for (int jj = 0; jj < 8; ++jj) {
                         word |= q[jj] << mfma_code_bit(m, jj);
-                        if (a.v_hist) tile[(t0 + jj) * LD + c] = decode1(q[jj], par[jj].y, par[jj].x);
+                        if constexpr (HIST) tile[vat(t0 + jj, c)] = decode1(q[jj], par[jj].y, par[jj].x);
                     }
                 }
-                vout[e] = word;
+                vout[l * NP + w] = word;
             }
         }
-        if (a.v_hist) {
+        if constexpr (HIST) {
             lds_barrier();
-            copy_hist(a.v_hist, hist_row0);
+            copy_hist(a.v_hist, hist_row0, vat);
         }
+    }
+}
+
+template <int G, int D, int GV, int MODE, bool HIST>
+void launch_fast5(const FlushArgs& a, int src, dim3 grid, hipStream_t st) {
+    switch (src) {
+        case kSrcBF16: flush_fast_kernel<G, D, GV, kSrcBF16, MODE, HIST><<<grid, kFlushBlock, 0, st>>>(a); break;
+        case kSrcF16: flush_fast_kernel<G, D, GV, kSrcF16, MODE, HIST><<<grid, kFlushBlock, 0, st>>>(a); break;
+        default: flush_fast_kernel<G, D, GV, kSrcF32, MODE, HIST><<<grid, kFlushBlock, 0, st>>>(a); break;
     }
 }
 
 template <int G, int D, int GV, int MODE>
 void launch_fast4(const FlushArgs& a, int src, dim3 grid, hipStream_t st) {
-    switch (src) {
-        case kSrcBF16: flush_fast_kernel<G, D, GV, kSrcBF16, MODE><<<grid, kFlushBlock, 0, st>>>(a); break;
-        case kSrcF16: flush_fast_kernel<G, D, GV, kSrcF16, MODE><<<grid, kFlushBlock, 0, st>>>(a); break;
-        default: flush_fast_kernel<G, D, GV, kSrcF32, MODE><<<grid, kFlushBlock, 0, st>>>(a); break;
-    }
+    if (a.k_hist) launch_fast5<G, D, GV, MODE, true>(a, src, grid, st);
+    else launch_fast5<G, D, GV, MODE, false>(a, src, grid, st);
 }
 
 template <int G, int D, int GV>

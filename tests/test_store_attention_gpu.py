@@ -137,3 +137,31 @@ def test_attention_outlier_heavy_scores(store_cls):
     err = rel_err(out.cpu().numpy(), ref)
     print(f"[attn] outlier-heavy rel_err={err:.3e}", flush=True)
     assert err <= ATTN_TOL
+
+
+def test_split_workspace_reuse(store_cls):
+    """Split launches merge their partials in a second kernel.  On one
+    workspace, calls with different split counts, interleaved with a smaller
+    store's calls, give the oracle's result every time and the same bits
+    for the same split count."""
+    B, Hq, Hkv, D, G, R, T = 2, 8, 2, 128, 32, 128, 2000
+    k, v = make_kv(B, Hkv, T, D, seed=21)
+    st = store_cls(B, Hkv, D, G, R, "cuda:0")
+    fill_store(st, k, v, R)
+    small = store_cls(1, Hkv, D, G, R, "cuda:0")
+    fill_store(small, k[:1, :, :700], v[:1, :, :700], R)
+    q = seeded_q(B, Hq, D, seed=22).cuda()
+    kh, vh = oracle_history(k, v, st.n_chunks, G, G)
+    q0 = st.n_chunks * G
+    ref = decode_attention(q.cpu().numpy(), kh, vh, k[:, :, q0:].numpy(), v[:, :, q0:].numpy())
+    ws = torch.empty(1 << 22, dtype=torch.uint8, device="cuda:0")
+    first = None
+    for splits in (7, 3, 64, 7, 2, 7):
+        out = st.attention(q, num_splits=splits, workspace=ws)
+        small.attention(q[:1], num_splits=5, workspace=ws)
+        o = out.cpu().numpy()
+        assert rel_err(o, ref) <= ATTN_TOL
+        if splits == 7:
+            if first is None:
+                first = o.copy()
+            assert np.array_equal(o.view(np.uint32), first.view(np.uint32))

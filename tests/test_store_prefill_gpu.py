@@ -119,3 +119,42 @@ def test_chunks_straddle_ring_and_new_tokens(store_cls, first, second):
     expect = 0 if T < R else (T - R) // G + 1
     assert st.n_chunks == expect and st.res_len == T - expect * G
     check_store_bit_exact(st, k, v)
+
+
+def _tie_heavy(B, H, T, D, seed):
+    """K/V whose codes sit on rounding ties: bf16-grid values (a coarse grid
+    puts (x - min) / scale within a hair of k + 0.5 in ~40% of 64-lane
+    waves), plus groups made of exact ties ({0, 0.5, 1.5, 2.5, 3} * step:
+    scale = step, quotients exactly 0.5, 1.5, 2.5) and constant groups."""
+    k, v = make_kv(B, H, T, D, seed)
+    k = k.to(torch.bfloat16).float()
+    v = v.to(torch.bfloat16).float()
+    g = torch.Generator().manual_seed(seed + 5)
+    pattern = torch.tensor([0.0, 0.5, 1.5, 2.5, 3.0])
+    for h in range(H):
+        step = float(2.0 ** int(torch.randint(-6, 6, (1,), generator=g)))
+        # keys: channel 3 of head h cycles through exact-tie multiples (per
+        # 32-token group its min is 0 and max 3*step, so scale = step)
+        idx = torch.arange(T) % 5
+        k[:, h, :, 3] = pattern[idx] * step
+        # values: token 7 of every 32 holds exact ties along its channels
+        for t in range(7, T, 32):
+            v[:, h, t, :] = pattern[torch.arange(D) % 5] * step
+        k[:, h, :, 5] = 1.25                     # constant channel: scale 1e-10
+    return k, v
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,H,D,G,Gv,R,T", [(2, 4, 128, 32, 32, 128, 1200),
+                                            (1, 4, 64, 32, 32, 64, 700),
+                                            (2, 2, 128, 64, 128, 128, 600)])
+def test_prompt_on_rounding_ties(store_cls, dtype, B, H, D, G, Gv, R, T):
+    """Inputs full of exact and near rounding ties (bf16 grids, crafted tie
+    groups, constant groups) through the one-launch flush: codes, scales,
+    zeros and history bit-exact against the oracle (round half away from
+    zero of the correctly rounded quotient, quant_tile.hpp:53-70)."""
+    print(f"[prefill-ties] {dtype} B={B} H={H} D={D} G={G} Gv={Gv} R={R} T={T}", flush=True)
+    k, v = _tie_heavy(B, H, T, D, seed=T + D)
+    st = store_cls(B, H, D, G, R, "cuda:0", group_size_v=Gv, keep_history=True)
+    st.extend(k.to("cuda:0", dtype), v.to("cuda:0", dtype), flush_at=R)
+    check_store_bit_exact(st, k, v)
