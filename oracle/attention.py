@@ -45,3 +45,48 @@ def decode_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None):
             p /= p.sum(axis=1, keepdims=True)
             out[b, kh * g:(kh + 1) * g] = p @ V
     return out
+
+
+def prefix_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None):
+    """Causal attention of the window's last ``q_len`` tokens.
+
+    q: [B, q_len, Hq, D] -- the queries of the ``q_len`` newest tokens, which
+    are the last ``q_len`` tokens of the residual window (k_res/v_res
+    [B, Hkv, Tr, D], Tr >= q_len) after the dequantised history
+    k_hist/v_hist [B, Hkv, Tq, D].  Query token i (0-based) sits at position
+    Tq + Tr - q_len + i and attends to positions 0 .. Tq + Tr - q_len + i:
+    the HF model's causal mask over [cache ; new tokens] in a forward of
+    ``q_len`` tokens on a non-empty cache (the reference's own attention check
+    uses q_len=3, tests/integration/test_attention_fix.py:19-36,91-93).
+    GQA as in decode_attention.  Returns o [B, q_len, Hq, D] float64.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    B, L, Hq, D = q.shape
+    Hkv = k_res.shape[1]
+    if Hq % Hkv:
+        raise ValueError("Hq must be a multiple of Hkv")
+    if k_res.shape[2] < L:
+        raise ValueError("the residual window must hold the q_len new tokens")
+    g = Hq // Hkv
+    scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
+    out = np.empty((B, L, Hq, D), dtype=np.float64)
+    for b in range(B):
+        for kh in range(Hkv):
+            parts_k, parts_v = [], []
+            if k_hist is not None and k_hist.shape[2]:
+                parts_k.append(np.asarray(k_hist[b, kh], dtype=np.float64))
+                parts_v.append(np.asarray(v_hist[b, kh], dtype=np.float64))
+            parts_k.append(np.asarray(k_res[b, kh], dtype=np.float64))
+            parts_v.append(np.asarray(v_res[b, kh], dtype=np.float64))
+            K = np.concatenate(parts_k, axis=0)          # [T, D]
+            V = np.concatenate(parts_v, axis=0)
+            T = K.shape[0]
+            for i in range(L):
+                n = T - L + i + 1                        # visible tokens of query i
+                qh = q[b, i, kh * g:(kh + 1) * g]        # [g, D]
+                s = (qh @ K[:n].T) * scale               # [g, n]
+                s -= s.max(axis=1, keepdims=True)
+                p = np.exp(s)
+                p /= p.sum(axis=1, keepdims=True)
+                out[b, i, kh * g:(kh + 1) * g] = p @ V[:n]
+    return out

@@ -148,3 +148,80 @@ def test_vectorised_history_matches_per_chunk_oracle(B, H, D, G, Gv, n):
         assert np.array_equal(o["v_deq"].view(np.uint32), vh[:, :, c * G:(c + 1) * G].view(np.uint32))
     kh0, vh0 = oracle_history(k, v, 0, G, Gv)
     assert kh0.shape == (B, H, 0, D) and vh0.shape == (B, H, 0, D)
+
+
+# ---- multi-token queries (causal over the window's newest tokens) ----------
+PREFIX_SHAPES = [
+    # B, L (q_len), Hq, Hkv, D, Tq, Tr
+    (2, 3, 8, 2, 64, 96, 17),     # the reference's q_len=3, GQA 4
+    (1, 8, 4, 4, 32, 0, 8),       # the whole window is new tokens, no history
+    (2, 2, 6, 3, 16, 64, 40),
+    (1, 5, 8, 1, 32, 32, 9),
+]
+
+
+def _sdpa_prefix(q, kh, vh, kr, vr):
+    B, L, Hq, D = q.shape
+    Hkv = kr.shape[1]
+    K = torch.cat([kh, kr], dim=2).repeat_interleave(Hq // Hkv, dim=1)
+    V = torch.cat([vh, vr], dim=2).repeat_interleave(Hq // Hkv, dim=1)
+    T = K.shape[2]
+    mask = torch.arange(T)[None, :] <= (T - L + torch.arange(L))[:, None]     # [L, T]
+    o = torch.nn.functional.scaled_dot_product_attention(q.transpose(1, 2), K, V,
+                                                         attn_mask=mask)
+    return o.transpose(1, 2)                                                 # [B, L, Hq, D]
+
+
+def _prefix_err(fn, shape, seed):
+    B, L, Hq, Hkv, D, Tq, Tr = shape
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, L, Hq, D, generator=g, dtype=torch.float64)
+    kh, vh = (torch.randn(B, Hkv, Tq, D, generator=g, dtype=torch.float64) for _ in range(2))
+    kr, vr = (torch.randn(B, Hkv, Tr, D, generator=g, dtype=torch.float64) for _ in range(2))
+    out = fn(q.numpy(), kh.numpy(), vh.numpy(), kr.numpy(), vr.numpy())
+    return float(np.abs(out - _sdpa_prefix(q, kh, vh, kr, vr).numpy()).max())
+
+
+@pytest.mark.parametrize("shape", PREFIX_SHAPES)
+def test_prefix_oracle_matches_sdpa_float64(shape):
+    assert _prefix_err(oracle_attention.prefix_attention, shape, seed=sum(shape)) < 1e-12
+
+
+def test_prefix_oracle_reduces_to_decode():
+    """q_len = 1 is the decode case; the last of q_len tokens sees the whole
+    cache, so it equals decode attention of that token alone."""
+    B, L, Hq, Hkv, D, Tq, Tr = 2, 4, 8, 2, 32, 64, 11
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((B, L, Hq, D))
+    kh, vh = rng.standard_normal((2, B, Hkv, Tq, D))
+    kr, vr = rng.standard_normal((2, B, Hkv, Tr, D))
+    o = oracle_attention.prefix_attention(q, kh, vh, kr, vr)
+    assert np.array_equal(o[:, -1], decode_attention(q[:, -1], kh, vh, kr, vr))
+    o1 = oracle_attention.prefix_attention(q[:, :1], kh, vh, kr[:, :, :Tr - L + 1],
+                                           vr[:, :, :Tr - L + 1])
+    assert np.array_equal(o1[:, 0], o[:, 0])
+
+
+PREFIX_MUTANTS = {
+    "mask off by one": ("n = T - L + i + 1", "n = T - L + i + 2"),
+    "mask reversed": ("n = T - L + i + 1", "n = T - i"),
+    "head map": ("q[b, i, kh * g:(kh + 1) * g]", "q[b, i, kh::Hkv]"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(PREFIX_MUTANTS))
+def test_prefix_planted_mistakes_fail(name):
+    old, new = PREFIX_MUTANTS[name]
+    path = os.path.abspath(oracle_attention.__file__)
+    with open(path) as f:
+        src = f.read()
+    assert src.count(old) >= 1, f"mutation site for '{name}' not found"
+    mutant = types.ModuleType("oracle_prefix_mutant")
+    exec(compile(src.replace(old, new), path, "exec"), mutant.__dict__)
+    worst = 0.0
+    for shape in PREFIX_SHAPES:
+        try:
+            worst = max(worst, _prefix_err(mutant.prefix_attention, shape, seed=sum(shape)))
+        except (ValueError, IndexError):
+            worst = np.inf
+    assert worst > 1e-6, f"mutant '{name}' passes (max err {worst:.2e})"
