@@ -281,11 +281,14 @@ def codec_bench(kt, v, G, iters=10):
 
 
 def prefill_bench(k, v, device, iters=20):
-    """Batched prefill flush: a prompt ``k``/``v [B, H, T, D]`` appended to an
+    """Batched prefill: a prompt ``k``/``v [B, H, T, D]`` appended to an
     empty PackedKVStore (R=128, G=32), which quantises every chunk it owes in
-    one launch reading the K/V in place; fp32 and bf16 inputs.  Algorithmic
-    bytes: the flushed tokens' K/V read once plus the codes, scales and zeros
-    written; Mtokens/s counts (b, t) positions with all heads of K and V."""
+    one launch reading the K/V in place and copies the leftover tokens into
+    its residual ring (of the prompt's type, as KiviPackedCache keeps it);
+    fp32 and bf16 inputs.  Algorithmic bytes: the flushed tokens' K/V read
+    once plus the codes, scales and zeros written, and the leftover tokens
+    read and written once; Mtokens/s counts (b, t) positions with all heads
+    of K and V."""
     import torch
     from intel_kivi_hybrid_amd.store import PackedKVStore
     B, H, T, D = k.shape
@@ -293,7 +296,7 @@ def prefill_bench(k, v, device, iters=20):
     out = {}
     for name, dt in (("fp32", torch.float32), ("bf16", torch.bfloat16)):
         kk, vv = k.to(device, dt), v.to(device, dt)
-        st = PackedKVStore(B, H, D, G, R, device, chunk_capacity=T // G + 1)
+        st = PackedKVStore(B, H, D, G, R, device, chunk_capacity=T // G + 1, residual_dtype=dt)
 
         def one():
             st.reset()
@@ -304,7 +307,8 @@ def prefill_bench(k, v, device, iters=20):
         nbytes = (2 * B * H * n_tok * D * kk.element_size()       # K/V read
                   + 2 * B * H * n_tok * D // 4                     # codes
                   + B * H * st.n_chunks * D * 8                    # key scales + zeros
-                  + B * H * n_tok * (D // G) * 8)                  # value scales + zeros
+                  + B * H * n_tok * (D // G) * 8                   # value scales + zeros
+                  + 2 * B * H * st.res_len * D * 2 * kk.element_size())   # leftover tokens
         out[name] = {"us": round(us, 1), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
                      "mtokens_s": round(B * n_tok / us, 1), "chunks": st.n_chunks,
                      "bytes": nbytes}

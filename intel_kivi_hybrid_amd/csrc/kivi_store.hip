@@ -447,14 +447,15 @@ __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
                         scv[4 * h] = ps.x; scv[4 * h + 1] = ps.y; scv[4 * h + 2] = ps.z; scv[4 * h + 3] = ps.w;
                         rcv[4 * h] = pr.x; rcv[4 * h + 1] = pr.y; rcv[4 * h + 2] = pr.z; rcv[4 * h + 3] = pr.w;
                     }
-                    bool bad = false;
+                    // An element near a rounding tie is resolved on its own,
+                    // so a wave pays the slow path only for the element
+                    // positions where some lane needs it.
                     uint32_t q[8];
 #pragma unroll
-                    for (int jj = 0; jj < 8; ++jj) q[jj] = code_fast(x[jj], mnv[jj], rcv[jj], bad);
-                    if (__builtin_expect(bad, 0)) {
-#pragma unroll
-                        for (int jj = 0; jj < 8; ++jj)
-                            q[jj] = code_slow(x[jj], mnv[jj], scv[jj], rcv[jj]);
+                    for (int jj = 0; jj < 8; ++jj) {
+                        bool bad = false;
+                        q[jj] = code_fast(x[jj], mnv[jj], rcv[jj], bad);
+                        if (__builtin_expect(bad, 0)) q[jj] = code_slow(x[jj], mnv[jj], scv[jj], rcv[jj]);
                     }
 #pragma unroll
                     for (int jj = 0; jj < 8; ++jj) {
@@ -514,14 +515,12 @@ __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
                         x[jj] = tile[vat(t0 + jj, c)];
                         par[jj] = vpar[(t0 + jj) * NG + c / GV];
                     }
-                    bool bad = false;
                     uint32_t q[8];
 #pragma unroll
-                    for (int jj = 0; jj < 8; ++jj)
+                    for (int jj = 0; jj < 8; ++jj) {
+                        bool bad = false;
                         q[jj] = code_fast(x[jj], par[jj].x, par[jj].z, bad);
-                    if (__builtin_expect(bad, 0)) {
-#pragma unroll
-                        for (int jj = 0; jj < 8; ++jj)
+                        if (__builtin_expect(bad, 0))
                             q[jj] = code_slow(x[jj], par[jj].x, par[jj].y, par[jj].z);
                     }
 #pragma unroll
