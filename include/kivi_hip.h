@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define KIVI_HIP_ABI_VERSION 3
+#define KIVI_HIP_ABI_VERSION 4
 
 #define KIVI_OK 0
 #define KIVI_ERR_INVALID_ARGUMENT 1
@@ -235,6 +235,36 @@ int kivi_packed_decode_attention_noalloc(
     int32_t kv_heads, int32_t head_dim, int32_t group_size_k, int32_t group_size_v,
     int32_t chunk_capacity, int32_t num_chunks, int32_t res_capacity, int32_t res_start,
     int32_t res_len, float softmax_scale, int32_t num_splits, void* stream);
+
+/* Attention of q_len query tokens per sequence over the packed store and the
+ * residual window: q and out are [batch][q_len][q_heads][head_dim] f32; all
+ * other arguments as for kivi_packed_decode_attention (q_len = 1 is that
+ * call, and one token always sees the whole context).  causal != 0 with
+ * q_len > 1: the query tokens are the window's last q_len tokens (res_len >=
+ * q_len) and token i sees every quantised token and the window up to itself
+ * -- a forward of q_len tokens on a non-empty cache (chunked prefill,
+ * speculative verification), HF's causal mask over [cache ; new tokens].
+ * causal == 0: every token sees the whole context (the reference's own
+ * q_len = 3 attention check, tests/integration/test_attention_fix.py:19-43).
+ * When q_len * (q_heads / kv_heads) exceeds 8 the tokens are split over
+ * several launches, each streaming the store once.  No reference counterpart
+ * beyond that math (the reference runs HF attention on the CPU,
+ * src/kivi_sycl/cache/manager.py:251-290). */
+size_t kivi_packed_attention_workspace_size(int32_t batch, int32_t q_len, int32_t q_heads,
+                                            int32_t kv_heads, int32_t head_dim,
+                                            int32_t group_size_k, int32_t group_size_v,
+                                            int32_t num_chunks, int32_t res_len,
+                                            int32_t num_splits);
+
+int kivi_packed_attention(const float* q, int32_t q_len, int32_t causal, const uint8_t* k_codes,
+                          const float* k_scale, const float* k_zero, const uint8_t* v_codes,
+                          const float* v_scale, const float* v_zero, const void* k_res,
+                          const void* v_res, int32_t res_dtype, float* out, void* workspace,
+                          size_t workspace_bytes, int32_t batch, int32_t q_heads,
+                          int32_t kv_heads, int32_t head_dim, int32_t group_size_k,
+                          int32_t group_size_v, int32_t chunk_capacity, int32_t num_chunks,
+                          int32_t res_capacity, int32_t res_start, int32_t res_len,
+                          float softmax_scale, int32_t num_splits, void* stream);
 
 /* kivi_packed_decode_attention with this step's new token appended in the
  * same launch: the window (res_start, res_len) already counts the new token

@@ -464,3 +464,52 @@ def packed_decode_attention(q, store, softmax_scale=None, out=None, num_splits=0
             store.res_start, store.res_len, scale, int(num_splits),
             ctypes.c_void_p(_stream_of(q.device))), "packed_decode_attention")
     return out
+
+
+def packed_attention(q, store, causal=True, softmax_scale=None, out=None, num_splits=0,
+                     workspace=None):
+    """Attention of ``L`` query tokens per sequence over a
+    :class:`PackedKVStore`, ``q [B, Hq, L, D]`` fp32 (the layout HF attention
+    functions receive); returns ``[B, L, Hq, D]`` fp32 (the layout they
+    return).  ``causal``: the L queries are the residual window's last L
+    tokens and token i attends to the cache up to itself (a multi-token
+    forward on a non-empty cache); otherwise every query sees the whole
+    context.  Launched on the current stream."""
+    _check(q.dtype == torch.float32, "q must be float32, got ", _dtype_name(q.dtype))
+    _check(q.dim() == 4 and q.shape[0] == store.B and q.shape[3] == store.D,
+           "q must be [B, Hq, L, D] matching the store, got ", tuple(q.shape))
+    _check(q.device == store.device, "q must be on the store's device")
+    B, Hq, L, D = q.shape
+    store._commit()
+    if causal:
+        _check(L <= store.res_len, "causal attention of ", L, " query tokens needs them in "
+               "the residual window (", store.res_len, " tokens)")
+    qk = q.transpose(1, 2).contiguous()                                  # [B, L, Hq, D]
+    if out is None:
+        out = torch.empty(B, L, Hq, D, dtype=torch.float32, device=q.device)
+    else:
+        _check_tensor(out, "out", torch.float32)
+        _check(out.numel() == B * L * Hq * D, "out must hold B*L*Hq*D elements")
+    scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
+    need = int(_lib.kivi_packed_attention_workspace_size(
+        B, L, Hq, store.H, D, store.G, store.Gv, store.n_chunks, store.res_len, num_splits))
+    if workspace is None:
+        workspace = _workspace(q.device, need)
+    elif need:
+        _check(workspace.is_contiguous() and workspace.numel() * workspace.element_size() >= need,
+               "workspace must be contiguous and hold ", need, " bytes")
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    with torch.cuda.device(q.device):
+        _native.check(_lib.kivi_packed_attention(
+            ctypes.c_void_p(qk.data_ptr()), L, 1 if causal else 0,
+            ctypes.c_void_p(store.k_codes.data_ptr()),
+            ctypes.c_void_p(store.k_scale.data_ptr()), ctypes.c_void_p(store.k_zero.data_ptr()),
+            ctypes.c_void_p(store.v_codes.data_ptr()), ctypes.c_void_p(store.v_scale.data_ptr()),
+            ctypes.c_void_p(store.v_zero.data_ptr()), ctypes.c_void_p(store.k_res.data_ptr()),
+            ctypes.c_void_p(store.v_res.data_ptr()), store.res_dtype_code,
+            ctypes.c_void_p(out.data_ptr()),
+            ctypes.c_void_p(workspace.data_ptr() if workspace is not None else 0), ws_bytes,
+            B, Hq, store.H, D, store.G, store.Gv, store.capacity, store.n_chunks, store.R,
+            store.res_start, store.res_len, scale, int(num_splits),
+            ctypes.c_void_p(_stream_of(q.device))), "packed_attention")
+    return out

@@ -54,6 +54,11 @@ SIGNATURES = {
     "kivi_packed_decode_attention": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp,
                                      _vp, ctypes.c_size_t, _i32, _i32, _i32, _i32, _i32,
                                      _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp],
+    "kivi_packed_attention_workspace_size": [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                             _i32, _i32],
+    "kivi_packed_attention": [_vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp,
+                              _vp, ctypes.c_size_t, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                              _i32, _i32, _i32, _i32, _f32, _i32, _vp],
     "kivi_packed_decode_attention_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
                                              _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                              _i32, _i32, _i32, _i32, _f32, _i32, _vp],
@@ -63,6 +68,7 @@ _RESTYPES = {
     "kivi_last_error": ctypes.c_char_p,
     "kivi_clear_error": None,
     "kivi_packed_decode_attention_workspace_size": ctypes.c_size_t,
+    "kivi_packed_attention_workspace_size": ctypes.c_size_t,
 }
 
 _lib = None

@@ -53,6 +53,7 @@ struct AttnArgs {
     int n_units, n_splits, units_per_split;
     float qscale;      // softmax scale * log2(e)
     int res_dt;        // 0 fp32, 1 bf16, 2 fp16
+    QueryRows qr;      // HG query rows per kv head (kivi_attention.hpp)
 };
 
 __device__ __forceinline__ void wave_sync() {
@@ -92,7 +93,7 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
 
     for (int e = threadIdx.x; e < HG * D; e += kAttnBlock) {
         const int h = e / D, d = e % D;
-        sq[e] = a.q[((int64_t)b * a.Hq + kvh * HG + h) * D + d] * a.qscale;
+        sq[e] = a.qr.real(h) ? a.q[a.qr.row(b, kvh, h, a.Hq, D) + d] * a.qscale : 0.f;
     }
     __syncthreads();
 
@@ -184,16 +185,20 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
                     }
                 }
             }
+            // row h sees the window's first qr.visible(h) tokens
 #pragma unroll
-            for (int h = 0; h < HG; ++h) s[h] = valid ? acc[h] : -INFINITY;
+            for (int h = 0; h < HG; ++h)
+                s[h] = valid && t < a.qr.visible(h, a.res_len) ? acc[h] : -INFINITY;
         }
 
         // Online softmax (log2 domain).
 #pragma unroll
         for (int h = 0; h < HG; ++h) {
             const float mnew = fmaxf(m[h], wave_max(s[h]));
-            const float alpha = exp2f(m[h] - mnew);
-            const float p = valid ? exp2f(s[h] - mnew) : 0.f;
+            // a row may see no token of a residual unit (then m and mnew
+            // can both be -inf): no weight, no rescale
+            const float alpha = m[h] == -INFINITY ? 0.f : exp2f(m[h] - mnew);
+            const float p = s[h] == -INFINITY ? 0.f : exp2f(s[h] - mnew);
             l[h] = l[h] * alpha + wave_sum(p);
             m[h] = mnew;
 #pragma unroll
@@ -264,7 +269,7 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
         }
     }
     __syncthreads();
-    const int64_t hq0 = (int64_t)b * a.Hq + kvh * HG;
+    const int64_t prow0 = ((int64_t)b * a.Hkv + kvh) * HG;      // partial rows
     for (int e = threadIdx.x; e < HG * D; e += kAttnBlock) {
         const int h = e / D, d = e % D;
         float M = -INFINITY;
@@ -278,10 +283,11 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
             acc = fmaf(f, reg[h * D + d], acc);
             L = fmaf(f, reg[HG * D + HG + h], L);
         }
+        if (!a.qr.real(h)) continue;     // a padding row
         if (a.n_splits == 1) {
-            a.out[(hq0 + h) * D + d] = acc / L;
+            a.out[a.qr.row(b, kvh, h, a.Hq, D) + d] = acc / L;
         } else {
-            const int64_t row = (hq0 + h) * a.n_splits + split;
+            const int64_t row = (prow0 + h) * a.n_splits + split;
             a.part_o[row * D + d] = acc;
             if (d == 0) {
                 a.part_ml[row * 2] = M;
@@ -291,8 +297,9 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
     }
 }
 
-// Merge split partials: grid (Hq, B), one thread per channel, dynamic LDS of
-// 2*S floats.  The S (m, l) pairs are read in parallel (one per thread) and
+// Merge split partials: grid (Hkv * HG, B), one block per partial row
+// (b, kv head, query row v), one thread per channel, dynamic LDS of 2*S
+// floats.  The S (m, l) pairs are read in parallel (one per thread) and
 // turned into weights f_s = 2^(m_s - M) in LDS; each thread then sums its
 // channel over the S partial rows with every load in flight at once (the
 // loop is unrolled), so the kernel costs about two memory round trips
@@ -300,11 +307,14 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
 // a plain sequential merge would.
 __global__ __launch_bounds__(kMaxD) void attn_merge_kernel(const float* __restrict__ part_o,
                                                            const float* __restrict__ part_ml,
-                                                           float* __restrict__ out, int Hq,
-                                                           int D, int S) {
+                                                           float* __restrict__ out, QueryRows qr,
+                                                           int Hq, int HG, int D, int S) {
     extern __shared__ float wl[];                 // [S] weights, then [S] l
     __shared__ float red[kMaxD / kWave];
-    const int64_t row = (int64_t)blockIdx.y * Hq + blockIdx.x;
+    const int kvh = blockIdx.x / HG, v = blockIdx.x % HG;
+    if (!qr.real(v)) return;                      // a padding row
+    const int64_t row = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+    float* const orow = out + qr.row(blockIdx.y, kvh, v, Hq, D);
     const float* ml = part_ml + row * S * 2;
     const int tid = threadIdx.x, nt = blockDim.x;
     float mloc = -INFINITY;
@@ -342,7 +352,7 @@ __global__ __launch_bounds__(kMaxD) void attn_merge_kernel(const float* __restri
             acc = fmaf(wl[s], po[(int64_t)s * D], acc);
             L = fmaf(wl[s], wl[S + s], L);
         }
-        out[row * D + d] = acc / L;
+        orow[d] = acc / L;
     }
 }
 
@@ -410,6 +420,16 @@ Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
 // workgroup covers a row.
 bool needs_workspace(const Plan& p) { return p.n_splits > 1; }
 
+// LDS per workgroup the current device allows (160 KB on gfx950).
+int max_lds_bytes() {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) ==
+            hipSuccess && v > 0)
+        return v;
+    return 160 * 1024;
+}
+
 // Head and group geometry every decode launch needs, whatever its context.
 int check_geometry(int q_heads, int kv_heads, int head_dim, int group_size_k,
                    int group_size_v) {
@@ -443,7 +463,7 @@ int launch_attention_mfma(const AttnLaunch& a, hipStream_t st) {
                          "splits %d, chunks per wave %d)", a.n_chunks, a.n_qsplits,
                          a.chunks_per_wave);
     const bool r16 = a.res_dt != kSrcF32;
-    switch (a.Hq / a.Hkv) {
+    switch (a.qr.rows) {
         case 1: return r16 ? launch_attention_mfma_hg1_r16(a, st) : launch_attention_mfma_hg1(a, st);
         case 2: return r16 ? launch_attention_mfma_hg2_r16(a, st) : launch_attention_mfma_hg2(a, st);
         case 4: return r16 ? launch_attention_mfma_hg4_r16(a, st) : launch_attention_mfma_hg4(a, st);
@@ -506,13 +526,7 @@ int kivi_packed_decode_attention_supported(int32_t q_heads, int32_t kv_heads,
     }
     const int lds = attention_mfma_lds_bytes(q_heads / kv_heads, head_dim, group_size_k,
                                              head_dim / group_size_v);
-    int dev = 0, limit = 160 * 1024;
-    if (hipGetDevice(&dev) == hipSuccess) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) ==
-                hipSuccess && v > 0)
-            limit = v;
-    }
+    const int limit = max_lds_bytes();
     if (lds < 0 || lds > limit)
         return set_error(kErrUnsupported,
                          "decode attention with q_heads/kv_heads=%d, head_dim=%d, G=%d, "
@@ -522,31 +536,55 @@ int kivi_packed_decode_attention_supported(int32_t q_heads, int32_t kv_heads,
     return kOk;
 }
 
-size_t kivi_packed_decode_attention_workspace_size(int32_t batch, int32_t q_heads,
-                                                   int32_t kv_heads, int32_t head_dim,
-                                                   int32_t group_size_k, int32_t group_size_v,
-                                                   int32_t num_chunks, int32_t res_len,
-                                                   int32_t num_splits) {
-    if (batch <= 0 || kv_heads <= 0 || q_heads <= 0 || head_dim <= 0 || group_size_k <= 0 ||
-        group_size_v <= 0)
-        return 0;
-    Plan p = make_plan(batch, kv_heads, head_dim, group_size_k, group_size_v, num_chunks,
-                       res_len, num_splits);
-    if (!needs_workspace(p)) return 0;
-    return (size_t)batch * q_heads * p.n_splits * (head_dim + 2) * sizeof(float);
+}  // extern "C"
+
+namespace {
+
+// Rows per kv head of one launch: qlen * hg rounded up to a power of two.
+int rows_for(int n) { return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : 8; }
+
+// Query tokens per launch: as many as fill at most 8 rows per kv head (the
+// kernels' widest instance) and, on the matrix-core kernel, fit its LDS.
+int tokens_per_launch(int hg, int q_len, bool mfma, int D, int G, int Gv) {
+    int t = max(1, min(8 / hg, q_len));
+    if (mfma) {
+        static const int limit = max_lds_bytes();
+        while (t > 1 && attention_mfma_lds_bytes(rows_for(t * hg), D, G, D / Gv) > limit) t /= 2;
+    }
+    return t;
 }
 
-static int decode_attention_impl(const float* q, const uint8_t* k_codes, const float* k_scale,
-                                 const float* k_zero, const uint8_t* v_codes,
-                                 const float* v_scale, const float* v_zero, const void* k_res,
-                                 const void* v_res, int32_t res_dtype, float* out, void* workspace,
-                                 size_t workspace_bytes, int32_t batch, int32_t q_heads,
-                                 int32_t kv_heads, int32_t head_dim, int32_t group_size_k,
-                                 int32_t group_size_v, int32_t chunk_capacity,
-                                 int32_t num_chunks, int32_t res_capacity, int32_t res_start,
-                                 int32_t res_len, float softmax_scale, int32_t num_splits,
-                                 const void* k_new, const void* v_new, int64_t new_sb,
-                                 int64_t new_sh, void* stream) {
+size_t workspace_for(int batch, int q_len, int q_heads, int kv_heads, int head_dim,
+                     int group_size_k, int group_size_v, int num_chunks, int res_len,
+                     int num_splits) {
+    if (batch <= 0 || kv_heads <= 0 || q_heads <= 0 || head_dim <= 0 || group_size_k <= 0 ||
+        group_size_v <= 0 || q_len <= 0 || q_heads % kv_heads)
+        return 0;
+    const Plan p = make_plan(batch, kv_heads, head_dim, group_size_k, group_size_v, num_chunks,
+                             res_len, num_splits);
+    if (!needs_workspace(p)) return 0;
+    const int hg = q_heads / kv_heads;
+    const int rows = rows_for(
+        tokens_per_launch(hg, q_len, p.mfma, head_dim, group_size_k, group_size_v) * hg);
+    return (size_t)batch * kv_heads * rows * p.n_splits * (head_dim + 2) * sizeof(float);
+}
+
+// Attention of q_len query tokens per sequence (q [batch][q_len][q_heads]
+// [head_dim], out likewise) over [packed history ; residual window]; causal:
+// the queries are the window's last q_len tokens and token i sees the window
+// up to itself, else every token sees the whole context.  Tokens are split
+// across launches when q_len * (q_heads / kv_heads) exceeds 8 rows; each
+// launch streams the store once.
+int attention_impl(const float* q, int32_t q_len, int32_t causal, const uint8_t* k_codes,
+                   const float* k_scale, const float* k_zero, const uint8_t* v_codes,
+                   const float* v_scale, const float* v_zero, const void* k_res,
+                   const void* v_res, int32_t res_dtype, float* out, void* workspace,
+                   size_t workspace_bytes, int32_t batch, int32_t q_heads, int32_t kv_heads,
+                   int32_t head_dim, int32_t group_size_k, int32_t group_size_v,
+                   int32_t chunk_capacity, int32_t num_chunks, int32_t res_capacity,
+                   int32_t res_start, int32_t res_len, float softmax_scale, int32_t num_splits,
+                   const void* k_new, const void* v_new, int64_t new_sb, int64_t new_sh,
+                   void* stream) {
     if (!q || !out)
         return set_error(kErrInvalidArgument, "null q/out pointer");
     if (batch <= 0)
@@ -557,6 +595,16 @@ static int decode_attention_impl(const float* q, const uint8_t* k_codes, const f
     if (num_chunks < 0 || res_len < 0 || num_chunks + res_len == 0)
         return set_error(kErrInvalidArgument, "empty context (num_chunks=%d, res_len=%d)",
                          num_chunks, res_len);
+    if (q_len < 1)
+        return set_error(kErrInvalidArgument, "q_len %d must be positive", q_len);
+    // One query token sees the whole context either way (a decode step whose
+    // token was just flushed has res_len 0).
+    if (causal && q_len > 1 && q_len > res_len)
+        return set_error(kErrInvalidArgument,
+                         "causal attention of %d query tokens needs them in the residual "
+                         "window (res_len %d)", q_len, res_len);
+    if (k_new && q_len != 1)
+        return set_error(kErrInvalidArgument, "the fused append takes one query token");
     const int layout = code_layout_for(head_dim, group_size_k, group_size_v);
     if (num_chunks > 0) {
         if (!k_codes || !k_scale || !k_zero || !v_codes || !v_scale || !v_zero)
@@ -581,56 +629,115 @@ static int decode_attention_impl(const float* q, const uint8_t* k_codes, const f
                              "residual window (start %d, len %d) outside capacity %d",
                              res_start, res_len, res_capacity);
     }
-    Plan p = make_plan(batch, kv_heads, head_dim, group_size_k, group_size_v, num_chunks,
-                       res_len, num_splits);
+    const Plan p = make_plan(batch, kv_heads, head_dim, group_size_k, group_size_v, num_chunks,
+                             res_len, num_splits);
+    const int tpl = tokens_per_launch(hg, q_len, p.mfma, head_dim, group_size_k, group_size_v);
+    const int rows = rows_for(tpl * hg);
     float* part_o = nullptr;
     float* part_ml = nullptr;
     if (needs_workspace(p)) {
-        const size_t need = (size_t)batch * q_heads * p.n_splits * (head_dim + 2) * sizeof(float);
+        const size_t need = workspace_for(batch, q_len, q_heads, kv_heads, head_dim,
+                                          group_size_k, group_size_v, num_chunks, res_len,
+                                          num_splits);
         if (workspace == nullptr || workspace_bytes < need)
             return set_error(kErrInvalidArgument, "workspace of %zu bytes needed, got %zu",
                              need, workspace_bytes);
         part_o = (float*)workspace;
-        part_ml = part_o + (size_t)batch * q_heads * p.n_splits * head_dim;
+        part_ml = part_o + (size_t)batch * kv_heads * rows * p.n_splits * head_dim;
     }
     hipStream_t st = (hipStream_t)stream;
     const int new_slot = k_new ? (res_start + res_len - 1) % res_capacity : 0;
     if (k_new && !p.mfma) {
         // the generic kernel reads the ring only: file the token there first
         rc = kivi_store_append(k_new, v_new, res_dtype, new_sb, new_sh, 0, 1,
-                                         const_cast<void*>(k_res), const_cast<void*>(v_res),
-                                         res_dtype, batch, kv_heads, head_dim, res_capacity,
-                                         new_slot, stream);
+                               const_cast<void*>(k_res), const_cast<void*>(v_res), res_dtype,
+                               batch, kv_heads, head_dim, res_capacity, new_slot, stream);
         if (rc) return rc;
     }
-    if (p.mfma) {
-        AttnLaunch L{q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res, v_res, out,
-                     part_o, part_ml, batch, q_heads, kv_heads, head_dim, group_size_k,
-                     group_size_v, chunk_capacity, num_chunks, res_capacity, res_start, res_len,
-                     p.n_qsplits, p.chunks_per_wave, p.res_waves, p.early_per_pass_x2, p.n_splits,
-                     softmax_scale * kLog2e, k_new, v_new, new_sb, new_sh, new_slot, res_dtype};
-        rc = launch_attention_mfma(L, st);
-        if (rc || !needs_workspace(p)) return rc;
-    } else {
-        AttnArgs a{q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res, v_res, out,
-                   part_o, part_ml, q_heads, kv_heads, head_dim, group_size_k, group_size_v,
-                   chunk_capacity, num_chunks, res_capacity, res_start, res_len, p.n_units,
-                   p.n_splits, p.units_per_split, softmax_scale * kLog2e, res_dtype};
-        const dim3 grid(p.n_splits, kv_heads, batch);
-        const size_t lds = (size_t)(hg * head_dim + kAttnWaves * (hg * head_dim + hg * kWave)) *
-                           sizeof(float);
-        switch (hg) {
-            case 1: attn_generic_kernel<1><<<grid, kAttnBlock, lds, st>>>(a); break;
-            case 2: attn_generic_kernel<2><<<grid, kAttnBlock, lds, st>>>(a); break;
-            case 4: attn_generic_kernel<4><<<grid, kAttnBlock, lds, st>>>(a); break;
-            case 8: attn_generic_kernel<8><<<grid, kAttnBlock, lds, st>>>(a); break;
+    const int64_t tok_stride = (int64_t)q_heads * head_dim;      // one query token
+    for (int i0 = 0; i0 < q_len; i0 += tpl) {
+        QueryRows qr;
+        qr.qlen = min(tpl, q_len - i0);
+        qr.hg = hg;
+        qr.hg_log2 = hg == 1 ? 0 : hg == 2 ? 1 : hg == 4 ? 2 : 3;
+        qr.q_bstride = (int64_t)q_len * tok_stride;
+        qr.vis0 = causal ? res_len - (q_len - 1 - i0) : res_len;
+        qr.rows = rows;
+        const float* qi = q + i0 * tok_stride;
+        float* oi = out + i0 * tok_stride;
+        if (p.mfma) {
+            AttnLaunch L{qi, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res, v_res,
+                         oi, part_o, part_ml, batch, q_heads, kv_heads, head_dim, group_size_k,
+                         group_size_v, chunk_capacity, num_chunks, res_capacity, res_start,
+                         res_len, p.n_qsplits, p.chunks_per_wave, p.res_waves,
+                         p.early_per_pass_x2, p.n_splits, softmax_scale * kLog2e, k_new, v_new,
+                         new_sb, new_sh, new_slot, res_dtype, qr};
+            rc = launch_attention_mfma(L, st);
+        } else {
+            AttnArgs a{qi, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res, v_res, oi,
+                       part_o, part_ml, q_heads, kv_heads, head_dim, group_size_k, group_size_v,
+                       chunk_capacity, num_chunks, res_capacity, res_start, res_len, p.n_units,
+                       p.n_splits, p.units_per_split, softmax_scale * kLog2e, res_dtype, qr};
+            const dim3 grid(p.n_splits, kv_heads, batch);
+            const size_t lds = (size_t)(rows * head_dim +
+                                        kAttnWaves * (rows * head_dim + rows * kWave)) *
+                               sizeof(float);
+            switch (rows) {
+                case 1: attn_generic_kernel<1><<<grid, kAttnBlock, lds, st>>>(a); break;
+                case 2: attn_generic_kernel<2><<<grid, kAttnBlock, lds, st>>>(a); break;
+                case 4: attn_generic_kernel<4><<<grid, kAttnBlock, lds, st>>>(a); break;
+                default: attn_generic_kernel<8><<<grid, kAttnBlock, lds, st>>>(a); break;
+            }
+            rc = check_launch("packed_attention");
         }
-        rc = check_launch("packed_decode_attention");
-        if (rc || !needs_workspace(p)) return rc;
+        if (rc) return rc;
+        if (needs_workspace(p)) {
+            attn_merge_kernel<<<dim3(kv_heads * rows, batch), head_dim,
+                                2 * p.n_splits * sizeof(float), st>>>(
+                part_o, part_ml, oi, qr, q_heads, rows, head_dim, p.n_splits);
+            rc = check_launch("packed_attention_merge");
+            if (rc) return rc;
+        }
     }
-    attn_merge_kernel<<<dim3(q_heads, batch), head_dim, 2 * p.n_splits * sizeof(float), st>>>(
-        part_o, part_ml, out, q_heads, head_dim, p.n_splits);
-    return check_launch("packed_decode_attention_merge");
+    return kOk;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t kivi_packed_decode_attention_workspace_size(int32_t batch, int32_t q_heads,
+                                                   int32_t kv_heads, int32_t head_dim,
+                                                   int32_t group_size_k, int32_t group_size_v,
+                                                   int32_t num_chunks, int32_t res_len,
+                                                   int32_t num_splits) {
+    return workspace_for(batch, 1, q_heads, kv_heads, head_dim, group_size_k, group_size_v,
+                         num_chunks, res_len, num_splits);
+}
+
+size_t kivi_packed_attention_workspace_size(int32_t batch, int32_t q_len, int32_t q_heads,
+                                            int32_t kv_heads, int32_t head_dim,
+                                            int32_t group_size_k, int32_t group_size_v,
+                                            int32_t num_chunks, int32_t res_len,
+                                            int32_t num_splits) {
+    return workspace_for(batch, q_len, q_heads, kv_heads, head_dim, group_size_k, group_size_v,
+                         num_chunks, res_len, num_splits);
+}
+
+int kivi_packed_attention(const float* q, int32_t q_len, int32_t causal, const uint8_t* k_codes,
+                          const float* k_scale, const float* k_zero, const uint8_t* v_codes,
+                          const float* v_scale, const float* v_zero, const void* k_res,
+                          const void* v_res, int32_t res_dtype, float* out, void* workspace,
+                          size_t workspace_bytes, int32_t batch, int32_t q_heads,
+                          int32_t kv_heads, int32_t head_dim, int32_t group_size_k,
+                          int32_t group_size_v, int32_t chunk_capacity, int32_t num_chunks,
+                          int32_t res_capacity, int32_t res_start, int32_t res_len,
+                          float softmax_scale, int32_t num_splits, void* stream) {
+    return attention_impl(q, q_len, causal, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero,
+                          k_res, v_res, res_dtype, out, workspace, workspace_bytes, batch,
+                          q_heads, kv_heads, head_dim, group_size_k, group_size_v,
+                          chunk_capacity, num_chunks, res_capacity, res_start, res_len,
+                          softmax_scale, num_splits, nullptr, nullptr, 0, 0, stream);
 }
 
 int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const float* k_scale,
@@ -643,7 +750,7 @@ int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const f
                                  int32_t num_chunks, int32_t res_capacity, int32_t res_start,
                                  int32_t res_len, float softmax_scale, int32_t num_splits,
                                  void* stream) {
-    return decode_attention_impl(q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
+    return attention_impl(q, 1, 1, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
                                  v_res, res_dtype, out, workspace, workspace_bytes, batch, q_heads,
                                  kv_heads, head_dim, group_size_k, group_size_v, chunk_capacity,
                                  num_chunks, res_capacity, res_start, res_len, softmax_scale,
@@ -671,7 +778,7 @@ int kivi_packed_decode_attention_noalloc(
     void* ws = nullptr;
     const int rc = scratch_for_current_device(&ws);
     if (rc) return rc;
-    return decode_attention_impl(q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
+    return attention_impl(q, 1, 1, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
                                  v_res, res_dtype, out, ws, KIVI_NOALLOC_SCRATCH_BYTES, batch,
                                  q_heads, kv_heads, head_dim, group_size_k, group_size_v,
                                  chunk_capacity, num_chunks, res_capacity, res_start, res_len,
@@ -705,7 +812,7 @@ int kivi_packed_decode_attention_append(
         return set_error(kErrInvalidArgument,
                          "new-token rows must be %d-byte aligned (strides multiples of 4)",
                          (int)vb);
-    return decode_attention_impl(q, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
+    return attention_impl(q, 1, 1, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
                                  v_res, res_dtype, out, workspace, workspace_bytes, batch, q_heads,
                                  kv_heads, head_dim, group_size_k, group_size_v, chunk_capacity,
                                  num_chunks, res_capacity, res_start, res_len, softmax_scale,

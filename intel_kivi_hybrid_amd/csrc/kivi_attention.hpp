@@ -7,8 +7,33 @@
 
 namespace kivi {
 
+// Query rows of one launch.  The HG rows a workgroup computes for kv head
+// kvh ("virtual heads" v) are query token i = v / hg and head kvh*hg + v % hg
+// (hg = Hq / Hkv): a launch covers qlen query tokens, so v < qlen*hg are real
+// rows and the rest padding (zero queries, never stored).  Row v of batch b
+// sits at q + b*q_bstride + (i*Hq + kvh*hg + h)*D, and its output likewise in
+// out.  Query token i sees every quantised chunk and the first
+// min(res_len, vis0 + i) tokens of the residual window (causal attention of
+// the window's newest tokens; vis0 = res_len when every token sees all).
+struct QueryRows {
+    int qlen = 1, hg = 1;
+    int hg_log2 = 0;         // hg is a power of two (1, 2, 4 or 8)
+    int64_t q_bstride = 0;
+    int vis0 = 0;
+    int rows = 1;            // HG: qlen*hg rounded up to a power of two (<= 8)
+    __host__ __device__ int64_t row(int b, int kvh, int v, int Hq, int D) const {
+        const int i = v >> hg_log2, h = v & (hg - 1);
+        return (int64_t)b * q_bstride + ((int64_t)i * Hq + (int64_t)kvh * hg + h) * D;
+    }
+    __host__ __device__ bool real(int v) const { return v < qlen * hg; }
+    __host__ __device__ int visible(int v, int res_len) const {
+        const int n = vis0 + (v >> hg_log2);
+        return n < res_len ? n : res_len;
+    }
+};
+
 struct AttnLaunch {
-    const float* q;          // [B, Hq, D]
+    const float* q;          // query rows (QueryRows)
     const uint8_t* k_codes;  // [B, Hkv, Cmax, G*D/4]
     const float* k_scale;    // [B, Hkv, Cmax, D]
     const float* k_zero;
@@ -17,9 +42,9 @@ struct AttnLaunch {
     const float* v_zero;
     const void* k_res;       // [B, Hkv, Rcap, D] ring of element type res_dt
     const void* v_res;
-    float* out;              // [B, Hq, D]
-    float* part_o;           // [B, Hq, n_splits, D] (n_splits > 1 only)
-    float* part_ml;          // [B, Hq, n_splits, 2]
+    float* out;              // output rows (QueryRows)
+    float* part_o;           // [B, Hkv, HG, n_splits, D] (n_splits > 1 only)
+    float* part_ml;          // [B, Hkv, HG, n_splits, 2]
     int B, Hq, Hkv, D, G, Gv, Cmax, n_chunks, Rcap, res_start, res_len;
     int n_qsplits;           // workgroups per (b, kv-head)
     int chunks_per_wave;     // packed chunks per wave
@@ -36,6 +61,7 @@ struct AttnLaunch {
     int64_t new_sb = 0, new_sh = 0;
     int new_slot = 0;
     int res_dt = 0;          // ring element type: 0 fp32, 1 bf16, 2 fp16
+    QueryRows qr;
 };
 
 // Launches the matrix-core kernel (kLayoutMfma stores, Hq/Hkv in {1,2,4,8}).

@@ -317,7 +317,7 @@ template <int HG, int D>
 __device__ void merge_and_store(unsigned char* smem, const float* rstate, const AttnLaunch& a,
                                 int split, int kvh, int b) {
     __syncthreads();
-    const int64_t hq0 = (int64_t)b * a.Hq + kvh * HG;
+    const int64_t prow0 = ((int64_t)b * a.Hkv + kvh) * HG;     // partial rows
     for (int e = threadIdx.x; e < HG * D; e += kBlock) {
         const int h = e / D, d = e % D;
         float M = -INFINITY;
@@ -333,11 +333,12 @@ __device__ void merge_and_store(unsigned char* smem, const float* rstate, const 
             acc = fmaf(f, s[h * D + d], acc);
             L = fmaf(f, s[HG * D + HG + h], L);
         }
+        if (!a.qr.real(h)) continue;    // a padding row
         if (a.n_splits == 1) {          // the only partial of its row: finish here
-            a.out[(hq0 + h) * D + d] = acc / L;
+            a.out[a.qr.row(b, kvh, h, a.Hq, D) + d] = acc / L;
             continue;
         }
-        const int64_t row = (hq0 + h) * a.n_splits + split;
+        const int64_t row = (prow0 + h) * a.n_splits + split;
         a.part_o[row * D + d] = acc;
         if (d == 0) {
             a.part_ml[row * 2] = M;
@@ -476,17 +477,27 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         kn = static_cast<const Quad*>(a.k_new)[new_row / 4 + lane];
         vn = static_cast<const Quad*>(a.v_new)[new_row / 4 + lane];
     }
+    // Query rows (QueryRows): padding rows read the last real row and are
+    // zeroed after the load, so no load sits in a branch.
     constexpr int QN = (HG * D + kBlock - 1) / kBlock;
-    const float* qg = a.q + ((int64_t)b * a.Hq + kvh * HG) * D;
+    const int n_real = a.qr.qlen * a.qr.hg;
     float qt[QN];
 #pragma unroll
-    for (int i = 0; i < QN; ++i) qt[i] = qg[min((int)threadIdx.x + i * kBlock, HG * D - 1)];
+    for (int i = 0; i < QN; ++i) {
+        const int e = min((int)threadIdx.x + i * kBlock, HG * D - 1);
+        const int v = e / D;
+        const float x = a.q[a.qr.row(b, kvh, min(v, n_real - 1), a.Hq, D) + e % D];
+        qt[i] = v < n_real ? x : 0.f;
+    }
     // W-prep lane: head wh, channels [wseg*CPL, +CPL).
     const bool wlane = lane < HG * S::LPH;
     const int wh = lane / S::LPH, wseg = lane % S::LPH;
+    const float* qw = a.q + a.qr.row(b, kvh, min(wh, n_real - 1), a.Hq, D) + wseg * S::CPL;
     float qv[S::CPL];
 #pragma unroll
-    for (int i = 0; i < S::CPL; ++i) qv[i] = wlane ? qg[wh * D + wseg * S::CPL + i] : 0.f;
+    for (int i = 0; i < S::CPL; ++i) qv[i] = wlane ? qw[i] : 0.f;
+#pragma unroll
+    for (int i = 0; i < S::CPL; ++i) qv[i] = wh < n_real ? qv[i] : 0.f;
     // Keeps the query loads ahead of the ring's: the query's LDS stores then
     // wait for the query alone.
     asm volatile("" ::: "memory");
@@ -869,14 +880,16 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                 }
                 acc += dpp<0xB1>(acc);        // quad_perm [1,0,3,2]
                 acc += dpp<0x4E>(acc);        // quad_perm [2,3,0,1]
-                sres[h] = tk < n ? acc : -INFINITY;
+                // row h sees the window's first qr.visible(h) tokens
+                sres[h] = tk < n && t0 + tk < a.qr.visible(h, a.res_len) ? acc : -INFINITY;
             }
 #pragma unroll
             for (int h = 0; h < HG; ++h) {
                 const float mnew = fmaxf(mr[h], wave_max(sres[h]));
                 const float alpha = mr[h] == -INFINITY ? 0.f : exp2_fast(mr[h] - mnew);
                 mr[h] = mnew;
-                const float p = tk < n ? exp2_fast(sres[h] - mnew) : 0.f;
+                const float p = tk < n && t0 + tk < a.qr.visible(h, a.res_len)
+                                    ? exp2_fast(sres[h] - mnew) : 0.f;
                 lr[h] = lr[h] * alpha + 0.25f * wave_sum(p);    // each token sits in 4 lanes
                 orr[h][0] *= alpha;
                 orr[h][1] *= alpha;

@@ -517,9 +517,17 @@ class PackedKVStore:
 
     def attention(self, q: torch.Tensor, softmax_scale: Optional[float] = None,
                   out: Optional[torch.Tensor] = None, num_splits: int = 0,
-                  workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """Fused decode attention of ``q [B, Hq, D]`` (or ``[B, Hq, 1, D]``)
-        over [packed history ; residual]; returns ``[B, Hq, D]`` fp32."""
+                  workspace: Optional[torch.Tensor] = None, causal: bool = True) -> torch.Tensor:
+        """Fused attention over [packed history ; residual].
+
+        ``q [B, Hq, D]`` (or ``[B, Hq, 1, D]``): one decode token per
+        sequence; returns ``[B, Hq, D]`` fp32.  ``q [B, Hq, L, D]`` with
+        L > 1: L query tokens per sequence (see ``_C.packed_attention``;
+        ``causal`` by default: they are the window's last L tokens); returns
+        ``[B, L, Hq, D]`` fp32."""
         from . import _C
+        if q.dim() == 4 and q.shape[2] > 1:
+            return _C.packed_attention(q, self, causal=causal, softmax_scale=softmax_scale,
+                                       out=out, num_splits=num_splits, workspace=workspace)
         return _C.packed_decode_attention(q, self, softmax_scale=softmax_scale, out=out,
                                           num_splits=num_splits, workspace=workspace)

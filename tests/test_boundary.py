@@ -44,7 +44,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_error_string():
     from intel_kivi_hybrid_amd import _native
     lib = _native.load()
-    assert lib.kivi_abi_version() == 3
+    assert lib.kivi_abi_version() == 4
     # invalid arguments are rejected on the host, before any launch
     rc = lib.kivi_quantize_keys_per_channel(None, None, None, None, 4, 32, None)
     assert rc == 1 and "null" in _native.last_error()
@@ -212,6 +212,13 @@ def test_store_entry_points_reject_bad_arguments():
                                           64, 32, 32, 1, 0, 32, 0, 1, ctypes.c_float(0.1), 0,
                                           None)
     assert rc == 1 and "res_dtype 4" in _native.last_error()
+    # several query tokens: causal ones must sit in the window, q_len >= 1
+    rc = lib.kivi_packed_attention(p, 3, 1, p, p, p, p, p, p, p, p, 0, p, None, 0, 1, 4, 4, 64,
+                                   32, 32, 1, 1, 32, 0, 2, ctypes.c_float(0.1), 0, None)
+    assert rc == 1 and "3 query tokens needs them in the residual" in _native.last_error()
+    rc = lib.kivi_packed_attention(p, 0, 0, p, p, p, p, p, p, p, p, 0, p, None, 0, 1, 4, 4, 64,
+                                   32, 32, 1, 1, 32, 0, 2, ctypes.c_float(0.1), 0, None)
+    assert rc == 1 and "q_len 0 must be positive" in _native.last_error()
 
 
 def test_noalloc_rejects_oversize_partials_on_host():
