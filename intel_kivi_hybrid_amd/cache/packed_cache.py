@@ -20,7 +20,14 @@ the 128 B the 2-bit store holds.  Here the cache plugs into the model's own
 * a prompt (more than one token on an empty layer) attends over its own
   unquantised K/V with PyTorch SDPA, exactly like the reference's prefill
   forward with a plain cache (generate.py:56-60), and is then quantised into
-  the store with the same flush rule.
+  the store with the same flush rule;
+* a forward of several tokens on a non-empty layer (chunked prefill, the
+  verification pass of assisted decoding) appends them all to the window and
+  runs the multi-token kernel, causal over [packed history ; window]: what
+  the reference's flow computes when the model is handed
+  get_full_cache() and a multi-token input.  Its flushes wait for the next
+  update, so crop() can still drop any of those tokens (assisted decoding
+  discards the rejected drafts that way).
 
 The served-cache path (:class:`KiviCache` with ``get_full_cache()``) stays the
 drop-in for the reference's control flow; this class is the fast path for
@@ -35,7 +42,7 @@ from typing import List, Optional
 import torch
 from transformers.cache_utils import Cache, CacheLayerMixin
 from transformers.integrations.sdpa_attention import sdpa_attention_forward
-from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
+from transformers.masking_utils import AttentionMaskInterface, causal_mask_function, sdpa_mask
 from transformers.modeling_utils import AttentionInterface
 
 from ..config.model_config import detect_model_config
@@ -182,9 +189,12 @@ class KiviPackedLayer(CacheLayerMixin):
             self._prompt = False
             self._awaiting_attention = True
         else:
-            raise NotImplementedError(
-                f"KiviPackedCache: a {n}-token forward pass on a non-empty cache (chunked "
-                f"prefill, assisted decoding) is not supported; decode one token per step")
+            # Every new token stays unquantised until the step has attended
+            # (room for R - 1 + n, so steps of this size never grow it again).
+            st.grow_residual(max(st.res_len + n, self.owner.R - 1 + n))
+            st.append(k, v)
+            self._prompt = False
+            self._awaiting_attention = True
         kt, vt = key_states.view_as(key_states), value_states.view_as(value_states)
         kt._kivi_layer = self
         vt._kivi_layer = self
@@ -192,18 +202,42 @@ class KiviPackedLayer(CacheLayerMixin):
 
     # --------------------------------------------------------- attention
     def attend(self, query: torch.Tensor, scaling: Optional[float]) -> torch.Tensor:
-        """Decode attention of ``query [B, Hq, 1, D]`` over this layer's store;
-        returns ``[B, 1, Hq, D]`` in the query's dtype and device."""
+        """Attention of ``query [B, Hq, L, D]`` (the step's L new tokens, the
+        window's newest) over this layer's store, causal among them; returns
+        ``[B, L, Hq, D]`` in the query's dtype and device.  A one-token step
+        does its flushes now; a longer one leaves them to the next update."""
         st = self.store
-        q = query[:, :, 0, :].to(st.device, torch.float32).contiguous()
-        o = st.attention(q, softmax_scale=scaling)
+        L = query.shape[2]
+        if L == 1:
+            q = query[:, :, 0, :].to(st.device, torch.float32).contiguous()
+            o = st.attention(q, softmax_scale=scaling).unsqueeze(1)
+        else:
+            q = query.to(st.device, torch.float32)
+            o = st.attention(q, softmax_scale=scaling, causal=True)
         self._awaiting_attention = False
-        self.settle()
-        return o.unsqueeze(1).to(query.device, query.dtype)
+        if L == 1:
+            self.settle()
+        return o.to(query.device, query.dtype)
 
-    # ------------------------------------------------ unsupported ops
+    # ------------------------------------------------------------ edits
     def crop(self, tokens_to_remove: int) -> None:
-        raise NotImplementedError("KiviPackedCache cannot drop tokens once they are stored")
+        """Drop the newest tokens (transformers' ``crop``: a negative count
+        removes that many; a positive one is the length to keep).  Only
+        tokens still in the residual window can go: a quantised chunk is
+        final (the window holds every token of the latest multi-token step,
+        and at least R - G of a prompt's last tokens)."""
+        if not self.is_initialized:
+            return
+        tokens_to_remove = int(tokens_to_remove)
+        n = self.get_seq_length()
+        if tokens_to_remove > 0:
+            if tokens_to_remove >= n:
+                return
+            drop = n - tokens_to_remove
+        else:
+            drop = -tokens_to_remove
+        if drop:
+            self.store.rollback(drop)
 
     def reorder_cache(self, beam_idx: torch.LongTensor) -> None:
         if self.get_seq_length() > 0:
@@ -320,8 +354,12 @@ class KiviPackedCache(Cache):
         windows ``k_residual``/``v_residual`` ``[B, Hkv, r, D]`` in the
         ring's type (fp32, or bf16/fp16 for a half-precision model);
         the file metadata holds the format tag, version, cache geometry and
-        per-layer flush counts."""
+        per-layer flush counts.  Flushes a multi-token step still owes are
+        done first (the file's windows hold fewer than R tokens)."""
         from safetensors.torch import save_file
+        for lay in self.layers:
+            if lay.is_initialized:
+                lay.settle()
         meta = {"format": FORMAT_NAME, "version": str(FORMAT_VERSION),
                 "num_layers": str(self.num_layers), "head_dim": str(self.head_dim),
                 "num_kv_heads": str(self.num_kv_heads or 0), "group_size": str(self.G),
@@ -403,19 +441,41 @@ def kivi_packed_attention_forward(module, query, key, value, attention_mask, sca
                              f"{key.shape[1]} kv heads cannot be decoded from the packed "
                              f"store: {err}")
         owner._heads_checked = True
-    if layer._prompt or query.shape[2] > 1:
+    if layer._prompt:
         return sdpa_attention_forward(module, query, key, value, attention_mask,
                                       dropout=dropout, scaling=scaling, **kwargs)
     if dropout:
         raise ValueError(f"'{KIVI_ATTENTION}' attention is inference-only (dropout={dropout})")
     if attention_mask is not None:
         raise NotImplementedError(
-            f"'{KIVI_ATTENTION}' decode attention takes no attention mask (padded batches are "
-            f"not supported); every sequence attends over its whole cache")
+            f"'{KIVI_ATTENTION}' attention over the cache takes no attention mask (padded "
+            f"batches are not supported): every sequence attends over its whole cache, its "
+            f"new tokens causally")
     for name in ("sliding_window", "softcap", "s_aux"):
         if kwargs.get(name) is not None:
             raise NotImplementedError(f"'{KIVI_ATTENTION}' attention does not support {name}")
     return layer.attend(query, scaling), None
+
+
+def kivi_causal_mask(batch_size: int, q_length: int, kv_length: int, q_offset: int = 0,
+                     kv_offset: int = 0, mask_function=causal_mask_function,
+                     attention_mask: Optional[torch.Tensor] = None,
+                     local_size: Optional[int] = None, allow_is_causal_skip: bool = True,
+                     **kwargs):
+    """Mask function of the ``"kivi_packed"`` attention: ``None`` when the
+    mask is the plain causal one over [cache ; new tokens] with no padding
+    (the new tokens are the newest kv positions), which the packed kernels
+    apply themselves at any cache length; anything else is SDPA's mask
+    (transformers.masking_utils.sdpa_mask), which prompt passes use and the
+    packed path refuses."""
+    if (allow_is_causal_skip and mask_function is causal_mask_function and local_size is None
+            and kv_offset == 0 and q_offset + q_length == kv_length
+            and (attention_mask is None or bool(attention_mask[:, -kv_length:].all()))):
+        return None
+    return sdpa_mask(batch_size=batch_size, q_length=q_length, kv_length=kv_length,
+                     q_offset=q_offset, kv_offset=kv_offset, mask_function=mask_function,
+                     attention_mask=attention_mask, local_size=local_size,
+                     allow_is_causal_skip=allow_is_causal_skip, **kwargs)
 
 
 _registered = False
@@ -423,11 +483,11 @@ _registered = False
 
 def register_packed_attention() -> None:
     """Register ``"kivi_packed"`` with transformers' attention and mask
-    interfaces (the mask is SDPA's, used by prompt passes)."""
+    interfaces."""
     global _registered
     if not _registered:
         AttentionInterface.register(KIVI_ATTENTION, kivi_packed_attention_forward)
-        AttentionMaskInterface.register(KIVI_ATTENTION, sdpa_mask)
+        AttentionMaskInterface.register(KIVI_ATTENTION, kivi_causal_mask)
         _registered = True
 
 

@@ -379,6 +379,25 @@ class PackedKVStore:
             self._pending = None          # the staged token is the newest
         self.res_len -= n
 
+    def grow_residual(self, capacity: int) -> None:
+        """Give the residual ring room for ``capacity`` tokens (nothing
+        happens if it has that already): a forward of several tokens holds
+        them all in the window until it has attended.  The window is copied
+        in token order into the new ring, which starts at slot 0."""
+        capacity = int(capacity)
+        if capacity <= self.R:
+            return
+        k, v = self.residual()
+        n = self.res_len
+        k_res = torch.zeros(self.B, self.H, capacity, self.D, dtype=self.k_res.dtype,
+                            device=self.device)
+        v_res = torch.zeros_like(k_res)
+        k_res[:, :, :n].copy_(k)
+        v_res[:, :, :n].copy_(v)
+        self.k_res, self.v_res = k_res, v_res
+        self.res_start = 0
+        self.R = capacity
+
     _TENSORS = ("k_res", "v_res", "k_codes", "k_scale", "k_zero", "v_codes", "v_scale",
                 "v_zero", "k_hist", "v_hist")
 

@@ -74,11 +74,28 @@ class CpuPackedStore:
                 flushes += 1
         return flushes
 
-    def attention(self, q, softmax_scale=None):
+    def attention(self, q, softmax_scale=None, causal=True):
+        if q.dim() == 4 and q.shape[2] > 1:
+            # [B, Hq, L, D] -> [B, L, Hq, D]: the window's newest L tokens
+            assert causal and q.shape[2] <= self.res_len
+            o = oracle_attention.prefix_attention(q.transpose(1, 2).numpy(), self.hist_k.numpy(),
+                                                  self.hist_v.numpy(), self.res_k.numpy(),
+                                                  self.res_v.numpy(), softmax_scale)
+            return torch.from_numpy(o).float()
         o = oracle_attention.decode_attention(q.numpy(), self.hist_k.numpy(),
                                               self.hist_v.numpy(), self.res_k.numpy(),
                                               self.res_v.numpy(), softmax_scale)
         return torch.from_numpy(o).float()
+
+    def grow_residual(self, capacity):
+        self.R = max(self.R, int(capacity))
+
+    def rollback(self, n):
+        if n < 0 or n > self.res_len:
+            raise ValueError(f"cannot roll back {n} tokens: the residual window holds "
+                             f"{self.res_len} (quantised tokens cannot be rolled back)")
+        m = self.res_len - n
+        self.res_k, self.res_v = self.res_k[:, :, :m], self.res_v[:, :, :m]
 
     def select_batch(self, index):
         for name in ("res_k", "res_v", "hist_k", "hist_v"):

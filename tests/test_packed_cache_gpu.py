@@ -186,3 +186,100 @@ def test_attention_output_matches_oracle(hip_device):
     assert w is None and out.shape == (B, 1, Hq, D)
     assert err <= 1e-3
     assert st.res_len == 150 - n * G + 1
+
+
+def _ref_step(model, ref, ids):
+    with torch.no_grad():
+        out = model(ids, past_key_values=ref.get_full_cache(), use_cache=True)
+    ref.add_tokens(out.past_key_values)
+    return out.logits
+
+
+def test_multitoken_steps_follow_reference_flow(hip_device):
+    """Forwards of several tokens on a non-empty cache (chunked prefill) run
+    the multi-token kernel causally over [history ; window ; new tokens]:
+    logits agree with the reference flow's forward over get_full_cache()
+    (fp32 SDPA over the oracle's served history) and the stores split the
+    context the same way after each step's flushes.  Model on the CPU in both
+    arms, attention of the packed arm on the GPU."""
+    from transformers import GPT2Config, GPT2LMHeadModel
+    torch.manual_seed(4)
+    model = GPT2LMHeadModel(GPT2Config(n_layer=4, n_head=4, n_embd=256)).eval()
+    G, R = 32, 64
+    ours = pc.KiviPackedCache.from_model(model, device="cuda:0", group_size=G,
+                                         residual_length=R)
+    ref = _OracleShim.from_model(model, group_size=G, residual_length=R)
+    gen = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, model.config.vocab_size, (2, 90), generator=gen)
+    with torch.no_grad(), pc.packed_attention(model):
+        model(ids, past_key_values=ours, use_cache=True)
+    _ref_step(model, ref, ids)
+    worst = 0.0
+    for n in [5, 1, 3, 8, 1, 17, 2, 64, 1, 40, 7]:
+        chunk = torch.randint(0, model.config.vocab_size, (2, n), generator=gen)
+        print(f"[packed-multi] step of {n} tokens", flush=True)
+        with torch.no_grad(), pc.packed_attention(model):
+            lo = model(chunk, past_key_values=ours, use_cache=True).logits
+        lr = _ref_step(model, ref, chunk)
+        err = ((lo - lr).abs().max() / lr.abs().max()).item()
+        worst = max(worst, err)
+        assert err <= 1e-3, err
+        assert torch.equal(lo.argmax(-1), lr.argmax(-1))
+        for lay in ours.layers:
+            lay.settle()
+        st = ours.store(0)
+        assert st.quantized_tokens == ref.get_stats(0)["quantized_tokens"]
+        assert st.res_len == ref.get_stats(0)["residual_tokens"]
+    print(f"[packed-multi] worst logits rel err {worst:.2e}", flush=True)
+    assert ours.total_flushes == ref.total_flushes
+
+
+def test_hf_assisted_generation(hip_device):
+    """transformers' assisted generation drives the cache: verification
+    passes of several tokens, then crop() of the rejected drafts.  Greedy
+    output equals plain greedy generation with the same cache type, and both
+    kinds of steps did occur."""
+    from transformers import GPT2Config, GPT2LMHeadModel
+    torch.manual_seed(6)
+    model = GPT2LMHeadModel(GPT2Config(n_layer=4, n_head=4, n_embd=256)).eval().to(hip_device)
+    torch.manual_seed(6)
+    draft = GPT2LMHeadModel(GPT2Config(n_layer=1, n_head=4, n_embd=256)).eval().to(hip_device)
+    draft.generation_config.num_assistant_tokens = 3
+    draft.generation_config.num_assistant_tokens_schedule = "constant"
+    draft.generation_config.assistant_confidence_threshold = 0.0
+    ids = torch.randint(0, model.config.vocab_size, (1, 40),
+                        generator=torch.Generator().manual_seed(7)).to(hip_device)
+    sizes, crops = [], []
+    update, crop = pc.KiviPackedLayer.update, pc.KiviPackedLayer.crop
+
+    def spy_update(self, k, v, *a, **kw):
+        if self.index == 0:
+            sizes.append(k.shape[2])
+        return update(self, k, v, *a, **kw)
+
+    def spy_crop(self, n):
+        if self.index == 0:
+            crops.append(int(n))
+        return crop(self, n)
+
+    outs = []
+    for assistant in (None, draft):
+        sizes.clear()
+        crops.clear()
+        cache = pc.KiviPackedCache.from_model(model, device="cuda:0", group_size=32,
+                                              residual_length=32)
+        kw = {} if assistant is None else {"assistant_model": assistant}
+        pc.KiviPackedLayer.update, pc.KiviPackedLayer.crop = spy_update, spy_crop
+        try:
+            with pc.packed_attention(model):
+                outs.append(model.generate(ids, past_key_values=cache, max_new_tokens=120,
+                                           do_sample=False, attention_mask=torch.ones_like(ids),
+                                           pad_token_id=0, **kw).cpu())
+        finally:
+            pc.KiviPackedLayer.update, pc.KiviPackedLayer.crop = update, crop
+        assert cache.get_seq_length() == ids.shape[1] + 119
+    n, tot = _match(outs[0][0].tolist(), outs[1][0].tolist())
+    print(f"[packed-assisted] token match {n}/{tot}; steps {sizes[-12:]}, crops {crops[-12:]}",
+          flush=True)
+    assert max(sizes[1:]) > 2 and any(c < 0 for c in crops)
+    assert torch.equal(outs[0], outs[1])

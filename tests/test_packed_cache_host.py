@@ -168,8 +168,9 @@ def test_unsupported_inputs_raise(cpu_store):
     cache = pc.KiviPackedCache.from_model(model, group_size=32, residual_length=32)
     with torch.no_grad(), pc.packed_attention(model):
         model(torch.tensor([[1, 2, 3]]), past_key_values=cache, use_cache=True)
-        with pytest.raises(NotImplementedError, match="non-empty cache"):
-            model(torch.tensor([[4, 5]]), past_key_values=cache, use_cache=True)
+        with pytest.raises(NotImplementedError, match="padded"):
+            model(torch.tensor([[4, 5]]), past_key_values=cache, use_cache=True,
+                  attention_mask=torch.tensor([[0, 1, 1, 1, 1]]))
     with torch.no_grad(), pc.packed_attention(model):
         with pytest.raises(RuntimeError, match="KiviPackedCache"):
             model(torch.tensor([[1, 2, 3]]), use_cache=False)
@@ -226,3 +227,136 @@ def test_unsupported_geometry_refused_up_front(cpu_store):
     assert decode_geometry_error(4, 4, 64, 32, 64) is None
     assert "q_heads / kv_heads = 3" in decode_geometry_error(6, 2, 64, 32, 32)
     assert "needs" in decode_geometry_error(8, 1, 256, 64, 32)     # LDS beyond the device's
+
+
+def _ref_step(model, ref, ids):
+    with torch.no_grad():
+        out = model(ids, past_key_values=ref.get_full_cache(), use_cache=True)
+    ref.add_tokens(out.past_key_values)
+    return out.logits
+
+
+def _check_layer0(ours, ref):
+    """Layer 0's store equals the reference's KiviCache bit for bit once the
+    flushes a multi-token step leaves to the next update are done."""
+    lay = ours.layers[0]
+    lay.settle()
+    st = ours.store(0)
+    k, v = list(ref.get_full_cache().layers)[0].keys, list(ref.get_full_cache().layers)[0].values
+    n_hist = st.quantized_tokens
+    assert st.res_len == k.shape[2] - n_hist
+    assert torch.equal(st.hist_k, k[:, :, :n_hist]) and torch.equal(st.hist_v, v[:, :, :n_hist])
+    assert torch.equal(st.res_k, k[:, :, n_hist:]) and torch.equal(st.res_v, v[:, :, n_hist:])
+
+
+@pytest.mark.parametrize("steps", [[5, 1, 3, 8, 1, 1, 17, 2, 1, 30, 4], [64, 1, 63, 2]])
+def test_multitoken_steps_follow_reference_flow(cpu_store, steps):
+    """Forwards of several tokens on a non-empty cache (chunked prefill)
+    attend causally over [history ; window ; new tokens] like the reference
+    flow's forward over get_full_cache(), and leave the same store once its
+    flushes are done: logits agree to float rounding (the stand-in attends in
+    float64, the reference flow in fp32 SDPA) and layer 0's history and
+    window bit for bit."""
+    model = _gpt2(3, 4, 128, seed=9)
+    G, R = 32, 64
+    ours = pc.KiviPackedCache.from_model(model, group_size=G, residual_length=R)
+    ref = _OracleShim.from_model(model, group_size=G, residual_length=R)
+    gen = torch.Generator().manual_seed(10)
+    ids = torch.randint(0, model.config.vocab_size, (2, 40), generator=gen)
+    with torch.no_grad(), pc.packed_attention(model):
+        model(ids, past_key_values=ours, use_cache=True)
+    _ref_step(model, ref, ids)
+    total = 40
+    for n in steps:
+        chunk = torch.randint(0, model.config.vocab_size, (2, n), generator=gen)
+        with torch.no_grad(), pc.packed_attention(model):
+            lo = model(chunk, past_key_values=ours, use_cache=True).logits
+        lr = _ref_step(model, ref, chunk)
+        total += n
+        assert lo.shape == lr.shape
+        torch.testing.assert_close(lo, lr, rtol=1e-4, atol=1e-4)
+        assert ours.get_seq_length() == total
+        _check_layer0(ours, ref)
+    assert ours.total_flushes == ref.total_flushes
+
+
+def test_crop_drops_a_steps_rejected_tokens(cpu_store):
+    """crop() after a multi-token step (assisted decoding's verification
+    pass) drops its rejected tokens: the cache then continues exactly as if
+    only the accepted tokens had been fed, here across a flush boundary
+    (the step takes the window past R, the crop brings it back)."""
+    model = _gpt2(2, 4, 128, seed=12)
+    G, R = 32, 64
+    ours = pc.KiviPackedCache.from_model(model, group_size=G, residual_length=R)
+    ref = _OracleShim.from_model(model, group_size=G, residual_length=R)
+    gen = torch.Generator().manual_seed(13)
+    ids = torch.randint(0, model.config.vocab_size, (1, 60), generator=gen)
+    with torch.no_grad(), pc.packed_attention(model):
+        model(ids, past_key_values=ours, use_cache=True)
+    _ref_step(model, ref, ids)
+    res0 = ours.store(0).res_len
+    draft = torch.randint(0, model.config.vocab_size, (1, 7), generator=gen)
+    with torch.no_grad(), pc.packed_attention(model):
+        model(draft, past_key_values=ours, use_cache=True)
+    assert ours.store(0).res_len == res0 + 7          # flushes wait for the next update
+    ours.crop(-5)                                     # two drafts accepted
+    assert ours.get_seq_length() == 62
+    _ref_step(model, ref, draft[:, :2])
+    nxt = torch.randint(0, model.config.vocab_size, (1, 1), generator=gen)
+    for step in range(40):
+        with torch.no_grad(), pc.packed_attention(model):
+            lo = model(nxt, past_key_values=ours, use_cache=True).logits
+        lr = _ref_step(model, ref, nxt)
+        torch.testing.assert_close(lo, lr, rtol=1e-4, atol=1e-4)
+        _check_layer0(ours, ref)
+        nxt = lo[:, -1:].argmax(-1)
+    # the legacy positive form keeps that many tokens
+    ours.crop(ours.get_seq_length() - 1)
+    assert ours.get_seq_length() == 60 + 2 + 40 - 1
+    # quantised tokens cannot be dropped
+    with pytest.raises(ValueError, match="cannot roll back"):
+        ours.crop(-(ours.store(0).res_len + 1))
+
+
+def test_hf_assisted_generation(cpu_store):
+    """transformers' assisted generation (a 1-layer draft proposing 3 tokens
+    per step) drives the cache with verification passes of several tokens and
+    crop() of the rejected drafts; greedy output equals plain greedy
+    generation with the same cache type."""
+    model = _gpt2(3, 4, 128, seed=7)
+    draft = _gpt2(1, 4, 128, seed=7)
+    draft.generation_config.num_assistant_tokens = 3
+    draft.generation_config.num_assistant_tokens_schedule = "constant"
+    draft.generation_config.assistant_confidence_threshold = 0.0
+    ids = torch.randint(0, model.config.vocab_size, (1, 20),
+                        generator=torch.Generator().manual_seed(1))
+    sizes, crops = [], []
+    update, crop = pc.KiviPackedLayer.update, pc.KiviPackedLayer.crop
+
+    def spy_update(self, k, v, *a, **kw):
+        if self.index == 0:
+            sizes.append(k.shape[2])
+        return update(self, k, v, *a, **kw)
+
+    def spy_crop(self, n):
+        if self.index == 0:
+            crops.append(int(n))
+        return crop(self, n)
+
+    outs = []
+    for assistant in (None, draft):
+        sizes.clear()
+        crops.clear()
+        cache = pc.KiviPackedCache.from_model(model, group_size=32, residual_length=32)
+        kw = {} if assistant is None else {"assistant_model": assistant}
+        pc.KiviPackedLayer.update, pc.KiviPackedLayer.crop = spy_update, spy_crop
+        try:
+            with pc.packed_attention(model):
+                outs.append(model.generate(ids, past_key_values=cache, max_new_tokens=60,
+                                           do_sample=False, attention_mask=torch.ones_like(ids),
+                                           pad_token_id=0, **kw))
+        finally:
+            pc.KiviPackedLayer.update, pc.KiviPackedLayer.crop = update, crop
+        assert cache.get_seq_length() == ids.shape[1] + 59
+    assert max(sizes[1:]) > 2 and any(c < 0 for c in crops)
+    assert torch.equal(outs[0], outs[1])
