@@ -116,6 +116,25 @@ def test_ragged_group_count(C):
     _assert_codec_parity(C, x, 32)
 
 
+def test_dequantize_unaligned_buffers(C):
+    """Dequantisation from packed bytes at any offset into an output at any
+    4-byte offset gives the oracle's bits (an unaligned output takes scalar
+    stores)."""
+    x = seeded_kv((1, 2, 301, 64), seed=17, kind="key")
+    _, packed, scales, zeros = _quantize_gpu(C, x, 64, "key")
+    ref = codec.dequantize_groups(_bits(packed), _bits(scales).view(np.float32),
+                                  _bits(zeros).view(np.float32), 64).view(np.uint32)
+    n = x.numel()
+    shifted = torch.empty(n // 4 + 1, dtype=torch.uint8, device="cuda:0")[1:]
+    shifted.copy_(packed)
+    assert shifted.data_ptr() % 4 != 0
+    for p, out in ((packed, torch.empty(n, device="cuda:0")),
+                   (shifted, torch.empty(n, device="cuda:0")),
+                   (packed, torch.empty(n + 1, device="cuda:0")[1:])):
+        C.dequantize_keys(p, scales, zeros, out.reshape(x.shape), 64)
+        assert np.array_equal(_bits(out).reshape(-1), ref)
+
+
 def test_unaligned_input_takes_scalar_path(C):
     base = seeded_kv((1, 1, 65, 32), seed=9, kind="key").reshape(-1)
     x = base[1:1 + 64 * 32].reshape(1, 1, 64, 32)   # 4-byte, not 16-byte aligned
