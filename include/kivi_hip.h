@@ -246,6 +246,11 @@ int kivi_packed_decode_attention_noalloc(
  * speculative verification), HF's causal mask over [cache ; new tokens].
  * causal == 0: every token sees the whole context (the reference's own
  * q_len = 3 attention check, tests/integration/test_attention_fix.py:19-43).
+ * kv_start: NULL, or a device array of batch int32 -- sequence b's first
+ * visible context position (a left-padded batch: HF's attention mask hides
+ * positions 0 .. kv_start[b]-1, quantised or in the window); each must leave
+ * every query token at least one visible position (for causal queries:
+ * kv_start[b] <= num_chunks*G + res_len - q_len).
  * When q_len * (q_heads / kv_heads) exceeds 8 the tokens are split over
  * several launches, each streaming the store once.  No reference counterpart
  * beyond that math (the reference runs HF attention on the CPU,
@@ -256,7 +261,8 @@ size_t kivi_packed_attention_workspace_size(int32_t batch, int32_t q_len, int32_
                                             int32_t num_chunks, int32_t res_len,
                                             int32_t num_splits);
 
-int kivi_packed_attention(const float* q, int32_t q_len, int32_t causal, const uint8_t* k_codes,
+int kivi_packed_attention(const float* q, int32_t q_len, int32_t causal,
+                          const int32_t* kv_start, const uint8_t* k_codes,
                           const float* k_scale, const float* k_zero, const uint8_t* v_codes,
                           const float* v_scale, const float* v_zero, const void* k_res,
                           const void* v_res, int32_t res_dtype, float* out, void* workspace,

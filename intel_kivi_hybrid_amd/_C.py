@@ -467,23 +467,41 @@ def packed_decode_attention(q, store, softmax_scale=None, out=None, num_splits=0
 
 
 def packed_attention(q, store, causal=True, softmax_scale=None, out=None, num_splits=0,
-                     workspace=None):
+                     workspace=None, kv_start=None):
     """Attention of ``L`` query tokens per sequence over a
     :class:`PackedKVStore`, ``q [B, Hq, L, D]`` fp32 (the layout HF attention
     functions receive); returns ``[B, L, Hq, D]`` fp32 (the layout they
     return).  ``causal``: the L queries are the residual window's last L
     tokens and token i attends to the cache up to itself (a multi-token
     forward on a non-empty cache); otherwise every query sees the whole
-    context.  Launched on the current stream."""
+    context (one query token sees it either way).  ``kv_start`` (B ints, a
+    list or an int32 tensor): sequence b's first visible context position,
+    for a left-padded batch; positions before it take no weight.  Checked
+    against the context length when given on the host.  Launched on the
+    current stream."""
     _check(q.dtype == torch.float32, "q must be float32, got ", _dtype_name(q.dtype))
     _check(q.dim() == 4 and q.shape[0] == store.B and q.shape[3] == store.D,
            "q must be [B, Hq, L, D] matching the store, got ", tuple(q.shape))
     _check(q.device == store.device, "q must be on the store's device")
     B, Hq, L, D = q.shape
     store._commit()
-    if causal:
+    if causal and L > 1:
         _check(L <= store.res_len, "causal attention of ", L, " query tokens needs them in "
                "the residual window (", store.res_len, " tokens)")
+    ks_ptr = 0
+    if kv_start is not None:
+        if not (torch.is_tensor(kv_start) and kv_start.device == q.device):
+            starts = [int(x) for x in (kv_start.tolist() if torch.is_tensor(kv_start)
+                                       else kv_start)]
+            T = store.quantized_tokens + store.res_len
+            last = T - L if causal else T - 1
+            _check(len(starts) == B and all(0 <= x <= last for x in starts),
+                   "kv_start must hold ", B, " positions in [0, ", last, "], got ", starts)
+            kv_start = torch.tensor(starts, dtype=torch.int32).to(q.device)
+        _check(kv_start.dtype == torch.int32 and kv_start.numel() == B and
+               kv_start.is_contiguous(), "kv_start must be a contiguous int32 tensor of ", B,
+               " positions")
+        ks_ptr = kv_start.data_ptr()
     qk = q.transpose(1, 2).contiguous()                                  # [B, L, Hq, D]
     if out is None:
         out = torch.empty(B, L, Hq, D, dtype=torch.float32, device=q.device)
@@ -501,7 +519,7 @@ def packed_attention(q, store, causal=True, softmax_scale=None, out=None, num_sp
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     with torch.cuda.device(q.device):
         _native.check(_lib.kivi_packed_attention(
-            ctypes.c_void_p(qk.data_ptr()), L, 1 if causal else 0,
+            ctypes.c_void_p(qk.data_ptr()), L, 1 if causal else 0, ctypes.c_void_p(ks_ptr),
             ctypes.c_void_p(store.k_codes.data_ptr()),
             ctypes.c_void_p(store.k_scale.data_ptr()), ctypes.c_void_p(store.k_zero.data_ptr()),
             ctypes.c_void_p(store.v_codes.data_ptr()), ctypes.c_void_p(store.v_scale.data_ptr()),

@@ -56,9 +56,9 @@ SIGNATURES = {
                                      _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp],
     "kivi_packed_attention_workspace_size": [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                              _i32, _i32],
-    "kivi_packed_attention": [_vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp,
-                              _vp, ctypes.c_size_t, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
-                              _i32, _i32, _i32, _i32, _f32, _i32, _vp],
+    "kivi_packed_attention": [_vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
+                              _vp, _vp, ctypes.c_size_t, _i32, _i32, _i32, _i32, _i32, _i32,
+                              _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp],
     "kivi_packed_decode_attention_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
                                              _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                              _i32, _i32, _i32, _i32, _f32, _i32, _vp],

@@ -201,19 +201,22 @@ class KiviPackedLayer(CacheLayerMixin):
         return kt, vt
 
     # --------------------------------------------------------- attention
-    def attend(self, query: torch.Tensor, scaling: Optional[float]) -> torch.Tensor:
+    def attend(self, query: torch.Tensor, scaling: Optional[float],
+               kv_start: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Attention of ``query [B, Hq, L, D]`` (the step's L new tokens, the
         window's newest) over this layer's store, causal among them; returns
-        ``[B, L, Hq, D]`` in the query's dtype and device.  A one-token step
-        does its flushes now; a longer one leaves them to the next update."""
+        ``[B, L, Hq, D]`` in the query's dtype and device.  ``kv_start``
+        (int32 ``[B]`` on the store's device): each sequence's first visible
+        position, for a left-padded batch.  A one-token step does its flushes
+        now; a longer one leaves them to the next update."""
         st = self.store
         L = query.shape[2]
         if L == 1:
             q = query[:, :, 0, :].to(st.device, torch.float32).contiguous()
-            o = st.attention(q, softmax_scale=scaling).unsqueeze(1)
+            o = st.attention(q, softmax_scale=scaling, kv_start=kv_start).unsqueeze(1)
         else:
             q = query.to(st.device, torch.float32)
-            o = st.attention(q, softmax_scale=scaling, causal=True)
+            o = st.attention(q, softmax_scale=scaling, causal=True, kv_start=kv_start)
         self._awaiting_attention = False
         if L == 1:
             self.settle()
@@ -296,6 +299,9 @@ class KiviPackedCache(Cache):
                              f"head_dim={head_dim}, group_size={group_size}, "
                              f"value_group_size={gv}: {err}")
         self._heads_checked = False
+        # (mask, kv_start) of the latest padded forward: every layer of a
+        # forward receives the same mask object, which is read once.
+        self._mask_memo = None
         register_packed_attention()
         self.device = _resolve_device(device)
         self.head_dim = head_dim
@@ -446,15 +452,43 @@ def kivi_packed_attention_forward(module, query, key, value, attention_mask, sca
                                       dropout=dropout, scaling=scaling, **kwargs)
     if dropout:
         raise ValueError(f"'{KIVI_ATTENTION}' attention is inference-only (dropout={dropout})")
-    if attention_mask is not None:
-        raise NotImplementedError(
-            f"'{KIVI_ATTENTION}' attention over the cache takes no attention mask (padded "
-            f"batches are not supported): every sequence attends over its whole cache, its "
-            f"new tokens causally")
     for name in ("sliding_window", "softcap", "s_aux"):
         if kwargs.get(name) is not None:
             raise NotImplementedError(f"'{KIVI_ATTENTION}' attention does not support {name}")
-    return layer.attend(query, scaling), None
+    kv_start = None
+    if attention_mask is not None:
+        kv_start = _padding_starts(owner, attention_mask, query.shape[2],
+                                   layer.get_seq_length(), layer.store.device)
+    return layer.attend(query, scaling, kv_start), None
+
+
+def _padding_starts(owner: "KiviPackedCache", mask: torch.Tensor, q_len: int, kv_len: int,
+                    device) -> torch.Tensor:
+    """Each sequence's first visible position from HF's boolean mask
+    ``[B, 1, q_len, kv_len]`` (True = attend) of a left-padded batch: the
+    mask must be exactly "position >= start[b], and causal among the new
+    tokens", which is checked (one device sync per forward: every layer gets
+    the same mask object, read once).  Anything else -- right padding, holes,
+    a float mask -- is refused."""
+    memo = owner._mask_memo
+    if memo is not None and memo[0] is mask:
+        return memo[1]
+    starts = None
+    if mask.dtype == torch.bool and mask.dim() == 4 and mask.shape[1] == 1 and \
+            tuple(mask.shape[2:]) == (q_len, kv_len):
+        s = mask[:, 0, -1, :].int().argmax(-1)                    # first visible of the newest
+        t = torch.arange(kv_len, device=mask.device)
+        newest = kv_len - q_len + torch.arange(q_len, device=mask.device)
+        expect = (t[None, None, :] >= s[:, None, None]) & (t[None, None, :] <= newest[None, :, None])
+        if torch.equal(mask[:, 0], expect):
+            starts = s.to(device=device, dtype=torch.int32)
+    if starts is None:
+        raise NotImplementedError(
+            f"'{KIVI_ATTENTION}' attention over the cache takes the mask of a left-padded batch "
+            f"(each sequence hides its first positions, causal among the new tokens); this "
+            f"mask is something else (shape {tuple(mask.shape)}, dtype {mask.dtype})")
+    owner._mask_memo = (mask, starts)
+    return starts
 
 
 def kivi_causal_mask(batch_size: int, q_length: int, kv_length: int, q_offset: int = 0,

@@ -54,6 +54,7 @@ struct AttnArgs {
     float qscale;      // softmax scale * log2(e)
     int res_dt;        // 0 fp32, 1 bf16, 2 fp16
     QueryRows qr;      // HG query rows per kv head (kivi_attention.hpp)
+    const int32_t* kv_start;   // [B] first visible position, or nullptr
 };
 
 __device__ __forceinline__ void wave_sync() {
@@ -90,6 +91,8 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
     float* sqs = smem + HG * D + wave * wave_floats;       // [HG][D]  q * k_scale
     float* sp = sqs + HG * D;                              // [HG][64] probabilities
     const int64_t bh = (int64_t)b * a.Hkv + kvh;
+    // left padding: context positions before kv_lo take no weight
+    const int kv_lo = a.kv_start ? a.kv_start[b] : 0;
 
     for (int e = threadIdx.x; e < HG * D; e += kAttnBlock) {
         const int h = e / D, d = e % D;
@@ -133,7 +136,7 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
             for (int h = 0; h < HG; ++h) bias[h] = wave_sum(bpart[h]);
             wave_sync();
             const int t = lane;
-            valid = t < G;
+            valid = t < G && u * G + t >= kv_lo;
             float acc[HG];
 #pragma unroll
             for (int h = 0; h < HG; ++h) acc[h] = 0.f;
@@ -167,7 +170,7 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
             rbase = (u - a.n_chunks) * kWave;
             rcount = min(kWave, a.res_len - rbase);
             const int t = rbase + lane;
-            valid = lane < rcount;
+            valid = lane < rcount && a.n_chunks * G + t >= kv_lo;
             float acc[HG];
 #pragma unroll
             for (int h = 0; h < HG; ++h) acc[h] = 0.f;
@@ -575,7 +578,8 @@ size_t workspace_for(int batch, int q_len, int q_heads, int kv_heads, int head_d
 // up to itself, else every token sees the whole context.  Tokens are split
 // across launches when q_len * (q_heads / kv_heads) exceeds 8 rows; each
 // launch streams the store once.
-int attention_impl(const float* q, int32_t q_len, int32_t causal, const uint8_t* k_codes,
+int attention_impl(const float* q, int32_t q_len, int32_t causal, const int32_t* kv_start,
+                   const uint8_t* k_codes,
                    const float* k_scale, const float* k_zero, const uint8_t* v_codes,
                    const float* v_scale, const float* v_zero, const void* k_res,
                    const void* v_res, int32_t res_dtype, float* out, void* workspace,
@@ -671,13 +675,14 @@ int attention_impl(const float* q, int32_t q_len, int32_t causal, const uint8_t*
                          group_size_v, chunk_capacity, num_chunks, res_capacity, res_start,
                          res_len, p.n_qsplits, p.chunks_per_wave, p.res_waves,
                          p.early_per_pass_x2, p.n_splits, softmax_scale * kLog2e, k_new, v_new,
-                         new_sb, new_sh, new_slot, res_dtype, qr};
+                         new_sb, new_sh, new_slot, res_dtype, qr, kv_start};
             rc = launch_attention_mfma(L, st);
         } else {
             AttnArgs a{qi, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res, v_res, oi,
                        part_o, part_ml, q_heads, kv_heads, head_dim, group_size_k, group_size_v,
                        chunk_capacity, num_chunks, res_capacity, res_start, res_len, p.n_units,
-                       p.n_splits, p.units_per_split, softmax_scale * kLog2e, res_dtype, qr};
+                       p.n_splits, p.units_per_split, softmax_scale * kLog2e, res_dtype, qr,
+                       kv_start};
             const dim3 grid(p.n_splits, kv_heads, batch);
             const size_t lds = (size_t)(rows * head_dim +
                                         kAttnWaves * (rows * head_dim + rows * kWave)) *
@@ -724,7 +729,8 @@ size_t kivi_packed_attention_workspace_size(int32_t batch, int32_t q_len, int32_
                          num_chunks, res_len, num_splits);
 }
 
-int kivi_packed_attention(const float* q, int32_t q_len, int32_t causal, const uint8_t* k_codes,
+int kivi_packed_attention(const float* q, int32_t q_len, int32_t causal,
+                          const int32_t* kv_start, const uint8_t* k_codes,
                           const float* k_scale, const float* k_zero, const uint8_t* v_codes,
                           const float* v_scale, const float* v_zero, const void* k_res,
                           const void* v_res, int32_t res_dtype, float* out, void* workspace,
@@ -733,11 +739,11 @@ int kivi_packed_attention(const float* q, int32_t q_len, int32_t causal, const u
                           int32_t group_size_v, int32_t chunk_capacity, int32_t num_chunks,
                           int32_t res_capacity, int32_t res_start, int32_t res_len,
                           float softmax_scale, int32_t num_splits, void* stream) {
-    return attention_impl(q, q_len, causal, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero,
-                          k_res, v_res, res_dtype, out, workspace, workspace_bytes, batch,
-                          q_heads, kv_heads, head_dim, group_size_k, group_size_v,
-                          chunk_capacity, num_chunks, res_capacity, res_start, res_len,
-                          softmax_scale, num_splits, nullptr, nullptr, 0, 0, stream);
+    return attention_impl(q, q_len, causal, kv_start, k_codes, k_scale, k_zero, v_codes,
+                          v_scale, v_zero, k_res, v_res, res_dtype, out, workspace,
+                          workspace_bytes, batch, q_heads, kv_heads, head_dim, group_size_k,
+                          group_size_v, chunk_capacity, num_chunks, res_capacity, res_start,
+                          res_len, softmax_scale, num_splits, nullptr, nullptr, 0, 0, stream);
 }
 
 int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const float* k_scale,
@@ -750,7 +756,7 @@ int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const f
                                  int32_t num_chunks, int32_t res_capacity, int32_t res_start,
                                  int32_t res_len, float softmax_scale, int32_t num_splits,
                                  void* stream) {
-    return attention_impl(q, 1, 1, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
+    return attention_impl(q, 1, 1, nullptr, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
                                  v_res, res_dtype, out, workspace, workspace_bytes, batch, q_heads,
                                  kv_heads, head_dim, group_size_k, group_size_v, chunk_capacity,
                                  num_chunks, res_capacity, res_start, res_len, softmax_scale,
@@ -778,7 +784,7 @@ int kivi_packed_decode_attention_noalloc(
     void* ws = nullptr;
     const int rc = scratch_for_current_device(&ws);
     if (rc) return rc;
-    return attention_impl(q, 1, 1, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
+    return attention_impl(q, 1, 1, nullptr, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
                                  v_res, res_dtype, out, ws, KIVI_NOALLOC_SCRATCH_BYTES, batch,
                                  q_heads, kv_heads, head_dim, group_size_k, group_size_v,
                                  chunk_capacity, num_chunks, res_capacity, res_start, res_len,
@@ -812,7 +818,7 @@ int kivi_packed_decode_attention_append(
         return set_error(kErrInvalidArgument,
                          "new-token rows must be %d-byte aligned (strides multiples of 4)",
                          (int)vb);
-    return attention_impl(q, 1, 1, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
+    return attention_impl(q, 1, 1, nullptr, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
                                  v_res, res_dtype, out, workspace, workspace_bytes, batch, q_heads,
                                  kv_heads, head_dim, group_size_k, group_size_v, chunk_capacity,
                                  num_chunks, res_capacity, res_start, res_len, softmax_scale,

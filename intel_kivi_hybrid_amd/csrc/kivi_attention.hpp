@@ -62,6 +62,10 @@ struct AttnLaunch {
     int new_slot = 0;
     int res_dt = 0;          // ring element type: 0 fp32, 1 bf16, 2 fp16
     QueryRows qr;
+    // Optional [B] first visible context position per sequence (a
+    // left-padded batch): positions before kv_start[b] -- quantised or in
+    // the window -- take no weight.  nullptr: every position is visible.
+    const int32_t* kv_start = nullptr;
 };
 
 // Launches the matrix-core kernel (kLayoutMfma stores, Hq/Hkv in {1,2,4,8}).

@@ -437,6 +437,8 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     const int NG = NGC > 0 ? NGC : D / a.Gv;
     const int Gv = NGC > 0 ? D / NGC : a.Gv;
     const int64_t bh = (int64_t)b * a.Hkv + kvh;
+    // Left padding: context positions before kv_lo take no weight (0: none).
+    const int kv_lo = __builtin_amdgcn_readfirstlane(a.kv_start ? a.kv_start[b] : 0);
 
     unsigned char* wl = smem + wave * S::wave_lds(NG);
     uint16_t* WA = reinterpret_cast<uint16_t*>(wl + S::OFF_WA);
@@ -647,7 +649,10 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // Scores of the chunk's G tokens (matrix cores), then the online softmax:
     // lane group gq holds heads 2gq, 2gq+1.  Returns whether any running max
     // moved (then O and l are already rescaled and AL[slot] holds the factors).
-    auto kside = [&](const ChunkRegs<S>& r, auto slot_c) -> bool {
+    // `chunk` is the chunk's index: its tokens before kv_lo (a left-padded
+    // sequence) get score -inf and weight 0, on a wave-uniform branch that
+    // unpadded sequences never take.
+    auto kside = [&](const ChunkRegs<S>& r, auto slot_c, int chunk) -> bool {
         constexpr int slot = decltype(slot_c)::value;
         bf16x8_t Aw[S::KS], Ab[S::NBB];
 #pragma unroll
@@ -681,10 +686,21 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                sc[e][nb] = Sc[nb][2 * e] + Sc[nb][2 * e + 1];
-                over |= hvalid[e] && sc[e][nb] > m_thr[e];
+            for (int nb = 0; nb < NB; ++nb) sc[e][nb] = Sc[nb][2 * e] + Sc[nb][2 * e + 1];
+        }
+        const int n_masked = kv_lo - chunk * G;       // leading tokens hidden by padding
+        if (__builtin_expect(n_masked > 0, 0)) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    sc[e][nb] = 16 * nb + col < n_masked ? -INFINITY : sc[e][nb];
             }
+        }
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) over |= hvalid[e] && sc[e][nb] > m_thr[e];
         }
         const bool any = __builtin_amdgcn_ballot_w64(over) != 0;
         if (__builtin_expect(any, 0)) {
@@ -712,14 +728,28 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             }
         }
         float* pl = PL + slot * (HG * S::PL_ROW);
+        float pv[2][NB];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) pv[e][nb] = exp2_fast(sc[e][nb] - m_run[e]);
+        }
+        // (a hidden token's weight is 0 even while the running max is -inf)
+        if (__builtin_expect(n_masked > 0, 0)) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    pv[e][nb] = 16 * nb + col < n_masked ? 0.f : pv[e][nb];
+            }
+        }
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             float lsum = 0.f;
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
-                const float p = exp2_fast(sc[e][nb] - m_run[e]);
-                lsum += p;
-                if (hvalid[e]) pl[(2 * gq + e) * S::PL_ROW + 16 * nb + col] = p;
+                lsum += pv[e][nb];
+                if (hvalid[e]) pl[(2 * gq + e) * S::PL_ROW + 16 * nb + col] = pv[e][nb];
             }
             l_part[e] += lsum;
         }
@@ -831,6 +861,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         const int r1 = min((p0 + pbase + (widx < pextra ? 1 : 0)) * kResPass, a.res_len);
         const int tk = lane / 4, qq = lane % 4;
         const int c4 = lane % F4, ts = lane / F4;
+        const int r_lo = kv_lo - a.n_chunks * G;      // first visible window token
         // Four channels of a ring row widened to fp32.  The ring's width is
         // a template parameter (a run-time branch here would cost registers
         // at the kernel's peak, the prefetched chunks being live); bf16 vs
@@ -881,14 +912,15 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                 acc += dpp<0xB1>(acc);        // quad_perm [1,0,3,2]
                 acc += dpp<0x4E>(acc);        // quad_perm [2,3,0,1]
                 // row h sees the window's first qr.visible(h) tokens
-                sres[h] = tk < n && t0 + tk < a.qr.visible(h, a.res_len) ? acc : -INFINITY;
+                sres[h] = tk < n && t0 + tk >= r_lo && t0 + tk < a.qr.visible(h, a.res_len)
+                              ? acc : -INFINITY;
             }
 #pragma unroll
             for (int h = 0; h < HG; ++h) {
                 const float mnew = fmaxf(mr[h], wave_max(sres[h]));
                 const float alpha = mr[h] == -INFINITY ? 0.f : exp2_fast(mr[h] - mnew);
                 mr[h] = mnew;
-                const float p = tk < n && t0 + tk < a.qr.visible(h, a.res_len)
+                const float p = tk < n && t0 + tk >= r_lo && t0 + tk < a.qr.visible(h, a.res_len)
                                     ? exp2_fast(sres[h] - mnew) : 0.f;
                 lr[h] = lr[h] * alpha + 0.25f * wave_sum(p);    // each token sits in 4 lanes
                 orr[h][0] *= alpha;
@@ -962,12 +994,13 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         wave_sync();
         wprep(Int<0>{});
         wave_sync();
-        any_cur = kside(buf[0], Int<0>{});
+        any_cur = kside(buf[0], Int<0>{}, cid[0]);
     }
     // Step i (of the wave's chunks, counted from 0) uses double-buffer
     // slot i & 1; PF is even, so within the unrolled ring the slot of step k
     // is k & 1, a compile-time constant.
-    auto step = [&](const ChunkRegs<S>& cur, const ChunkRegs<S>& nxt, bool has_next, auto slot_c) {
+    auto step = [&](const ChunkRegs<S>& cur, const ChunkRegs<S>& nxt, bool has_next, auto slot_c,
+                    int nxt_chunk) {
         constexpr int slot = decltype(slot_c)::value, nslot = slot ^ 1;
         if (has_next) stage_meta<S>(nxt, MT + nslot * meta_stride, lane, NG, meta_floats);
         wave_sync();
@@ -984,7 +1017,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         // instead, did not help.
         __builtin_amdgcn_s_setprio(2);
         vside(cur);
-        if (has_next) any_cur = kside(nxt, Int<nslot>{});
+        if (has_next) any_cur = kside(nxt, Int<nslot>{}, nxt_chunk);
         __builtin_amdgcn_s_setprio(0);
     };
     static_assert(PF % 2 == 0, "the slot parity of a ring step must be static");
@@ -1036,7 +1069,8 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     while (cid[PF - 1] >= 0) {
         static_for<0, PF>([&](auto kc) {
             constexpr int k = decltype(kc)::value;
-            step(buf[k], buf[(k + 1) % PF], k + 1 < PF || cid[0] >= 0, Int<k & 1>{});
+            step(buf[k], buf[(k + 1) % PF], k + 1 < PF || cid[0] >= 0, Int<k & 1>{},
+                 cid[(k + 1) % PF]);
             cid[k] = chunk_of(next_j++);
             load_chunk<S>(buf[k], src, cid[k] >= 0 ? cid[k] : c_last);
         });
@@ -1047,7 +1081,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     }
     static_for<0, PF - 1>([&](auto kc) {
         constexpr int k = decltype(kc)::value;
-        if (cid[k] >= 0) step(buf[k], buf[k + 1], cid[k + 1] >= 0, Int<k & 1>{});
+        if (cid[k] >= 0) step(buf[k], buf[k + 1], cid[k + 1] >= 0, Int<k & 1>{}, cid[k + 1]);
     });
     // ---- wave state -> merge slot --------------------------------------------
     wave_sync();

@@ -536,17 +536,29 @@ class PackedKVStore:
 
     def attention(self, q: torch.Tensor, softmax_scale: Optional[float] = None,
                   out: Optional[torch.Tensor] = None, num_splits: int = 0,
-                  workspace: Optional[torch.Tensor] = None, causal: bool = True) -> torch.Tensor:
+                  workspace: Optional[torch.Tensor] = None, causal: bool = True,
+                  kv_start=None) -> torch.Tensor:
         """Fused attention over [packed history ; residual].
 
         ``q [B, Hq, D]`` (or ``[B, Hq, 1, D]``): one decode token per
         sequence; returns ``[B, Hq, D]`` fp32.  ``q [B, Hq, L, D]`` with
         L > 1: L query tokens per sequence (see ``_C.packed_attention``;
         ``causal`` by default: they are the window's last L tokens); returns
-        ``[B, L, Hq, D]`` fp32."""
+        ``[B, L, Hq, D]`` fp32.  ``kv_start``: per-sequence first visible
+        position of a left-padded batch (``_C.packed_attention``)."""
         from . import _C
+        if kv_start is not None and (q.dim() == 3 or q.shape[2] == 1):
+            q4 = q if q.dim() == 4 else q.unsqueeze(2)
+            o = _C.packed_attention(q4, self, causal=True, softmax_scale=softmax_scale,
+                                    num_splits=num_splits, workspace=workspace,
+                                    kv_start=kv_start)[:, 0]
+            if out is not None:
+                out.copy_(o.view_as(out))
+                return out
+            return o
         if q.dim() == 4 and q.shape[2] > 1:
             return _C.packed_attention(q, self, causal=causal, softmax_scale=softmax_scale,
-                                       out=out, num_splits=num_splits, workspace=workspace)
+                                       out=out, num_splits=num_splits, workspace=workspace,
+                                       kv_start=kv_start)
         return _C.packed_decode_attention(q, self, softmax_scale=softmax_scale, out=out,
                                           num_splits=num_splits, workspace=workspace)

@@ -13,9 +13,13 @@ from __future__ import annotations
 import numpy as np
 
 
-def decode_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None):
+def decode_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None, kv_start=None):
     """q: [B, Hq, D]; k_hist/v_hist: [B, Hkv, Tq, D] dequantised history;
     k_res/v_res: [B, Hkv, Tr, D] fp32 residual.  Returns o [B, Hq, D] float64.
+
+    ``kv_start`` (B ints, optional): sequence b attends to context positions
+    kv_start[b] .. Tq+Tr-1 only -- a left-padded batch, whose HF attention
+    mask hides each sequence's leading pad positions.
 
     Works one (batch, kv-head) at a time so that long contexts fit in memory.
     """
@@ -38,6 +42,8 @@ def decode_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None):
                 parts_v.append(np.asarray(v_res[b, kh], dtype=np.float64))
             K = np.concatenate(parts_k, axis=0)          # [T, D]
             V = np.concatenate(parts_v, axis=0)
+            s0 = 0 if kv_start is None else int(kv_start[b])
+            K, V = K[s0:], V[s0:]
             qh = q[b, kh * g:(kh + 1) * g]               # [g, D]
             s = (qh @ K.T) * scale                       # [g, T]
             s -= s.max(axis=1, keepdims=True)
@@ -47,7 +53,7 @@ def decode_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None):
     return out
 
 
-def prefix_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None):
+def prefix_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None, kv_start=None):
     """Causal attention of the window's last ``q_len`` tokens.
 
     q: [B, q_len, Hq, D] -- the queries of the ``q_len`` newest tokens, which
@@ -58,7 +64,8 @@ def prefix_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None):
     the HF model's causal mask over [cache ; new tokens] in a forward of
     ``q_len`` tokens on a non-empty cache (the reference's own attention check
     uses q_len=3, tests/integration/test_attention_fix.py:19-36,91-93).
-    GQA as in decode_attention.  Returns o [B, q_len, Hq, D] float64.
+    GQA and ``kv_start`` as in decode_attention.  Returns o [B, q_len, Hq, D]
+    float64.
     """
     q = np.asarray(q, dtype=np.float64)
     B, L, Hq, D = q.shape
@@ -81,12 +88,13 @@ def prefix_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None):
             K = np.concatenate(parts_k, axis=0)          # [T, D]
             V = np.concatenate(parts_v, axis=0)
             T = K.shape[0]
+            s0 = 0 if kv_start is None else int(kv_start[b])
             for i in range(L):
                 n = T - L + i + 1                        # visible tokens of query i
                 qh = q[b, i, kh * g:(kh + 1) * g]        # [g, D]
-                s = (qh @ K[:n].T) * scale               # [g, n]
+                s = (qh @ K[s0:n].T) * scale             # [g, n - s0]
                 s -= s.max(axis=1, keepdims=True)
                 p = np.exp(s)
                 p /= p.sum(axis=1, keepdims=True)
-                out[b, i, kh * g:(kh + 1) * g] = p @ V[:n]
+                out[b, i, kh * g:(kh + 1) * g] = p @ V[s0:n]
     return out

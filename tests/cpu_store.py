@@ -74,17 +74,18 @@ class CpuPackedStore:
                 flushes += 1
         return flushes
 
-    def attention(self, q, softmax_scale=None, causal=True):
+    def attention(self, q, softmax_scale=None, causal=True, kv_start=None):
+        starts = None if kv_start is None else [int(x) for x in kv_start]
         if q.dim() == 4 and q.shape[2] > 1:
             # [B, Hq, L, D] -> [B, L, Hq, D]: the window's newest L tokens
             assert causal and q.shape[2] <= self.res_len
             o = oracle_attention.prefix_attention(q.transpose(1, 2).numpy(), self.hist_k.numpy(),
                                                   self.hist_v.numpy(), self.res_k.numpy(),
-                                                  self.res_v.numpy(), softmax_scale)
+                                                  self.res_v.numpy(), softmax_scale, starts)
             return torch.from_numpy(o).float()
         o = oracle_attention.decode_attention(q.numpy(), self.hist_k.numpy(),
                                               self.hist_v.numpy(), self.res_k.numpy(),
-                                              self.res_v.numpy(), softmax_scale)
+                                              self.res_v.numpy(), softmax_scale, starts)
         return torch.from_numpy(o).float()
 
     def grow_residual(self, capacity):

@@ -225,3 +225,74 @@ def test_prefix_planted_mistakes_fail(name):
         except (ValueError, IndexError):
             worst = np.inf
     assert worst > 1e-6, f"mutant '{name}' passes (max err {worst:.2e})"
+
+
+# ---- left-padded batches: each sequence hides its first kv_start[b] positions
+PAD_SHAPES = [
+    # B, L, Hq, Hkv, D, Tq, Tr, kv_start
+    (3, 1, 8, 2, 32, 64, 17, (0, 5, 70)),        # start in the history, in the window
+    (2, 3, 4, 4, 16, 32, 9, (31, 32)),            # the last history token, the first window one
+    (2, 4, 6, 3, 16, 0, 12, (0, 7)),              # no history
+]
+
+
+def _sdpa_padded(q, kh, vh, kr, vr, kv_start):
+    B, L, Hq, D = q.shape
+    Hkv = kr.shape[1]
+    K = torch.cat([kh, kr], dim=2).repeat_interleave(Hq // Hkv, dim=1)
+    V = torch.cat([vh, vr], dim=2).repeat_interleave(Hq // Hkv, dim=1)
+    T = K.shape[2]
+    t = torch.arange(T)
+    causal = t[None, :] <= (T - L + torch.arange(L))[:, None]                     # [L, T]
+    pad = t[None, :] >= torch.tensor(kv_start)[:, None]                          # [B, T]
+    mask = causal[None, None] & pad[:, None, None]                               # [B, 1, L, T]
+    o = torch.nn.functional.scaled_dot_product_attention(q.transpose(1, 2), K, V,
+                                                         attn_mask=mask)
+    return o.transpose(1, 2)
+
+
+def _padded_err(mod, shape, seed):
+    B, L, Hq, Hkv, D, Tq, Tr, kv_start = shape
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, L, Hq, D, generator=g, dtype=torch.float64)
+    kh, vh = (torch.randn(B, Hkv, Tq, D, generator=g, dtype=torch.float64) for _ in range(2))
+    kr, vr = (torch.randn(B, Hkv, Tr, D, generator=g, dtype=torch.float64) for _ in range(2))
+    ref = _sdpa_padded(q, kh, vh, kr, vr, kv_start).numpy()
+    args = (kh.numpy(), vh.numpy(), kr.numpy(), vr.numpy())
+    if L == 1:
+        out = mod.decode_attention(q[:, 0].numpy(), *args, kv_start=kv_start)[:, None]
+    else:
+        out = mod.prefix_attention(q.numpy(), *args, kv_start=kv_start)
+    return float(np.abs(out - ref).max())
+
+
+@pytest.mark.parametrize("shape", PAD_SHAPES)
+def test_padded_oracle_matches_sdpa_float64(shape):
+    """kv_start against SDPA with HF's boolean mask of a left-padded batch
+    (padding positions hidden, causal among the new tokens)."""
+    assert _padded_err(oracle_attention, shape, seed=len(shape)) < 1e-12
+
+
+PAD_MUTANTS = {
+    "decode start ignored": ("K, V = K[s0:], V[s0:]", "K, V = K, V"),
+    "decode start off by one": ("K, V = K[s0:], V[s0:]", "K, V = K[s0 + 1:], V[s0 + 1:]"),
+    "prefix start ignored": ("K[s0:n].T", "K[:n].T"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(PAD_MUTANTS))
+def test_padded_planted_mistakes_fail(name):
+    old, new = PAD_MUTANTS[name]
+    path = os.path.abspath(oracle_attention.__file__)
+    with open(path) as f:
+        src = f.read()
+    assert src.count(old) == 1, f"mutation site for '{name}' not found"
+    mutant = types.ModuleType("oracle_pad_mutant")
+    exec(compile(src.replace(old, new), path, "exec"), mutant.__dict__)
+    worst = 0.0
+    for shape in PAD_SHAPES:
+        try:
+            worst = max(worst, _padded_err(mutant, shape, seed=len(shape)))
+        except (ValueError, IndexError):
+            worst = np.inf
+    assert worst > 1e-6, f"mutant '{name}' passes (max err {worst:.2e})"

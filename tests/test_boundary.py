@@ -213,11 +213,11 @@ def test_store_entry_points_reject_bad_arguments():
                                           None)
     assert rc == 1 and "res_dtype 4" in _native.last_error()
     # several query tokens: causal ones must sit in the window, q_len >= 1
-    rc = lib.kivi_packed_attention(p, 3, 1, p, p, p, p, p, p, p, p, 0, p, None, 0, 1, 4, 4, 64,
-                                   32, 32, 1, 1, 32, 0, 2, ctypes.c_float(0.1), 0, None)
+    rc = lib.kivi_packed_attention(p, 3, 1, None, p, p, p, p, p, p, p, p, 0, p, None, 0, 1, 4,
+                                   4, 64, 32, 32, 1, 1, 32, 0, 2, ctypes.c_float(0.1), 0, None)
     assert rc == 1 and "3 query tokens needs them in the residual" in _native.last_error()
-    rc = lib.kivi_packed_attention(p, 0, 0, p, p, p, p, p, p, p, p, 0, p, None, 0, 1, 4, 4, 64,
-                                   32, 32, 1, 1, 32, 0, 2, ctypes.c_float(0.1), 0, None)
+    rc = lib.kivi_packed_attention(p, 0, 0, None, p, p, p, p, p, p, p, p, 0, p, None, 0, 1, 4,
+                                   4, 64, 32, 32, 1, 1, 32, 0, 2, ctypes.c_float(0.1), 0, None)
     assert rc == 1 and "q_len 0 must be positive" in _native.last_error()
 
 

@@ -283,3 +283,53 @@ def test_hf_assisted_generation(hip_device):
           flush=True)
     assert max(sizes[1:]) > 2 and any(c < 0 for c in crops)
     assert torch.equal(outs[0], outs[1])
+
+
+def test_left_padded_batch_follows_reference_flow(hip_device):
+    """A left-padded batch of three prompts (50, 37 and 12 tokens) decoded
+    with one-token and multi-token steps: the packed attention on the GPU
+    hides each sequence's pad positions from HF's mask, and the logits agree
+    with the reference flow's (HF SDPA with the same mask over
+    get_full_cache()); the stores split the context the same way.  Model on
+    the CPU in both arms."""
+    from transformers import GPT2Config, GPT2LMHeadModel
+    torch.manual_seed(21)
+    model = GPT2LMHeadModel(GPT2Config(n_layer=3, n_head=4, n_embd=256)).eval()
+    G, R = 32, 64
+    ours = pc.KiviPackedCache.from_model(model, device="cuda:0", group_size=G,
+                                         residual_length=R)
+    ref = _OracleShim.from_model(model, group_size=G, residual_length=R)
+    gen = torch.Generator().manual_seed(22)
+    lengths = [50, 37, 12]
+    T = max(lengths)
+    ids = torch.zeros(3, T, dtype=torch.long)
+    mask = torch.zeros(3, T, dtype=torch.long)
+    for b, n in enumerate(lengths):
+        ids[b, T - n:] = torch.randint(1, model.config.vocab_size, (n,), generator=gen)
+        mask[b, T - n:] = 1
+
+    def kw(n):
+        return dict(attention_mask=mask, position_ids=(mask.cumsum(-1) - 1).clamp(min=0)[:, -n:],
+                    use_cache=True)
+    with torch.no_grad(), pc.packed_attention(model):
+        model(ids, past_key_values=ours, **kw(T))
+    _ref_step_kw = lambda x, n: model(x, past_key_values=ref.get_full_cache(), **kw(n))  # noqa: E731
+    with torch.no_grad():
+        ref.add_tokens(model(ids, **kw(T)).past_key_values)
+    worst = 0.0
+    for n in [1, 1, 3, 1, 9, 1, 1, 30, 1, 2] + [1] * 20:
+        new = torch.randint(1, model.config.vocab_size, (3, n), generator=gen)
+        mask = torch.cat([mask, torch.ones(3, n, dtype=torch.long)], dim=1)
+        with torch.no_grad(), pc.packed_attention(model):
+            lo = model(new, past_key_values=ours, **kw(n)).logits
+        with torch.no_grad():
+            out = _ref_step_kw(new, n)
+        ref.add_tokens(out.past_key_values)
+        err = ((lo - out.logits).abs().max() / out.logits.abs().max()).item()
+        worst = max(worst, err)
+        assert err <= 1e-3, (n, err)
+        for lay in ours.layers:
+            lay.settle()
+        assert ours.store(0).quantized_tokens == ref.get_stats(0)["quantized_tokens"]
+    print(f"[packed-padded] worst logits rel err {worst:.2e}", flush=True)
+    assert ours.total_flushes == ref.total_flushes > 0

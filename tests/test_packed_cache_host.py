@@ -168,9 +168,9 @@ def test_unsupported_inputs_raise(cpu_store):
     cache = pc.KiviPackedCache.from_model(model, group_size=32, residual_length=32)
     with torch.no_grad(), pc.packed_attention(model):
         model(torch.tensor([[1, 2, 3]]), past_key_values=cache, use_cache=True)
-        with pytest.raises(NotImplementedError, match="padded"):
+        with pytest.raises(NotImplementedError, match="left-padded"):
             model(torch.tensor([[4, 5]]), past_key_values=cache, use_cache=True,
-                  attention_mask=torch.tensor([[0, 1, 1, 1, 1]]))
+                  attention_mask=torch.tensor([[1, 0, 1, 1, 1]]))     # a hole, not padding
     with torch.no_grad(), pc.packed_attention(model):
         with pytest.raises(RuntimeError, match="KiviPackedCache"):
             model(torch.tensor([[1, 2, 3]]), use_cache=False)
@@ -360,3 +360,56 @@ def test_hf_assisted_generation(cpu_store):
         assert cache.get_seq_length() == ids.shape[1] + 59
     assert max(sizes[1:]) > 2 and any(c < 0 for c in crops)
     assert torch.equal(outs[0], outs[1])
+
+
+def _padded_batch(vocab, lengths, gen):
+    """Left-padded prompts: ids [B, T] (pad id 0), attention mask, positions
+    as transformers' generate() makes them (cumsum of the mask - 1)."""
+    T = max(lengths)
+    ids = torch.zeros(len(lengths), T, dtype=torch.long)
+    mask = torch.zeros(len(lengths), T, dtype=torch.long)
+    for b, n in enumerate(lengths):
+        ids[b, T - n:] = torch.randint(1, vocab, (n,), generator=gen)
+        mask[b, T - n:] = 1
+    return ids, mask
+
+
+def _positions(mask, n):
+    pos = mask.cumsum(-1) - 1
+    return pos.clamp(min=0)[:, -n:]
+
+
+@pytest.mark.parametrize("steps", [[1] * 40, [1, 3, 1, 1, 9, 1, 2, 1, 1, 1, 30, 1]])
+def test_left_padded_batch_follows_reference_flow(cpu_store, steps):
+    """A left-padded batch (prompts of 50, 37 and 12 tokens): every forward
+    after the prompt hides each sequence's pad positions through HF's
+    boolean mask, which the packed attention turns into a per-sequence first
+    visible position.  Logits equal the reference flow's (HF SDPA with the
+    same mask over get_full_cache()) to float rounding, and layer 0's store
+    (pad tokens included, as the reference's add_tokens stores them) bit for
+    bit, over one-token and multi-token steps across several flushes."""
+    model = _gpt2(3, 4, 128, seed=21)
+    G, R = 32, 64
+    ours = pc.KiviPackedCache.from_model(model, group_size=G, residual_length=R)
+    ref = _OracleShim.from_model(model, group_size=G, residual_length=R)
+    gen = torch.Generator().manual_seed(22)
+    ids, mask = _padded_batch(model.config.vocab_size, [50, 37, 12], gen)
+    kw = dict(attention_mask=mask, position_ids=_positions(mask, ids.shape[1]), use_cache=True)
+    with torch.no_grad(), pc.packed_attention(model):
+        lo = model(ids, past_key_values=ours, **kw).logits
+    with torch.no_grad():
+        out = model(ids, **kw)
+    ref.add_tokens(out.past_key_values)
+    torch.testing.assert_close(lo, out.logits, rtol=1e-5, atol=1e-5)
+    for n in steps:
+        new = torch.randint(1, model.config.vocab_size, (3, n), generator=gen)
+        mask = torch.cat([mask, torch.ones(3, n, dtype=torch.long)], dim=1)
+        kw = dict(attention_mask=mask, position_ids=_positions(mask, n), use_cache=True)
+        with torch.no_grad(), pc.packed_attention(model):
+            lo = model(new, past_key_values=ours, **kw).logits
+        with torch.no_grad():
+            out = model(new, past_key_values=ref.get_full_cache(), **kw)
+        ref.add_tokens(out.past_key_values)
+        torch.testing.assert_close(lo, out.logits, rtol=1e-4, atol=1e-4)
+        _check_layer0(ours, ref)
+    assert ours.total_flushes == ref.total_flushes > 0
