@@ -113,10 +113,10 @@ def make_store(k, v, G, Gv, R, device, extra_chunks=16):
     return st
 
 
-def settle_clocks(fn, seconds=0.05, min_calls=20):
+def settle_clocks(fn, seconds=0.1, min_calls=20):
     """Runs fn back to back for ~`seconds` of GPU time (untimed).  From idle,
-    MI355X clocks take tens of milliseconds to ramp up: timing without this
-    reports the first calls ~20% slow."""
+    MI355X clocks take tens of milliseconds to ramp up (and dip once on the
+    way): timing without this reports the first calls ~20% slow."""
     import torch
     t0 = time.perf_counter()
     n = 0
@@ -484,7 +484,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--attn-iters", type=int, default=50)
+    ap.add_argument("--attn-iters", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 counter passes behind roofline.traffic")

@@ -158,3 +158,18 @@ def test_prompt_on_rounding_ties(store_cls, dtype, B, H, D, G, Gv, R, T):
     st = store_cls(B, H, D, G, R, "cuda:0", group_size_v=Gv, keep_history=True)
     st.extend(k.to("cuda:0", dtype), v.to("cuda:0", dtype), flush_at=R)
     check_store_bit_exact(st, k, v)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_prompt_with_huge_ranges(store_cls, dtype):
+    """Groups whose scale exceeds 2^120 (values near 1e37, where the divide-
+    free exact quotient's argument does not hold) take the correctly rounded
+    divide for their tensor; every code, scale and zero stays bit-exact."""
+    B, H, D, G, Gv, R, T = 2, 2, 128, 32, 32, 128, 300
+    k, v = make_kv(B, H, T, D, seed=77)
+    k[0, 1, :, 9] *= 3e36            # one key channel of every chunk
+    v[1, 0, 40:45, :] *= 3e36        # the value groups of five tokens
+    k, v = k.to(dtype).float(), v.to(dtype).float()
+    st = store_cls(B, H, D, G, R, "cuda:0", group_size_v=Gv, keep_history=True)
+    st.extend(k.to("cuda:0", dtype), v.to("cuda:0", dtype), flush_at=R)
+    check_store_bit_exact(st, k, v)
