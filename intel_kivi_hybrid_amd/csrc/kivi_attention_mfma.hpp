@@ -368,13 +368,41 @@ struct ChunkSrc {
     int meta_stride[S::NMETA];    // float4s per chunk
 };
 
+// Paired metadata sweep (PAIRED): the first NMETA/2 float4s of a lane are
+// scales, from [ks | vs], and the last NMETA/2 the zeros of the same
+// channels or tokens, from [kz | vz], so that the lane can stage
+// zero - 8*scale (the correction terms' factor) in place of the zero.  Used
+// where it needs no more loads per lane than the plain sweep.
 template <class S>
+constexpr bool paired_meta(int NG) {
+    return NG > 0 && 2 * ((S::D / 4 + NG * S::G / 4 + 63) / 64) <= S::NMETA && S::NMETA % 2 == 0;
+}
+
+template <class S, bool PAIRED>
 __device__ __forceinline__ ChunkSrc<S> chunk_src(const AttnLaunch& a, int64_t cid0, int lane,
                                                  int NG) {
     ChunkSrc<S> c;
     c.kc = reinterpret_cast<const uint32_t*>(a.k_codes) + cid0 * (64 * S::NP) + lane * S::NP;
     c.vc = reinterpret_cast<const uint32_t*>(a.v_codes) + cid0 * (64 * S::NP) + lane * S::NP;
     const int kq = S::D / 4, vq = NG * S::G / 4;
+    if constexpr (PAIRED) {
+        constexpr int HALF = S::NMETA / 2;
+#pragma unroll
+        for (int i = 0; i < HALF; ++i) {
+            const int e = min(lane + 64 * i, kq + vq - 1);     // past the end: reload the last
+            if (e < kq) {
+                c.meta[i] = reinterpret_cast<const float4*>(a.k_scale + cid0 * S::D) + e;
+                c.meta[i + HALF] = reinterpret_cast<const float4*>(a.k_zero + cid0 * S::D) + e;
+                c.meta_stride[i] = c.meta_stride[i + HALF] = kq;
+            } else {
+                c.meta[i] = reinterpret_cast<const float4*>(a.v_scale + cid0 * NG * S::G) + (e - kq);
+                c.meta[i + HALF] = reinterpret_cast<const float4*>(a.v_zero + cid0 * NG * S::G) +
+                                   (e - kq);
+                c.meta_stride[i] = c.meta_stride[i + HALF] = vq;
+            }
+        }
+        return c;
+    }
 #pragma unroll
     for (int i = 0; i < S::NMETA; ++i) {
         // Lanes past the end reload the last float4 (never stored), so every
@@ -412,14 +440,52 @@ __device__ __forceinline__ void load_chunk(ChunkRegs<S>& r, const ChunkSrc<S>& s
     for (int i = 0; i < S::NMETA; ++i) r.meta[i] = src.meta[i][(int64_t)c * src.meta_stride[i]];
 }
 
+// LDS float4 slots where a paired lane stages its i-th scale and zero float4
+// ([ks | kz | vs | vz] order, meta_slot spacing), or -1 past the end.
+// Fixed per wave: computed once.
 template <class S>
+struct PairSlots {
+    int sc[S::NMETA / 2 > 0 ? S::NMETA / 2 : 1], zr[S::NMETA / 2 > 0 ? S::NMETA / 2 : 1];
+};
+template <class S>
+__device__ __forceinline__ PairSlots<S> pair_slots(int lane, int NG) {
+    PairSlots<S> p;
+    const int kq = S::D / 4, vq = NG * S::G / 4;
+#pragma unroll
+    for (int i = 0; i < S::NMETA / 2; ++i) {
+        const int e = lane + 64 * i;
+        const bool key = e < kq;
+        p.sc[i] = e < kq + vq ? S::meta_slot(key ? e : kq + e) : -1;
+        p.zr[i] = e < kq + vq ? S::meta_slot(key ? kq + e : kq + vq + e) : -1;
+    }
+    return p;
+}
+
+// Stages a chunk's metadata in LDS as [ks | kz | vs | vz] float4 slots
+// (meta_slot).  PAIRED: the zero slots receive zero - 8*scale instead.
+template <class S, bool PAIRED>
 __device__ __forceinline__ void stage_meta(const ChunkRegs<S>& r, float* MT, int lane, int NG,
-                                           int meta_floats) {
+                                           int meta_floats, const PairSlots<S>& ps) {
+    float4* mt = reinterpret_cast<float4*>(MT);
+    if constexpr (PAIRED) {
+        constexpr int HALF = S::NMETA / 2;
+#pragma unroll
+        for (int i = 0; i < HALF; ++i) {
+            const float4 sc = r.meta[i], z = r.meta[i + HALF];
+            const float4 u = make_float4(fmaf(-8.f, sc.x, z.x), fmaf(-8.f, sc.y, z.y),
+                                         fmaf(-8.f, sc.z, z.z), fmaf(-8.f, sc.w, z.w));
+            if (ps.sc[i] >= 0) {
+                mt[ps.sc[i]] = sc;
+                mt[ps.zr[i]] = u;
+            }
+        }
+        return;
+    }
     const int n4 = meta_floats / 4;
 #pragma unroll
     for (int i = 0; i < S::NMETA; ++i) {
         const int e = lane + 64 * i;
-        if (e < n4) reinterpret_cast<float4*>(MT)[S::meta_slot(e)] = r.meta[i];
+        if (e < n4) mt[S::meta_slot(e)] = r.meta[i];
     }
 }
 
@@ -436,6 +502,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     const int lane = threadIdx.x % kWave;
     const int NG = NGC > 0 ? NGC : D / a.Gv;
     const int Gv = NGC > 0 ? D / NGC : a.Gv;
+    constexpr bool PAIRED = paired_meta<S>(NGC);
     const int64_t bh = (int64_t)b * a.Hkv + kvh;
     // Left padding: context positions before kv_lo take no weight (0: none).
     const int kv_lo = __builtin_amdgcn_readfirstlane(a.kv_start ? a.kv_start[b] : 0);
@@ -543,7 +610,8 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     constexpr int PF = S::PF;
     ChunkRegs<S> buf[PF];
     int cid[PF];     // the chunk in each ring slot; -1 past the end (its load re-reads c_last)
-    const ChunkSrc<S> src = chunk_src<S>(a, bh * a.Cmax, lane, NG);
+    const ChunkSrc<S> src = chunk_src<S, PAIRED>(a, bh * a.Cmax, lane, NG);
+    const PairSlots<S> pslots = pair_slots<S>(lane, NG);
     // (the launch gives every workgroup at least one chunk, so c_last is a
     // valid chunk and these loads need no branch: a branch here would make the
     // compiler wait for them before the query's LDS stores)
@@ -620,8 +688,10 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
 #pragma unroll
         for (int j = 0; j < S::CPL / 2; ++j) {
             split_pair(qv[2 * j] * ks[2 * j], qv[2 * j + 1] * ks[2 * j + 1], hi[j], lo[j]);
-            corr = fmaf(qv[2 * j], fmaf(-8.f, ks[2 * j], kz[2 * j]), corr);
-            corr = fmaf(qv[2 * j + 1], fmaf(-8.f, ks[2 * j + 1], kz[2 * j + 1]), corr);
+            // (PAIRED: the kz slots hold kz - 8 ks already)
+            corr = fmaf(qv[2 * j], PAIRED ? kz[2 * j] : fmaf(-8.f, ks[2 * j], kz[2 * j]), corr);
+            corr = fmaf(qv[2 * j + 1],
+                        PAIRED ? kz[2 * j + 1] : fmaf(-8.f, ks[2 * j + 1], kz[2 * j + 1]), corr);
         }
         uint16_t* rhi = WA + (2 * wh) * S::WA_ROW + wseg * S::CPL;
         uint16_t* rlo = rhi + S::WA_ROW;
@@ -807,7 +877,8 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                 }
                 float acc = vb[it];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc = fmaf(p[j], fmaf(-8.f, vs[j], vz[j]), acc);
+                for (int j = 0; j < 8; ++j)
+                    acc = fmaf(p[j], PAIRED ? vz[j] : fmaf(-8.f, vs[j], vz[j]), acc);
                 vb[it] = acc;
                 uint16_t* base = PA + it_pa[it];
                 *reinterpret_cast<u32x4_t*>(base) = hi;
@@ -990,7 +1061,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // chunk, so no load is inside a branch and the compiler waits only for
     // the chunk about to be used).
     if (cid[0] >= 0) {
-        stage_meta<S>(buf[0], MT, lane, NG, meta_floats);
+        stage_meta<S, PAIRED>(buf[0], MT, lane, NG, meta_floats, pslots);
         wave_sync();
         wprep(Int<0>{});
         wave_sync();
@@ -1002,7 +1073,8 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     auto step = [&](const ChunkRegs<S>& cur, const ChunkRegs<S>& nxt, bool has_next, auto slot_c,
                     int nxt_chunk) {
         constexpr int slot = decltype(slot_c)::value, nslot = slot ^ 1;
-        if (has_next) stage_meta<S>(nxt, MT + nslot * meta_stride, lane, NG, meta_floats);
+        if (has_next)
+            stage_meta<S, PAIRED>(nxt, MT + nslot * meta_stride, lane, NG, meta_floats, pslots);
         wave_sync();
         if (has_next) wprep(Int<nslot>{});
         pprep(Int<slot>{}, any_cur);
