@@ -85,14 +85,34 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// The bf16 pairs (-1, 0) and (0, -1), held in VGPRs: split_pair's v_dot2
+// reads them as register operands.  (As literals, the compiler's encoding of
+// the (-1, 0) pair made the instruction read the pair's high half -- measured
+// on gfx950 -- so the values are hidden from it.)
+struct SplitConsts {
+    uint32_t neg_x, neg_y;
+};
+__device__ __forceinline__ SplitConsts split_consts() {
+    SplitConsts c{0x0000bf80u, 0xbf800000u};
+    asm("" : "+v"(c.neg_x));
+    asm("" : "+v"(c.neg_y));
+    return c;
+}
+
 // (a, b) -> hi and lo bf16 pairs with a ~ hi.x + lo.x, b ~ hi.y + lo.y.
-__device__ __forceinline__ void split_pair(float a, float b, uint32_t& hi, uint32_t& lo) {
+// a - hi.x is exact in fp32 (hi.x is a rounded to 8 significant bits), so
+// one v_dot2_f32_bf16 of hi with (-1, 0) accumulated onto a forms it: two
+// ops instead of widening hi's halves and subtracting (bit-identical over
+// 8.4 M random pairs on gfx950, tiny normals included).
+__device__ __forceinline__ void split_pair(float a, float b, uint32_t& hi, uint32_t& lo,
+                                           SplitConsts k) {
     hi = pack_bf16x2(a, b);
-    // hi << 16 as a byte permute: LLVM rewrites a plain shift of the packed
-    // pair into a second conversion of a alone plus the shift.
-    const float ha = __builtin_bit_cast(float, __builtin_amdgcn_perm(0u, hi, 0x01000c0cu));
-    const float hb = __builtin_bit_cast(float, hi & 0xffff0000u);
-    lo = pack_bf16x2(a - ha, b - hb);
+    const bf16x2_t h2 = __builtin_bit_cast(bf16x2_t, hi);
+    const float la = __builtin_amdgcn_fdot2_f32_bf16(h2, __builtin_bit_cast(bf16x2_t, k.neg_x), a,
+                                                     false);
+    const float lb = __builtin_amdgcn_fdot2_f32_bf16(h2, __builtin_bit_cast(bf16x2_t, k.neg_y), b,
+                                                     false);
+    lo = pack_bf16x2(la, lb);
 }
 
 // (x & mask) | base.  With both constants opaque (read through
@@ -650,6 +670,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     const int n_items = HG * NSEG * NG;
 
     const UnpackConsts uc = unpack_consts();
+    const SplitConsts spc = split_consts();
     const bf16x8_t ones = __builtin_bit_cast(
         bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
 
@@ -687,7 +708,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         float corr = 0.f;
 #pragma unroll
         for (int j = 0; j < S::CPL / 2; ++j) {
-            split_pair(qv[2 * j] * ks[2 * j], qv[2 * j + 1] * ks[2 * j + 1], hi[j], lo[j]);
+            split_pair(qv[2 * j] * ks[2 * j], qv[2 * j + 1] * ks[2 * j + 1], hi[j], lo[j], spc);
             // (PAIRED: the kz slots hold kz - 8 ks already)
             corr = fmaf(qv[2 * j], PAIRED ? kz[2 * j] : fmaf(-8.f, ks[2 * j], kz[2 * j]), corr);
             corr = fmaf(qv[2 * j + 1],
@@ -711,7 +732,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             }
         }
         uint32_t chi, clo;
-        split_pair(corr, 0.f, chi, clo);
+        split_pair(corr, 0.f, chi, clo, spc);
         BA[(2 * wh) * S::BA_ROW + wseg] = (uint16_t)chi;
         BA[(2 * wh + 1) * S::BA_ROW + wseg] = (uint16_t)clo;
     };
@@ -871,7 +892,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     uint32_t h2, l2;
-                    split_pair(p[2 * j] * vs[2 * j], p[2 * j + 1] * vs[2 * j + 1], h2, l2);
+                    split_pair(p[2 * j] * vs[2 * j], p[2 * j + 1] * vs[2 * j + 1], h2, l2, spc);
                     hi[j] = h2;
                     lo[j] = l2;
                 }
