@@ -324,7 +324,11 @@ __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
                   GV % 32 == 0, "flush_fast shape");
     __shared__ __align__(16) float tile[G * LD];
     __shared__ __align__(16) float kpar[3][D];          // min, scale, 1/scale per channel
-    __shared__ __align__(16) float4 vpar[G * NG];       // (min, scale, 1/scale, -) per group
+    // (min, scale, 1/scale, -) per value group, token-major with one pad
+    // float4 after every 8 tokens: the code pass's lanes read 4 token rows 8
+    // apart at once, which then fall in distinct banks.
+    __shared__ __align__(16) float4 vpar[G * NG + G / 8];
+    auto vpi = [](int t, int g) { return t * NG + g + t / 8; };
     __shared__ float part[2][NSK][D];
 
     const int tid = threadIdx.x;
@@ -492,7 +496,7 @@ __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
             if (sg == 0) {
                 a.v_scale[(chunk_id * NG + gi) * G + t] = scale;
                 a.v_zero[(chunk_id * NG + gi) * G + t] = mn;
-                vpar[t * NG + gi] = make_float4(mn, scale, crcp_or_nan(scale), 0.0f);
+                vpar[vpi(t, gi)] = make_float4(mn, scale, crcp_or_nan(scale), 0.0f);
             }
         }
         lds_barrier();
@@ -513,7 +517,7 @@ __global__ __launch_bounds__(kFlushBlock) void flush_fast_kernel(FlushArgs a) {
 #pragma unroll
                     for (int jj = 0; jj < 8; ++jj) {
                         x[jj] = tile[vat(t0 + jj, c)];
-                        par[jj] = vpar[(t0 + jj) * NG + c / GV];
+                        par[jj] = vpar[vpi(t0 + jj, c / GV)];
                     }
                     uint32_t q[8];
 #pragma unroll
