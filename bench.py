@@ -151,11 +151,19 @@ def time_calls(fn, iters, blocks=5):
     return {"avg_us": 1e3 * sum(ms) / len(ms), "median_us": 1e3 * ms[len(ms) // 2]}
 
 
-def time_attention(st, q, iters):
-    """One fused-attention call over the store as it stands."""
+def time_attention(st, q, iters, rotate=None):
+    """One fused-attention call over the store as it stands.  ``rotate``: more
+    stores of the same shape, called in turn with ``st`` so that the bytes
+    touched between two calls on one store exceed the 256 MB MALL."""
     import torch
     out = torch.empty_like(q)
-    r = time_calls(lambda: st.attention(q, out=out), iters)
+    stores = [st] + list(rotate or [])
+    turn = [0]
+
+    def call():
+        stores[turn[0]].attention(q, out=out)
+        turn[0] = (turn[0] + 1) % len(stores)
+    r = time_calls(call, iters)
     Hq = q.shape[1]
     nbytes = attn_bytes(st.B, Hq, st.H, st.D, st.quantized_tokens, st.res_len, st.G, st.Gv)
     ws = st.workspace_bytes(Hq)
@@ -570,28 +578,39 @@ def main():
         # ---- config 3: MHA, 4096 quantised + 128 residual tokens -----------
         B3, H3, D3, R3, G3 = 16, 32, 128, 128, 32
         k, v = synth_kv(B3, H3, 4096 + R3, D3, 1234 + 3)
-        st = make_store(k[:, :, :4096 + R3 - 1], v[:, :, :4096 + R3 - 1], G3, G3, R3, dev)
-        st.append(k[:, :, -1:].to(dev), v[:, :, -1:].to(dev))
+        # two copies of the 336 MB store, called in turn (> 512 MB between
+        # two reads of one copy, so the MALL cannot serve them)
+        sts = []
+        for _ in range(2):
+            s3 = make_store(k[:, :, :4096 + R3 - 1], v[:, :, :4096 + R3 - 1], G3, G3, R3, dev)
+            s3.append(k[:, :, -1:].to(dev), v[:, :, -1:].to(dev))
+            sts.append(s3)
         del k, v
         q = (torch.randn(B3, H3, D3, generator=torch.Generator().manual_seed(6))
              * D3 ** -0.5).to(dev)
-        a3 = time_attention(st, q, args.attn_iters)
+        a3 = time_attention(sts[0], q, args.attn_iters, rotate=sts[1:])
         log(f"[bench] config3 attention: {a3['avg_us']:.1f} us, {a3['gbs']:.0f} GB/s "
-            f"(Tq={a3['Tq']}, Tr={a3['Tr']})")
+            f"(Tq={a3['Tq']}, Tr={a3['Tr']}; two stores in turn)")
         extra["attention_config3"] = {k_: a3[k_] for k_ in ("avg_us", "gbs", "Tq", "Tr", "splits")}
-        del st
+        del sts
         torch.cuda.empty_cache()
 
     if only in (None, "config5"):
         # ---- config 5: 131072 quantised tokens, Gv=128, split-K + merge ----
         B5, Hq5, H5, D5, R5, G5, Gv5 = 4, 32, 8, 128, 128, 32, 128
         k, v = synth_kv(B5, H5, 131072 + R5, D5, 1234 + 5)
-        st = make_store(k[:, :, :131072 + R5 - 1], v[:, :, :131072 + R5 - 1], G5, Gv5, R5, dev)
-        st.append(k[:, :, -1:].to(dev), v[:, :, -1:].to(dev))
+        # two copies of the 441 MB store, called in turn (see config 3)
+        sts = []
+        for _ in range(2):
+            s5 = make_store(k[:, :, :131072 + R5 - 1], v[:, :, :131072 + R5 - 1], G5, Gv5, R5,
+                            dev)
+            s5.append(k[:, :, -1:].to(dev), v[:, :, -1:].to(dev))
+            sts.append(s5)
+        st = sts[0]
         del k, v
         q = (torch.randn(B5, Hq5, D5, generator=torch.Generator().manual_seed(7))
              * D5 ** -0.5).to(dev)
-        a5 = time_attention(st, q, args.attn_iters)
+        a5 = time_attention(st, q, args.attn_iters, rotate=sts[1:])
         f5 = time_flush(st)
         step_us = a5["avg_us"] + f5["avg_us"]
         log(f"[bench] config5 attention: {a5['avg_us']:.1f} us, {a5['gbs']:.0f} GB/s "
@@ -601,7 +620,7 @@ def main():
         extra["attention_config5"].update({
             "flush_us": round(f5["avg_us"], 2), "step_us": round(step_us, 2),
             "step_gbs": round((a5["bytes"] + f5["bytes"]) / (step_us * 1e-6) / 1e9, 1)})
-        del st
+        del st, sts
         torch.cuda.empty_cache()
 
     qb = None
