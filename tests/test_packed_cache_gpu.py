@@ -333,3 +333,47 @@ def test_left_padded_batch_follows_reference_flow(hip_device):
         assert ours.store(0).quantized_tokens == ref.get_stats(0)["quantized_tokens"]
     print(f"[packed-padded] worst logits rel err {worst:.2e}", flush=True)
     assert ours.total_flushes == ref.total_flushes > 0
+
+
+def test_hf_generate_left_padded_batch(hip_device):
+    """transformers' generate() on a left-padded batch (prompts of 23 and 9
+    tokens) with the packed cache on the GPU picks the tokens of a greedy loop
+    over the reference flow with the same masks and positions (model on the
+    CPU in both arms)."""
+    from transformers import GPT2Config, GPT2LMHeadModel
+    torch.manual_seed(31)
+    model = GPT2LMHeadModel(GPT2Config(n_layer=4, n_head=4, n_embd=256)).eval()
+    G, R = 32, 32
+    gen = torch.Generator().manual_seed(32)
+    lengths, T = [23, 9], 23
+    ids = torch.zeros(2, T, dtype=torch.long)
+    mask = torch.zeros(2, T, dtype=torch.long)
+    for b, n in enumerate(lengths):
+        ids[b, T - n:] = torch.randint(1, model.config.vocab_size, (n,), generator=gen)
+        mask[b, T - n:] = 1
+    new_tokens = 60
+    cache = pc.KiviPackedCache.from_model(model, device="cuda:0", group_size=G,
+                                          residual_length=R)
+    with pc.packed_attention(model):
+        hf = model.generate(ids, attention_mask=mask, past_key_values=cache,
+                            max_new_tokens=new_tokens, do_sample=False, pad_token_id=0)
+    ref = _OracleShim.from_model(model, group_size=G, residual_length=R)
+
+    def kw(m, n):
+        return dict(attention_mask=m, position_ids=(m.cumsum(-1) - 1).clamp(min=0)[:, -n:],
+                    use_cache=True)
+    with torch.no_grad():
+        out = model(ids, **kw(mask, T))
+    ref.add_tokens(out.past_key_values)
+    toks = [out.logits[:, -1:].argmax(-1)]
+    for _ in range(new_tokens - 1):
+        mask = torch.cat([mask, torch.ones(2, 1, dtype=torch.long)], dim=1)
+        with torch.no_grad():
+            out = model(toks[-1], past_key_values=ref.get_full_cache(), **kw(mask, 1))
+        ref.add_tokens(out.past_key_values)
+        toks.append(out.logits[:, -1:].argmax(-1))
+    ours = hf[:, T:]
+    want = torch.cat(toks, dim=1)
+    n, tot = _match(ours.reshape(-1).tolist(), want.reshape(-1).tolist())
+    print(f"[packed-padded-generate] token match {n}/{tot}", flush=True)
+    assert torch.equal(ours, want)

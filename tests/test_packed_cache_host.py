@@ -413,3 +413,34 @@ def test_left_padded_batch_follows_reference_flow(cpu_store, steps):
         torch.testing.assert_close(lo, out.logits, rtol=1e-4, atol=1e-4)
         _check_layer0(ours, ref)
     assert ours.total_flushes == ref.total_flushes > 0
+
+
+def test_hf_generate_left_padded_batch(cpu_store):
+    """transformers' generate() on a left-padded batch of prompts drives the
+    packed cache (padding mask on every step) to the tokens of a greedy loop
+    over the reference flow with the same masks and positions."""
+    model = _gpt2(3, 4, 128, seed=31)
+    G, R = 32, 32
+    gen = torch.Generator().manual_seed(32)
+    ids, mask = _padded_batch(model.config.vocab_size, [23, 9], gen)
+    new_tokens = 40
+    cache = pc.KiviPackedCache.from_model(model, group_size=G, residual_length=R)
+    with pc.packed_attention(model):
+        hf = model.generate(ids, attention_mask=mask, past_key_values=cache,
+                            max_new_tokens=new_tokens, do_sample=False, pad_token_id=0)
+    # the reference flow, step by step
+    ref = _OracleShim.from_model(model, group_size=G, residual_length=R)
+    kw = dict(attention_mask=mask, position_ids=_positions(mask, ids.shape[1]), use_cache=True)
+    with torch.no_grad():
+        out = model(ids, **kw)
+    ref.add_tokens(out.past_key_values)
+    toks = [out.logits[:, -1:].argmax(-1)]
+    for _ in range(new_tokens - 1):
+        mask = torch.cat([mask, torch.ones(2, 1, dtype=torch.long)], dim=1)
+        kw = dict(attention_mask=mask, position_ids=_positions(mask, 1), use_cache=True)
+        with torch.no_grad():
+            out = model(toks[-1], past_key_values=ref.get_full_cache(), **kw)
+        ref.add_tokens(out.past_key_values)
+        toks.append(out.logits[:, -1:].argmax(-1))
+    assert torch.equal(hf[:, ids.shape[1]:], torch.cat(toks, dim=1))
+    assert cache.total_flushes == ref.total_flushes > 0
