@@ -1223,16 +1223,19 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     merge_and_store<HG, D>(smem, rstate, a, split, kvh, b);
 }
 
-// Occupancy target: four waves per SIMD for head_dim 64 with G=32 and up to 4
-// query heads per kv head (the kernel fits 128 VGPRs there without spilling;
-// left to itself the compiler's choice lands on either side of 128 as
-// unrelated code changes); two where the 4-deep prefetch ring fits that
+// Occupancy target: four waves per SIMD for head_dim 64 with G=32 and up to
+// 2 query heads per kv head (128 VGPRs; the few bytes the compiler spills
+// there are reloaded outside the chunk loop), three with 4 query heads per kv
+// head (at four, spills landed in the chunk loop: 85 us against 70 us at
+// B=64, 32/8 heads, 8K context); two where the 4-deep prefetch ring fits that
 // register budget without spilling (head_dim 64, or head_dim 128 with up to
 // 4 query heads per kv head), which measured faster than three waves with a
 // 2-deep ring.  Larger shapes keep the full register file (one wave per SIMD).
 template <int HG, int D, int G>
 constexpr int attn_waves_per_eu() {
-    return (D <= 64 && G <= 32 && HG <= 4) ? 4 : (D <= 64 || (D <= 128 && HG <= 4)) ? 2 : 1;
+    return (D <= 64 && G <= 32 && HG <= 2) ? 4
+           : (D <= 64 && G <= 32 && HG <= 4) ? 3
+           : (D <= 64 || (D <= 128 && HG <= 4)) ? 2 : 1;
 }
 
 template <int HG, int D, int G, int NGC, bool R16>
