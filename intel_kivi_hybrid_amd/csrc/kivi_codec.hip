@@ -143,7 +143,7 @@ __global__ __launch_bounds__(kBlock) void roundtrip_seg_kernel(
         seg_min_max<LANES>(mn, mx);
         finish_group(mn, mx, scale);
         const uint32_t byte = encode4(v[u].x, v[u].y, v[u].z, v[u].w, mn, scale);
-        if (idx < n_vec) out[idx] = decode4(byte, scale, mn);
+        if (idx < n_vec) store_stream(out + idx, decode4(byte, scale, mn));
     }
 }
 
@@ -219,12 +219,12 @@ __global__ __launch_bounds__(kBlock) void dequantize_kernel(
         const int64_t g = BPG ? (idx / BPG) : (idx / bpg);
         const float4 d = decode4(b[u], scales[g], zeros[g]);
         if constexpr (kAligned) {
-            reinterpret_cast<float4*>(out)[idx] = d;
+            store_stream(reinterpret_cast<float4*>(out) + idx, d);
         } else {
-            out[4 * idx] = d.x;
-            out[4 * idx + 1] = d.y;
-            out[4 * idx + 2] = d.z;
-            out[4 * idx + 3] = d.w;
+            store_stream(out + 4 * idx, d.x);
+            store_stream(out + 4 * idx + 1, d.y);
+            store_stream(out + 4 * idx + 2, d.z);
+            store_stream(out + 4 * idx + 3, d.w);
         }
     }
 }

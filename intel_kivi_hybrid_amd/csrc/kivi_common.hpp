@@ -19,6 +19,10 @@ namespace kivi {
 
 constexpr int kWave = 64;
 
+// Clang vector types for nontemporal loads and stores of 16 and 8 bytes.
+typedef float kivi_f4v __attribute__((ext_vector_type(4)));
+typedef unsigned int kivi_u2v __attribute__((ext_vector_type(2)));
+
 // ---------------------------------------------------------------------------
 // Host-side status plumbing (defined in kivi_runtime.hip).
 // ---------------------------------------------------------------------------
@@ -204,13 +208,20 @@ __device__ __forceinline__ float widen(const void* p, int64_t i) {
 }
 
 // Elements i..i+3 widened to fp32 with one 16-byte (fp32) or 8-byte (16-bit)
-// load: the offset must be aligned to that size.
+// load: the offset must be aligned to that size.  The load is nontemporal: its
+// callers (the flush reading K/V, the ring and new-token reads) stream data
+// they read once, and keeping it out of L2 and the MALL measured 5-10 % faster
+// for the batched prefill flush.
 template <int SRC>
 __device__ __forceinline__ float4 load4_vec(const void* p, int64_t i) {
     if constexpr (SRC == kSrcF32) {
-        return *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+        const kivi_f4v x = __builtin_nontemporal_load(
+            reinterpret_cast<const kivi_f4v*>(static_cast<const float*>(p) + i));
+        return make_float4(x.x, x.y, x.z, x.w);
     } else {
-        const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+        const kivi_u2v w = __builtin_nontemporal_load(
+            reinterpret_cast<const kivi_u2v*>(static_cast<const uint16_t*>(p) + i));
+        const uint2 u = make_uint2(w.x, w.y);
         if constexpr (SRC == kSrcBF16) {
             return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u),
                                __uint_as_float(u.y << 16), __uint_as_float(u.y & 0xffff0000u));
@@ -267,6 +278,18 @@ __device__ __forceinline__ float4 decode4(uint32_t byte, float scale, float zero
     o.z = decode1((byte >> 4) & 3u, scale, zero);
     o.w = decode1((byte >> 6) & 3u, scale, zero);
     return o;
+}
+
+// Streaming (nontemporal) stores for outputs written once and not read back
+// by the same kernel: the lines go to HBM without being kept in L2 and the
+// MALL.  For a write-dominated stream (dequantise writes 16 bytes per code
+// byte read) this is the difference between ~4.8 and ~6.7 TB/s on MI355X.
+__device__ __forceinline__ void store_stream(float4* p, const float4& v) {
+    const kivi_f4v x = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(x, reinterpret_cast<kivi_f4v*>(p));
+}
+__device__ __forceinline__ void store_stream(float* p, float v) {
+    __builtin_nontemporal_store(v, p);
 }
 
 // Workgroup barrier that orders LDS accesses only.  __syncthreads() also
