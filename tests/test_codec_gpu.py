@@ -231,3 +231,31 @@ def test_async_ops_and_event(C):
     assert torch.equal(vo, vf)
     assert np.array_equal(_bits(vf).reshape(-1),
                           codec.roundtrip_groups(v.cpu().numpy(), 32).view(np.uint32))
+
+
+def test_event_recorded_at_first_use(C):
+    """An async op's event is recorded at its first wait()/query(), after
+    the op on its stream: waiting then covers the op (and any work queued
+    behind it), repeated calls return at once, and results are exact."""
+    import time
+    x = seeded_kv((4, 8, 128, 256), seed=23, kind="key")
+    xd = x.cuda()
+    n = xd.numel()
+    packed = torch.empty(n // 4, dtype=torch.uint8, device="cuda:0")
+    scales = torch.empty(n // 32, device="cuda:0")
+    zeros = torch.empty(n // 32, device="cuda:0")
+    ev = C.quantize_keys_async(xd, packed, scales, zeros, 32)
+    assert ev._ev is None                      # no marker put on the stream yet
+    out = torch.empty_like(xd)
+    ev2 = C.dequantize_keys_async(packed, scales, zeros, out, 32)   # queued behind it
+    ev.wait()
+    assert ev.query() and ev._ev is None       # released after the wait
+    ev.wait()                                  # a second wait returns at once
+    op, os_, oz = codec.quantize_groups(x.numpy(), 32)
+    assert np.array_equal(packed.cpu().numpy(), op)
+    deadline = time.monotonic() + 30.0
+    while not ev2.query():
+        assert time.monotonic() < deadline, "dequantize never completed"
+    ev2.wait()
+    ref = codec.dequantize_groups(op, os_, oz, 32).reshape(x.shape)
+    assert np.array_equal(_bits(out.cpu()).reshape(-1), ref.view(np.uint32).reshape(-1))
