@@ -291,6 +291,9 @@ __device__ __forceinline__ void store_stream(float4* p, const float4& v) {
 __device__ __forceinline__ void store_stream(float* p, float v) {
     __builtin_nontemporal_store(v, p);
 }
+__device__ __forceinline__ void store_stream(uint32_t* p, uint32_t v) {
+    __builtin_nontemporal_store(v, p);
+}
 
 // Workgroup barrier that orders LDS accesses only.  __syncthreads() also
 // waits for every outstanding global load and store (s_waitcnt vmcnt(0)),
