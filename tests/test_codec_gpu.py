@@ -135,6 +135,31 @@ def test_dequantize_unaligned_buffers(C):
         assert np.array_equal(_bits(out).reshape(-1), ref)
 
 
+def test_quantize_codes_at_any_offset(C):
+    """Quantisation into a code buffer 4-byte aligned (paired 32-bit code
+    stores), 2-byte aligned (16-bit stores) or at an odd byte offset
+    (per-byte stores) gives the oracle's codes, scales and zeros."""
+    for kind, shape, G, D in (("key", (2, 3, 64, 256), 32, None),
+                              ("value", (2, 3, 256, 64), 32, 64)):
+        x = seeded_kv(shape, seed=31, kind=kind)
+        xd = x.cuda()
+        n = x.numel()
+        op, os_, oz = codec.quantize_groups(x.numpy(), G)
+        for off in (0, 2, 1):
+            buf = torch.empty(n // 4 + 4, dtype=torch.uint8, device="cuda:0")
+            packed = buf[off:off + n // 4]
+            assert packed.data_ptr() % 4 == off
+            scales = torch.empty(n // G, device="cuda:0")
+            zeros = torch.empty(n // G, device="cuda:0")
+            if kind == "key":
+                C.quantize_keys(xd, packed, scales, zeros, G)
+            else:
+                C.quantize_values(xd, packed, scales, zeros, D, G)
+            assert np.array_equal(_bits(packed), op), (kind, off)
+            assert np.array_equal(_bits(scales), os_.view(np.uint32)), (kind, off)
+            assert np.array_equal(_bits(zeros), oz.view(np.uint32)), (kind, off)
+
+
 def test_unaligned_input_takes_scalar_path(C):
     base = seeded_kv((1, 1, 65, 32), seed=9, kind="key").reshape(-1)
     x = base[1:1 + 64 * 32].reshape(1, 1, 64, 32)   # 4-byte, not 16-byte aligned
