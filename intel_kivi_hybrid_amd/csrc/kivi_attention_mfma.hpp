@@ -242,10 +242,17 @@ struct Shape {
     static constexpr int META4_MAX = (2 * D + 2 * NGMAX * G) / 4;
     static constexpr int NMETA = (META4_MAX + 63) / 64;      // float4 loads per lane
     // chunks kept in flight per wave: ~64 VGPRs of prefetch ring, and at
-    // least 2 (the pipelined loop holds chunks i and i+1 at once)
+    // least 2 (the pipelined loop holds chunks i and i+1 at once).  With 8
+    // query heads per kv head the operand builds hold twice the products per
+    // lane, and two waves per SIMD fit only with half the ring (32 VGPRs): at
+    // B=16-64, 64/8 heads, head_dim 128, 8K context that measured 7-12 %
+    // faster than a 4-deep ring at two waves (spilling) and 25-30 % faster
+    // than a 4-deep ring at one wave per SIMD.
     static constexpr int REGS_PER_CHUNK = 2 * NP + 4 * NMETA;
-    static constexpr int PF = (64 / REGS_PER_CHUNK) < 2 ? 2
-                              : (64 / REGS_PER_CHUNK) > 4 ? 4 : 64 / REGS_PER_CHUNK;
+    static constexpr int RING_REGS = HG >= 8 ? 32 : 64;
+    static constexpr int PF = (RING_REGS / REGS_PER_CHUNK) < 2 ? 2
+                              : (RING_REGS / REGS_PER_CHUNK) > 4 ? 4
+                              : RING_REGS / REGS_PER_CHUNK;
     // Per-wave LDS (bytes).  gfx950 LDS serves a ds_read_b128 16 lanes per
     // cycle from 64 banks of 4 bytes, the lanes {0-3, 12-15, 20-27} then
     // {4-11, 16-19, 28-31} of each half-wave; a ds_write_b128 8 consecutive
@@ -266,10 +273,14 @@ struct Shape {
     // The rest depends on the number of value groups NG = D / Gv.
     __host__ __device__ static constexpr int off_pl(int NG) { return OFF_PA + NG * PA_MAT * 2; }
     __host__ __device__ static constexpr int off_al(int NG) { return off_pl(NG) + 2 * HG * PL_ROW * 4; }
-    __host__ __device__ static constexpr int off_vb(int NG) { return off_al(NG) + 2 * 16 * 4; }
-    __host__ __device__ static constexpr int off_mt(int NG) {
-        return off_vb(NG) + HG * NG * (G / 8) * 4;
-    }
+    // The value corrections [HG][NG][G/8] fp32 are staged only between
+    // whole rings and after the chunk loop, when the key A operands are dead
+    // (every step's key operand build rewrites all 2*HG data rows before its
+    // scores read them), so they share the key A rows.  That keeps a
+    // workgroup at 8 query heads per kv head (head_dim 128, G=32) within
+    // 80 KB of LDS: two workgroups per CU instead of one.
+    __host__ __device__ static constexpr int off_vb(int NG) { return OFF_WA; }
+    __host__ __device__ static constexpr int off_mt(int NG) { return off_al(NG) + 2 * 16 * 4; }
     __host__ __device__ static constexpr int meta_floats(int NG) { return 2 * D + 2 * NG * G; }
     // Staged metadata is stored with one empty 16-byte slot after every 16
     // (float4 slot s at slot s + s/16): the key operand build reads float4s
@@ -303,6 +314,8 @@ struct Shape {
     static_assert(NP >= 1 && LPH * CPL == D && CPL % 2 == 0, "shape");
     // NG = 1 gives the smallest per-wave region
     static_assert(QRES_LDS <= wave_lds(1) && MERGE_LDS <= qres_off(1), "residual buffers");
+    static_assert(HG * NGMAX * (G / 8) * 4 <= 2 * HG * WA_ROW * 2,
+                  "value corrections fit in the key A data rows");
 };
 
 // Writes this wave's state (o unnormalised over D channels, m, l) to the
@@ -1246,12 +1259,16 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
 // B=64, 32/8 heads, 8K context); two where the 4-deep prefetch ring fits that
 // register budget without spilling (head_dim 64, or head_dim 128 with up to
 // 4 query heads per kv head), which measured faster than three waves with a
-// 2-deep ring.  Larger shapes keep the full register file (one wave per SIMD).
+// 2-deep ring.  Head_dim 128 with 8 query heads per kv head and G=32 also
+// runs two waves per SIMD, with a 2-deep ring (Shape::PF): two of its
+// workgroups fit a CU's LDS.  With G=64 that workgroup needs more than half
+// the LDS, so one workgroup runs per CU whatever its registers, and it keeps
+// the full register file, as does head_dim 256 (one wave per SIMD).
 template <int HG, int D, int G>
 constexpr int attn_waves_per_eu() {
     return (D <= 64 && G <= 32 && HG <= 2) ? 4
            : (D <= 64 && G <= 32 && HG <= 4) ? 3
-           : (D <= 64 || (D <= 128 && HG <= 4)) ? 2 : 1;
+           : (D <= 64 || (D <= 128 && (HG <= 4 || G <= 32))) ? 2 : 1;
 }
 
 template <int HG, int D, int G, int NGC, bool R16>
@@ -1259,6 +1276,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(attn_wav
 void attn_mfma_kernel(AttnLaunch a) {
     extern __shared__ __align__(16) unsigned char smem[];
     using S = Shape<HG, D, G>;
+    // A workgroup puts one wave on each SIMD, so n waves per SIMD need n
+    // workgroups' LDS on a CU (160 KB on gfx950).
+    static_assert(attn_waves_per_eu<HG, D, G>() == 1 ||
+                      attn_waves_per_eu<HG, D, G>() * S::lds(S::NGMAX) <= 160 * 1024,
+                  "occupancy target exceeds the CU's LDS");
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     wave_path<S, NGC, R16>(smem, a, split, kvh, b);
 }

@@ -16,6 +16,10 @@ tests/integration/test_attention_fix.py:40-43).
 * Config 5 (split-K): B=4, 32/8 heads, D=128, 131072 quantised tokens with
   value groups of 128, a full window of 128; the automatic split count (16)
   and the log-sum-exp merge; the decode step's flush.
+* Eight query heads per kv head (Llama-3-70B-shaped GQA, not one of the
+  benchmark configs): B=4, 64/8 heads, D=128, context 8192, at the automatic
+  split count and at 1 and 2 splits, where each wave takes 32-63 chunks and
+  so folds its value corrections into the output several times.
 
 Bar: 1e-3 relative (max |o - o_ref| / max |o_ref| per (batch, head)) for
 attention; bit-exact for codes, scales and zeros.
@@ -133,3 +137,22 @@ def test_config5_split_k_full_size(hip_device):
         e = rel_err(o, ref)
         _say(f"[full]   after the flush, {s} splits: rel_err={e:.3e}")
         assert e <= ATTN_TOL
+
+
+def test_gqa8_long_context(hip_device):
+    B, Hq, Hkv, D, R, G, T = 4, 64, 8, 128, 128, 32, 8192
+    Tq = T - R
+    _say(f"[full] gqa8 B={B} Hq={Hq} Hkv={Hkv} D={D} Tq={Tq} Tr={R}")
+    k, v = bench.synth_kv(B, Hkv, T, D, 1234 + 8)
+    st = bench.make_store(k[:, :, :T - 1], v[:, :, :T - 1], G, G, R, hip_device)
+    st.append(k[:, :, -1:].to(hip_device), v[:, :, -1:].to(hip_device))
+    assert (st.quantized_tokens, st.res_len) == (Tq, R)
+    q = seeded_q(B, Hq, D, seed=8)
+    outs = {s: st.attention(q.to(hip_device), num_splits=s).cpu().numpy() for s in (0, 1, 2)}
+    _say("[full]   GPU done; oracle history")
+    kh, vh = oracle_history(k, v, st.n_chunks, G, G)
+    ref = _oracle(q, kh, vh, k, v, Tq, T)
+    for s, o in outs.items():
+        err = rel_err(o, ref)
+        _say(f"[full]   gqa8 splits={s} rel_err={err:.3e}")
+        assert err <= ATTN_TOL, f"splits={s}"
