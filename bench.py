@@ -496,12 +496,13 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 counter passes behind roofline.traffic")
-    ap.add_argument("--only", choices=["config4", "attention", "config3", "config5", "codec",
-                                       "prefill", "copy", "traffic"],
+    ap.add_argument("--only", choices=["config4", "attention", "gqa8", "config3", "config5",
+                                       "codec", "prefill", "copy", "traffic"],
                     default=None,
-                    help="run one workload (for profiling); 'copy' is a plain 512 MiB device "
-                         "copy for calibrating the FETCH_SIZE / WRITE_SIZE counters; "
-                         "'traffic' is the workload of the counter passes")
+                    help="run one workload (for profiling); 'gqa8' is attention of 64 query "
+                         "heads over config 4's store (8 query heads per kv head); 'copy' is "
+                         "a plain 512 MiB device copy for calibrating the FETCH_SIZE / "
+                         "WRITE_SIZE counters; 'traffic' is the workload of the counter passes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the KIVI hot path here is built and "
@@ -531,7 +532,7 @@ def main():
     extra = {}
     loop = attn4 = None
     # ---- config 4: the headline decode loop -------------------------------
-    if only in (None, "config4", "attention"):
+    if only in (None, "config4", "attention", "gqa8"):
         B, Hq, Hkv, D, T, R, G = CONFIG4
         Tq = T - R
         # the store starts Tr0 tokens into its window so that the first timed
@@ -555,11 +556,23 @@ def main():
         # quantised, a full window of R), the first tokens of the loop filling it
         m = R - Tr0
         st.append(k_new[:, :, :m], v_new[:, :, :m])
-        attn4 = time_attention(st, q4, args.attn_iters)
+        if only != "gqa8":
+            attn4 = time_attention(st, q4, args.attn_iters)
+            log(f"[bench] config4 attention: {attn4['avg_us']:.1f} us, {attn4['gbs']:.0f} GB/s "
+                f"(Tq={attn4['Tq']}, Tr={attn4['Tr']}, splits={attn4['splits']})")
+        if only in (None, "gqa8"):
+            # the same store read by 64 query heads: 8 per kv head, the
+            # Llama-3-70B grouping (not a benchmark config)
+            q8 = (torch.randn(B, 8 * Hkv, D, generator=torch.Generator().manual_seed(8))
+                  * D ** -0.5).to(dev)
+            a8 = time_attention(st, q8, args.attn_iters)
+            log(f"[bench] gqa8 attention (B={B}, {8 * Hkv}/{Hkv} heads, config 4's store): "
+                f"{a8['avg_us']:.1f} us, {a8['gbs']:.0f} GB/s (splits={a8['splits']})")
+            extra["attention_gqa8"] = {k_: a8[k_] for k_ in ("avg_us", "gbs", "Tq", "Tr",
+                                                             "splits")}
+            del q8
         st.rollback(m)
-        log(f"[bench] config4 attention: {attn4['avg_us']:.1f} us, {attn4['gbs']:.0f} GB/s "
-            f"(Tq={attn4['Tq']}, Tr={attn4['Tr']}, splits={attn4['splits']})")
-        if only == "attention":
+        if only in ("attention", "gqa8"):
             return
         flush4 = time_flush(st)
         log(f"[bench] config4 flush: {flush4['avg_us']:.1f} us, {flush4['gbs']:.0f} GB/s")
