@@ -244,10 +244,11 @@ struct Shape {
     // chunks kept in flight per wave: ~64 VGPRs of prefetch ring, and at
     // least 2 (the pipelined loop holds chunks i and i+1 at once).  With 8
     // query heads per kv head the operand builds hold twice the products per
-    // lane, and two waves per SIMD fit only with half the ring (32 VGPRs): at
-    // B=16-64, 64/8 heads, head_dim 128, 8K context that measured 7-12 %
-    // faster than a 4-deep ring at two waves (spilling) and 25-30 % faster
-    // than a 4-deep ring at one wave per SIMD.
+    // lane, and two waves per SIMD fit only with half the ring (32 VGPRs):
+    // with 64/8 heads, head_dim 128, that measured 25-30 % faster than a
+    // 4-deep ring at one wave per SIMD (B=4-64, 8K-32K context), and 7-12 %
+    // faster than a 4-deep ring at two waves, which spills (the same at
+    // B=64).
     static constexpr int REGS_PER_CHUNK = 2 * NP + 4 * NMETA;
     static constexpr int RING_REGS = HG >= 8 ? 32 : 64;
     static constexpr int PF = (RING_REGS / REGS_PER_CHUNK) < 2 ? 2
