@@ -183,8 +183,10 @@ int kivi_store_code_layout(int32_t head_dim, int32_t group_size_k, int32_t group
  * kivi_store_flush), query head h reading kv head h / (q_heads/kv_heads).
  * num_splits <= 0 picks the split-K factor; workspace must hold
  * kivi_packed_decode_attention_workspace_size(...) bytes (0 means none is
- * needed and workspace may be NULL).  Supported: q_heads/kv_heads in
- * {1,2,4,8}, head_dim % 16 == 0 and <= 256; plain-layout stores also need
+ * needed and workspace may be NULL).  Supported: any q_heads that is a
+ * multiple of kv_heads (more than 8 query heads per kv head run one launch
+ * per group of 8, each streaming the store once), head_dim % 16 == 0 and
+ * <= 256; plain-layout stores also need
  * group_size_k % 16 == 0 and <= 64.  Matrix-core-layout stores run on the
  * bf16 MFMA units with fp32 accumulation (relative error ~1e-5). */
 /* 0 if kivi_packed_decode_attention can run a store of this geometry (for
@@ -252,7 +254,8 @@ int kivi_packed_decode_attention_noalloc(
  * every query token at least one visible position (for causal queries:
  * kv_start[b] <= num_chunks*G + res_len - q_len).
  * When q_len * (q_heads / kv_heads) exceeds 8 the tokens are split over
- * several launches, each streaming the store once.  No reference counterpart
+ * several launches (and more than 8 query heads per kv head into groups of
+ * 8), each streaming the store once.  No reference counterpart
  * beyond that math (the reference runs HF attention on the CPU,
  * src/kivi_sycl/cache/manager.py:251-290). */
 size_t kivi_packed_attention_workspace_size(int32_t batch, int32_t q_len, int32_t q_heads,

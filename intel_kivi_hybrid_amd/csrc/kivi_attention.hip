@@ -433,6 +433,14 @@ int max_lds_bytes() {
     return 160 * 1024;
 }
 
+// Rows per kv head of one launch: qlen * hg rounded up to a power of two.
+int rows_for(int n) { return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : 8; }
+
+// Query heads per kv head that one launch covers: all of them up to 8 (the
+// kernels' widest instance); more (multi-query models) take one launch per
+// group of 8, each streaming the store once.
+int heads_per_launch(int hg) { return hg < 8 ? hg : 8; }
+
 // Head and group geometry every decode launch needs, whatever its context.
 int check_geometry(int q_heads, int kv_heads, int head_dim, int group_size_k,
                    int group_size_v) {
@@ -440,9 +448,6 @@ int check_geometry(int q_heads, int kv_heads, int head_dim, int group_size_k,
         return set_error(kErrInvalidArgument,
                          "q_heads (%d) must be a positive multiple of kv_heads (%d)",
                          q_heads, kv_heads);
-    const int hg = q_heads / kv_heads;
-    if (hg != 1 && hg != 2 && hg != 4 && hg != 8)
-        return set_error(kErrUnsupported, "q_heads / kv_heads = %d (supported: 1, 2, 4, 8)", hg);
     if (head_dim <= 0 || head_dim % 16 || head_dim > kMaxD)
         return set_error(kErrUnsupported, "head_dim %d (supported: multiple of 16, <= %d)",
                          head_dim, kMaxD);
@@ -527,8 +532,8 @@ int kivi_packed_decode_attention_supported(int32_t q_heads, int32_t kv_heads,
                              "group_size_k %d (supported: multiple of 16, <= 64)", group_size_k);
         return kOk;
     }
-    const int lds = attention_mfma_lds_bytes(q_heads / kv_heads, head_dim, group_size_k,
-                                             head_dim / group_size_v);
+    const int lds = attention_mfma_lds_bytes(rows_for(heads_per_launch(q_heads / kv_heads)),
+                                             head_dim, group_size_k, head_dim / group_size_v);
     const int limit = max_lds_bytes();
     if (lds < 0 || lds > limit)
         return set_error(kErrUnsupported,
@@ -542,9 +547,6 @@ int kivi_packed_decode_attention_supported(int32_t q_heads, int32_t kv_heads,
 }  // extern "C"
 
 namespace {
-
-// Rows per kv head of one launch: qlen * hg rounded up to a power of two.
-int rows_for(int n) { return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : 8; }
 
 // Query tokens per launch: as many as fill at most 8 rows per kv head (the
 // kernels' widest instance) and, on the matrix-core kernel, fit its LDS.
@@ -566,9 +568,9 @@ size_t workspace_for(int batch, int q_len, int q_heads, int kv_heads, int head_d
     const Plan p = make_plan(batch, kv_heads, head_dim, group_size_k, group_size_v, num_chunks,
                              res_len, num_splits);
     if (!needs_workspace(p)) return 0;
-    const int hg = q_heads / kv_heads;
+    const int hl = heads_per_launch(q_heads / kv_heads);
     const int rows = rows_for(
-        tokens_per_launch(hg, q_len, p.mfma, head_dim, group_size_k, group_size_v) * hg);
+        tokens_per_launch(hl, q_len, p.mfma, head_dim, group_size_k, group_size_v) * hl);
     return (size_t)batch * kv_heads * rows * p.n_splits * (head_dim + 2) * sizeof(float);
 }
 
@@ -576,8 +578,9 @@ size_t workspace_for(int batch, int q_len, int q_heads, int kv_heads, int head_d
 // [head_dim], out likewise) over [packed history ; residual window]; causal:
 // the queries are the window's last q_len tokens and token i sees the window
 // up to itself, else every token sees the whole context.  Tokens are split
-// across launches when q_len * (q_heads / kv_heads) exceeds 8 rows; each
-// launch streams the store once.
+// across launches when q_len * (q_heads / kv_heads) exceeds 8 rows, and the
+// query heads of a kv head in groups of 8 when there are more; each launch
+// streams the store once.
 int attention_impl(const float* q, int32_t q_len, int32_t causal, const int32_t* kv_start,
                    const uint8_t* k_codes,
                    const float* k_scale, const float* k_zero, const uint8_t* v_codes,
@@ -635,8 +638,9 @@ int attention_impl(const float* q, int32_t q_len, int32_t causal, const int32_t*
     }
     const Plan p = make_plan(batch, kv_heads, head_dim, group_size_k, group_size_v, num_chunks,
                              res_len, num_splits);
-    const int tpl = tokens_per_launch(hg, q_len, p.mfma, head_dim, group_size_k, group_size_v);
-    const int rows = rows_for(tpl * hg);
+    const int hl = heads_per_launch(hg);
+    const int tpl = tokens_per_launch(hl, q_len, p.mfma, head_dim, group_size_k, group_size_v);
+    const int rows = rows_for(tpl * hl);
     float* part_o = nullptr;
     float* part_ml = nullptr;
     if (needs_workspace(p)) {
@@ -659,11 +663,17 @@ int attention_impl(const float* q, int32_t q_len, int32_t causal, const int32_t*
         if (rc) return rc;
     }
     const int64_t tok_stride = (int64_t)q_heads * head_dim;      // one query token
+    for (int h0 = 0; h0 < hg; h0 += hl)
     for (int i0 = 0; i0 < q_len; i0 += tpl) {
         QueryRows qr;
         qr.qlen = min(tpl, q_len - i0);
-        qr.hg = hg;
-        qr.hg_log2 = hg == 1 ? 0 : hg == 2 ? 1 : hg == 4 ? 2 : 3;
+        qr.hg = min(hl, hg - h0);
+        qr.hg_all = hg;
+        qr.h0 = h0;
+        for (int v = 0; v < qr.qlen * qr.hg; ++v) {
+            qr.row_tok |= (uint32_t)(v / qr.hg) << (4 * v);
+            qr.row_head |= (uint32_t)(v % qr.hg) << (4 * v);
+        }
         qr.q_bstride = (int64_t)q_len * tok_stride;
         qr.vis0 = causal ? res_len - (q_len - 1 - i0) : res_len;
         qr.rows = rows;

@@ -7,27 +7,34 @@
 
 namespace kivi {
 
-// Query rows of one launch.  The HG rows a workgroup computes for kv head
-// kvh ("virtual heads" v) are query token i = v / hg and head kvh*hg + v % hg
-// (hg = Hq / Hkv): a launch covers qlen query tokens, so v < qlen*hg are real
-// rows and the rest padding (zero queries, never stored).  Row v of batch b
-// sits at q + b*q_bstride + (i*Hq + kvh*hg + h)*D, and its output likewise in
-// out.  Query token i sees every quantised chunk and the first
+// Query rows of one launch.  A launch covers qlen query tokens and hg query
+// heads of each kv head (heads h0 .. h0+hg-1 of the hg_all = Hq / Hkv that
+// share it): the rows a workgroup computes for kv head kvh ("virtual heads"
+// v) are query token i = v / hg and head kvh*hg_all + h0 + v % hg, so that
+// v < qlen*hg are real rows and the rest padding (zero queries, never
+// stored).  Both maps are tables of 4 bits per row (at most 8 rows), so any
+// head ratio costs the kernels a shift and a mask.  Row v of batch b sits at
+// q + b*q_bstride + (i*Hq + kvh*hg_all + h0 + h)*D, and its output likewise
+// in out.  Query token i sees every quantised chunk and the first
 // min(res_len, vis0 + i) tokens of the residual window (causal attention of
 // the window's newest tokens; vis0 = res_len when every token sees all).
 struct QueryRows {
     int qlen = 1, hg = 1;
-    int hg_log2 = 0;         // hg is a power of two (1, 2, 4 or 8)
+    int hg_all = 1, h0 = 0;
+    uint32_t row_tok = 0;     // bits 4v..4v+3: query token of row v
+    uint32_t row_head = 0;    // bits 4v..4v+3: head of row v within the launch
     int64_t q_bstride = 0;
     int vis0 = 0;
     int rows = 1;            // HG: qlen*hg rounded up to a power of two (<= 8)
+    __host__ __device__ int tok(int v) const { return (int)((row_tok >> (4 * v)) & 15u); }
     __host__ __device__ int64_t row(int b, int kvh, int v, int Hq, int D) const {
-        const int i = v >> hg_log2, h = v & (hg - 1);
-        return (int64_t)b * q_bstride + ((int64_t)i * Hq + (int64_t)kvh * hg + h) * D;
+        const int h = (int)((row_head >> (4 * v)) & 15u);
+        return (int64_t)b * q_bstride +
+               ((int64_t)tok(v) * Hq + (int64_t)kvh * hg_all + h0 + h) * D;
     }
     __host__ __device__ bool real(int v) const { return v < qlen * hg; }
     __host__ __device__ int visible(int v, int res_len) const {
-        const int n = vis0 + (v >> hg_log2);
+        const int n = vis0 + tok(v);
         return n < res_len ? n : res_len;
     }
 };

@@ -46,6 +46,9 @@ CASES = [
     (1, 2, 2, 64, 16, 16, 32, 100, 4, 0),        # plain layout: the generic kernel
     (2, 8, 2, 64, 32, 32, 64, 40, 3, 0),         # no chunk yet: the generic kernel
     (1, 4, 1, 128, 64, 64, 128, 1300, 6, 4),     # G = 64, GQA 4, 4 splits
+    (1, 6, 2, 128, 32, 32, 128, 600, 3, 0),      # GQA 3: 2 tokens per launch, 2 padding rows
+    (2, 24, 2, 64, 32, 32, 64, 300, 2, 2),       # GQA 12: head groups of 8 and 4, 2 splits
+    (1, 14, 2, 64, 16, 16, 32, 100, 3, 0),       # GQA 7, plain layout: the generic kernel
 ]
 
 

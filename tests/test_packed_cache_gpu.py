@@ -106,6 +106,48 @@ def test_hf_generate_with_packed_cache(hip_device):
     assert cache.total_flushes == 4 * ((st["total_tokens"] - 32) // 32 + 1)
 
 
+@pytest.mark.parametrize("heads,kv_heads", [(14, 2), (16, 1)])
+def test_any_head_ratio_llama_logits(hip_device, heads, kv_heads):
+    """Llama layers with 7 query heads per kv head (the Qwen2-7B grouping)
+    and with one kv head (multi-query), model on the GPU in fp32: fed the
+    same tokens, the packed cache's logits (fused decode kernel) match the
+    served cache's (HF attention over the dequantised history) at every
+    step, across several flushes.  Logits rather than greedy tokens, so a
+    near-tie in a random model cannot decide the outcome."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+    from intel_kivi_hybrid_amd.cache.manager import KiviCache
+    torch.manual_seed(4)
+    cfg = LlamaConfig(vocab_size=512, hidden_size=64 * heads, intermediate_size=1024,
+                      num_hidden_layers=2, num_attention_heads=heads,
+                      num_key_value_heads=kv_heads, max_position_embeddings=512)
+    model = LlamaForCausalLM(cfg).eval().to(hip_device)
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, cfg.vocab_size, (1, 160), generator=g).to(hip_device)
+    n_prompt, R = 40, 32
+    print(f"[packed-ratio] heads={heads} kv_heads={kv_heads}", flush=True)
+    packed = pc.KiviPackedCache.from_model(model, device="cuda:0", group_size=32,
+                                           residual_length=R)
+    served = KiviCache.from_model(model, device="cuda:0", group_size=32, residual_length=R)
+    worst = 0.0
+    with torch.no_grad():
+        out = model(ids[:, :n_prompt], use_cache=True)
+        served.add_tokens(out.past_key_values)
+        with pc.packed_attention(model):
+            model(ids[:, :n_prompt], past_key_values=packed, use_cache=True)
+        for s in range(n_prompt, ids.shape[1]):
+            ref = model(ids[:, s:s + 1], past_key_values=served.get_full_cache(),
+                        use_cache=True)
+            served.add_tokens(ref.past_key_values)
+            with pc.packed_attention(model):
+                ours = model(ids[:, s:s + 1], past_key_values=packed, use_cache=True)
+            a, b = ours.logits[0, -1].float(), ref.logits[0, -1].float()
+            worst = max(worst, ((a - b).abs().max() / b.abs().max()).item())
+    print(f"[packed-ratio]   worst logits rel diff {worst:.3e} over "
+          f"{ids.shape[1] - n_prompt} steps", flush=True)
+    assert packed.get_stats(0)["total_tokens"] == ids.shape[1]
+    assert worst <= 1e-3
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_gqa_llama_packed_vs_served(hip_device, dtype):
     """Grouped-query Llama (8 query heads over 2 kv heads, D=128), model on

@@ -225,7 +225,9 @@ def test_unsupported_geometry_refused_up_front(cpu_store):
         pc.KiviPackedCache(2, 512, 2, group_size=32, residual_length=32)
     assert decode_geometry_error(8, 2, 128, 32, 32) is None
     assert decode_geometry_error(4, 4, 64, 32, 64) is None
-    assert "q_heads / kv_heads = 3" in decode_geometry_error(6, 2, 64, 32, 32)
+    assert decode_geometry_error(6, 2, 64, 32, 32) is None         # any head ratio
+    assert decode_geometry_error(40, 1, 128, 32, 32) is None
+    assert "multiple of kv_heads" in decode_geometry_error(6, 4, 64, 32, 32)
     assert "needs" in decode_geometry_error(8, 1, 256, 64, 32)     # LDS beyond the device's
 
 

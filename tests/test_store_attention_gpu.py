@@ -66,6 +66,52 @@ def test_attention_gqa_ratios(store_cls, Hq, Hkv, D):
     _attention_case(store_cls, 2, Hq, Hkv, D, 32, 32, 64, 300)
 
 
+# Ratios of query to kv heads that are not a power of two (Llama-3.2-3B 3,
+# Qwen2.5-14B 5, Qwen2-7B 7) pad the launch's rows to the next power of two;
+# more than 8 (multi-query models) take one launch per group of 8 heads.
+@pytest.mark.parametrize("Hq,Hkv", [(6, 2), (10, 2), (12, 2), (14, 2), (28, 4), (24, 2),
+                                    (32, 2), (40, 1)])
+@pytest.mark.parametrize("D", [64, 128])
+def test_attention_any_head_ratio(store_cls, Hq, Hkv, D):
+    _attention_case(store_cls, 2, Hq, Hkv, D, 32, 32, 64, 300)
+
+
+@pytest.mark.parametrize("Hq,Hkv,splits", [(14, 2, 0), (14, 2, 3), (24, 2, 1), (40, 1, 5)])
+def test_attention_any_head_ratio_long(store_cls, Hq, Hkv, splits):
+    """Long enough for the mode where one wave takes the window (1 split),
+    and split merges, with padded rows and head groups."""
+    _attention_case(store_cls, 1, Hq, Hkv, 128, 32, 32, 128, 2400, splits=splits, seed=5)
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(6, 2), (24, 2)])
+def test_attention_any_head_ratio_plain_layout(store_cls, Hq, Hkv):
+    """The generic kernel (plain layout, G=16) with padded rows and head groups."""
+    _attention_case(store_cls, 2, Hq, Hkv, 64, 16, 16, 32, 100)
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(14, 2), (24, 2)])
+def test_fused_append_any_head_ratio(store_cls, Hq, Hkv):
+    """A decode step whose token the attention launch itself files in the ring:
+    with head groups every launch reads the token from its own tensor, and
+    the result matches the call that reads it from the ring bit for bit."""
+    B, D, G, R, T = 2, 128, 32, 128, 700
+    print(f"[attn] fused append Hq={Hq} Hkv={Hkv}", flush=True)
+    k, v = make_kv(B, Hkv, T, D, seed=17)
+    st = store_cls(B, Hkv, D, G, R, "cuda:0")
+    fill_store(st, k[:, :, :T - 1], v[:, :, :T - 1], R)
+    st.stage_token(k[:, :, T - 1:].cuda(), v[:, :, T - 1:].cuda())
+    q = seeded_q(B, Hq, D, seed=18).cuda()
+    fused = st.attention(q).cpu().numpy()
+    ring = st.attention(q).cpu().numpy()
+    assert np.array_equal(fused.view(np.uint32), ring.view(np.uint32))
+    kh, vh = oracle_history(k, v, st.n_chunks, G, G)
+    q0 = st.n_chunks * G
+    ref = decode_attention(q.cpu().numpy(), kh, vh, k[:, :, q0:].numpy(), v[:, :, q0:].numpy())
+    err = rel_err(fused, ref)
+    print(f"[attn]   rel_err={err:.3e}", flush=True)
+    assert err <= ATTN_TOL
+
+
 @pytest.mark.parametrize("G,Gv,R,T", [
     (16, 16, 32, 100), (32, 128, 128, 400), (64, 64, 64, 400), (32, 32, 32, 32),
     (32, 32, 128, 127),   # residual only, no chunk yet
