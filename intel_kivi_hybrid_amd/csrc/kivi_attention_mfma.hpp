@@ -987,8 +987,8 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         // Four channels of a ring row widened to fp32.  The ring's width is
         // a template parameter (a run-time branch here would cost registers
         // at the kernel's peak, the prefetched chunks being live); bf16 vs
-        // fp16 is a select in the widening.
-        const bool res_half = a.res_dt == kSrcF16;
+        // fp16 is a bit mask in the widening (load4_16).
+        const uint32_t res_half = a.res_dt == kSrcF16 ? 0xffffffffu : 0u;
         auto load4 = [&](const void* p, int64_t i) {
             if constexpr (R16) return load4_16(p, i, res_half);
             else return load4_vec<kSrcF32>(p, i);
