@@ -17,8 +17,10 @@ at their stated token counts, the config-2 codec ops through ``_C``
 baselines of the reference path timed on the host over the same K/V bits.
 
 Algorithmic bytes (per (batch, kv-head)):
-  attention : D*Tq/4 + 8*D*Tq/Gk + Tq*D/4 + 8*Tq*D/Gv + 8*Tr*D + 8*(Hq/Hkv)*D
-              (the step's new token is read as part of Tr)
+  attention : D*Tq/4 + 8*D*Tq/Gk + Tq*D/4 + 8*Tq*D/Gv + 2*r*Tr*D + 8*(Hq/Hkv)*D
+              (r = 4 for the fp32 ring, 2 for the bf16 ring of the
+              ``attention_config4_ring_bf16`` leg; the step's new token is
+              read as part of Tr)
   append    : 4*D*2 written (the new token's K and V into the ring)
   flush     : 8*G*D (read residual) + G*D/4 + 8*D + G*D/4 + 8*G*D/Gv (write)
   quantise  : per tensor of N fp32: 4N read + N/4 + 8N/G written
@@ -41,9 +43,12 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0
 
 
-def attn_bytes(B, Hq, Hkv, D, Tq, Tr, Gk, Gv):
+def attn_bytes(B, Hq, Hkv, D, Tq, Tr, Gk, Gv, ring_bytes=4):
+    """Algorithmic bytes of one decode-attention call: codes, scales and zeros
+    of Tq quantised tokens, Tr residual tokens of K and V (ring_bytes per
+    element: 4 fp32, 2 bf16/fp16), q and o (fp32)."""
     per = (D * Tq // 4 + 8 * D * Tq // Gk + Tq * D // 4 + 8 * Tq * D // Gv
-           + 8 * Tr * D + 8 * (Hq // Hkv) * D)
+           + 2 * ring_bytes * Tr * D + 8 * (Hq // Hkv) * D)
     return per * B * Hkv
 
 
@@ -165,7 +170,8 @@ def time_attention(st, q, iters, rotate=None):
         turn[0] = (turn[0] + 1) % len(stores)
     r = time_calls(call, iters)
     Hq = q.shape[1]
-    nbytes = attn_bytes(st.B, Hq, st.H, st.D, st.quantized_tokens, st.res_len, st.G, st.Gv)
+    nbytes = attn_bytes(st.B, Hq, st.H, st.D, st.quantized_tokens, st.res_len, st.G, st.Gv,
+                        st.k_res.element_size())
     ws = st.workspace_bytes(Hq)
     r.update({"bytes": nbytes, "gbs": nbytes / (r["avg_us"] * 1e-6) / 1e9,
               "Tq": st.quantized_tokens, "Tr": st.res_len,
@@ -496,11 +502,13 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 counter passes behind roofline.traffic")
-    ap.add_argument("--only", choices=["config4", "attention", "gqa8", "config3", "config5",
-                                       "codec", "prefill", "copy", "traffic"],
+    ap.add_argument("--only", choices=["config4", "attention", "gqa8", "ring16", "config3",
+                                       "config5", "codec", "prefill", "copy", "traffic"],
                     default=None,
                     help="run one workload (for profiling); 'gqa8' is attention of 64 query "
-                         "heads over config 4's store (8 query heads per kv head); 'copy' is "
+                         "heads over config 4's store (8 query heads per kv head); 'ring16' "
+                         "is config-4 attention over a store whose residual ring is bf16 (a "
+                         "bf16 model's packed cache); 'copy' is "
                          "a plain 512 MiB device copy for calibrating the FETCH_SIZE / "
                          "WRITE_SIZE counters; 'traffic' is the workload of the counter passes")
     args = ap.parse_args()
@@ -532,7 +540,7 @@ def main():
     extra = {}
     loop = attn4 = None
     # ---- config 4: the headline decode loop -------------------------------
-    if only in (None, "config4", "attention", "gqa8"):
+    if only in (None, "config4", "attention", "gqa8", "ring16"):
         B, Hq, Hkv, D, T, R, G = CONFIG4
         Tq = T - R
         # the store starts Tr0 tokens into its window so that the first timed
@@ -548,6 +556,28 @@ def main():
         v_new = v[:, :, Tq + Tr0:].to(dev)
         cpu_k4 = k[:4, :, :T].clone()
         cpu_v4 = v[:4, :, :T].clone()
+        if only in (None, "ring16"):
+            # the same context with a bf16 residual ring, as a bf16 model's
+            # KiviPackedCache keeps it: bf16 K/V quantised, window in bf16
+            from intel_kivi_hybrid_amd.store import PackedKVStore
+            st16 = PackedKVStore(B, Hkv, D, G, R, dev, group_size_v=G,
+                                 chunk_capacity=T // G + 4, residual_dtype=torch.bfloat16)
+            k16, v16 = k[:, :, :T].to(dev, torch.bfloat16), v[:, :, :T].to(dev, torch.bfloat16)
+            st16.extend(k16[:, :, :T - 1], v16[:, :, :T - 1], flush_at=R)
+            st16.append(k16[:, :, T - 1:], v16[:, :, T - 1:])
+            del k16, v16
+            assert (st16.quantized_tokens, st16.res_len) == (Tq, R)
+            q16 = (torch.randn(B, Hq, D, generator=torch.Generator().manual_seed(16))
+                   * D ** -0.5).to(dev)
+            a16 = time_attention(st16, q16, args.attn_iters)
+            log(f"[bench] config4 attention, bf16 residual ring: {a16['avg_us']:.1f} us, "
+                f"{a16['gbs']:.0f} GB/s (Tq={a16['Tq']}, Tr={a16['Tr']})")
+            extra["attention_config4_ring_bf16"] = {k_: a16[k_] for k_ in ("avg_us", "gbs", "Tq",
+                                                                           "Tr")}
+            del st16, q16
+            torch.cuda.empty_cache()
+            if only == "ring16":
+                return
         del k, v
         gq = torch.Generator().manual_seed(5)
         q_all = (torch.randn(n_new, B, Hq, D, generator=gq) * D ** -0.5).to(dev)

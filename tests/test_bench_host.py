@@ -21,6 +21,9 @@ def test_attention_bytes_match_the_config_closed_forms():
     assert bench.attn_bytes(16, 32, 32, 128, 4096, 128, 32, 32) == 656_384 * 512 == 336_068_608
     # config 4 (Tq = 8064, Tr = 128): 1,167,360 B x 512 pairs
     assert bench.attn_bytes(64, 32, 8, 128, 8064, 128, 32, 32) == 1_167_360 * 512 == 597_688_320
+    # the same with a bf16 residual ring: the window's K and V at 2 bytes
+    assert bench.attn_bytes(64, 32, 8, 128, 8064, 128, 32, 32, ring_bytes=2) == \
+        597_688_320 - 512 * 2 * 128 * 128 * 2 == 564_133_888
     # config 5 (Gv = 128): 13,766,656 B x 32 pairs
     assert bench.attn_bytes(4, 32, 8, 128, 131072, 128, 32, 128) == 13_766_656 * 32
 
