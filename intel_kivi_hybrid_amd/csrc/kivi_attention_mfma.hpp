@@ -531,11 +531,17 @@ __device__ __forceinline__ void stage_meta(const ChunkRegs<S>& r, float* MT, int
         }
         return;
     }
+    // Every lane stores: a lane past the end holds the last float4 (its load
+    // was clamped to it, chunk_src) and writes those same bits to the last
+    // slot.  A conditional store was the value's only use, so the compiler
+    // moved the chunk's metadata load into the branch, right before the
+    // store and behind a wait for every outstanding load (the prefetch
+    // ring's included).
     const int n4 = meta_floats / 4;
 #pragma unroll
     for (int i = 0; i < S::NMETA; ++i) {
-        const int e = lane + 64 * i;
-        if (e < n4) mt[S::meta_slot(e)] = r.meta[i];
+        const int e = min(lane + 64 * i, n4 - 1);
+        mt[S::meta_slot(e)] = r.meta[i];
     }
 }
 
