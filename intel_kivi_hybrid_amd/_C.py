@@ -20,6 +20,7 @@ import ctypes
 import torch
 
 from . import _native
+from ._device import device_index, on_device, stream_handle
 
 _lib = _native.load()
 
@@ -206,7 +207,7 @@ def _validate_roundtrip_values(input, output, head_dim, group_size) -> int:
 # Launch plumbing.
 # --------------------------------------------------------------------------
 def _stream_of(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    return stream_handle(device)
 
 
 def _ptr(t: torch.Tensor) -> int:
@@ -424,7 +425,7 @@ _ws_cache = {}
 def _workspace(device, nbytes: int):
     if nbytes == 0:
         return None
-    key = (str(device), torch.cuda.current_stream(device).cuda_stream)
+    key = (device_index(device), stream_handle(device))
     buf = _ws_cache.get(key)
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
@@ -463,32 +464,28 @@ def packed_decode_attention(q, store, softmax_scale=None, out=None, num_splits=0
     if pend is not None:
         # the staged token goes into the ring within this launch
         kn, vn = pend
-        with torch.cuda.device(q.device):
+        # (plain ints for the pointers: the entry points' argtypes convert them)
+        with on_device(q.device):
             _native.check(_lib.kivi_packed_decode_attention_append(
-                ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(kn.data_ptr()),
-                ctypes.c_void_p(vn.data_ptr()), kn.stride(0), kn.stride(1),
-                ctypes.c_void_p(store.k_codes.data_ptr()),
-                ctypes.c_void_p(store.k_scale.data_ptr()), ctypes.c_void_p(store.k_zero.data_ptr()),
-                ctypes.c_void_p(store.v_codes.data_ptr()), ctypes.c_void_p(store.v_scale.data_ptr()),
-                ctypes.c_void_p(store.v_zero.data_ptr()), ctypes.c_void_p(store.k_res.data_ptr()),
-                ctypes.c_void_p(store.v_res.data_ptr()), res_dt, ctypes.c_void_p(out.data_ptr()),
-                ctypes.c_void_p(workspace.data_ptr() if workspace is not None else 0), ws_bytes,
+                q.data_ptr(), kn.data_ptr(), vn.data_ptr(), kn.stride(0), kn.stride(1),
+                store.k_codes.data_ptr(), store.k_scale.data_ptr(), store.k_zero.data_ptr(),
+                store.v_codes.data_ptr(), store.v_scale.data_ptr(), store.v_zero.data_ptr(),
+                store.k_res.data_ptr(), store.v_res.data_ptr(), res_dt, out.data_ptr(),
+                workspace.data_ptr() if workspace is not None else 0, ws_bytes,
                 B, Hq, store.H, D, store.G, store.Gv, store.capacity, store.n_chunks, store.R,
                 store.res_start, store.res_len, scale, int(num_splits),
-                ctypes.c_void_p(_stream_of(q.device))), "packed_decode_attention")
+                stream_handle(q.device)), "packed_decode_attention")
         store._pending = None
         return out
-    with torch.cuda.device(q.device):
+    with on_device(q.device):
         _native.check(_lib.kivi_packed_decode_attention(
-            ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(store.k_codes.data_ptr()),
-            ctypes.c_void_p(store.k_scale.data_ptr()), ctypes.c_void_p(store.k_zero.data_ptr()),
-            ctypes.c_void_p(store.v_codes.data_ptr()), ctypes.c_void_p(store.v_scale.data_ptr()),
-            ctypes.c_void_p(store.v_zero.data_ptr()), ctypes.c_void_p(store.k_res.data_ptr()),
-            ctypes.c_void_p(store.v_res.data_ptr()), res_dt, ctypes.c_void_p(out.data_ptr()),
-            ctypes.c_void_p(workspace.data_ptr() if workspace is not None else 0), ws_bytes,
+            q.data_ptr(), store.k_codes.data_ptr(), store.k_scale.data_ptr(),
+            store.k_zero.data_ptr(), store.v_codes.data_ptr(), store.v_scale.data_ptr(),
+            store.v_zero.data_ptr(), store.k_res.data_ptr(), store.v_res.data_ptr(), res_dt,
+            out.data_ptr(), workspace.data_ptr() if workspace is not None else 0, ws_bytes,
             B, Hq, store.H, D, store.G, store.Gv, store.capacity, store.n_chunks, store.R,
             store.res_start, store.res_len, scale, int(num_splits),
-            ctypes.c_void_p(_stream_of(q.device))), "packed_decode_attention")
+            stream_handle(q.device)), "packed_decode_attention")
     return out
 
 
@@ -543,7 +540,7 @@ def packed_attention(q, store, causal=True, softmax_scale=None, out=None, num_sp
         _check(workspace.is_contiguous() and workspace.numel() * workspace.element_size() >= need,
                "workspace must be contiguous and hold ", need, " bytes")
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    with torch.cuda.device(q.device):
+    with on_device(q.device):
         _native.check(_lib.kivi_packed_attention(
             ctypes.c_void_p(qk.data_ptr()), L, 1 if causal else 0, ctypes.c_void_p(ks_ptr),
             ctypes.c_void_p(store.k_codes.data_ptr()),

@@ -1,0 +1,37 @@
+"""Device and stream plumbing for the native calls on the per-step paths.
+
+Each decode step makes a few native calls per layer, and at small batches
+their host cost bounds the step: ``torch.cuda.current_stream(device)``
+builds a Python stream object on every call, and ``torch.cuda.device(...)``
+switches the current device even when it is already current.  These helpers
+give the same answers without that work.
+"""
+
+from __future__ import annotations
+
+import contextlib
+
+import torch
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_NULL = contextlib.nullcontext()
+
+
+def device_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
+def stream_handle(device: torch.device) -> int:
+    """The HIP stream handle of ``device``'s current stream (the stream
+    ``torch.cuda.current_stream(device)`` names)."""
+    if _raw_stream is not None:
+        return _raw_stream(device_index(device))
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def on_device(device: torch.device):
+    """A context in which ``device`` is the current device: no switch when it
+    already is."""
+    if torch.cuda.current_device() == device_index(device):
+        return _NULL
+    return torch.cuda.device(device)

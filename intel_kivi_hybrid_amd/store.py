@@ -27,6 +27,7 @@ from typing import Optional
 import torch
 
 from . import _native
+from ._device import on_device, stream_handle
 
 _lib = _native.load()
 
@@ -39,8 +40,8 @@ def _vp(t: Optional[torch.Tensor]):
     return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
 
 
-def _stream(device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+def _stream(device) -> int:
+    return stream_handle(device)
 
 
 def _pack_last(codes: torch.Tensor) -> torch.Tensor:
@@ -214,7 +215,7 @@ class PackedKVStore:
 
     def _launch_append(self, k: torch.Tensor, v: torch.Tensor, slot: int) -> None:
         sb, sh, st, _ = k.stride()
-        with torch.cuda.device(self.device):
+        with on_device(self.device):
             _native.check(_lib.kivi_store_append(
                 _vp(k), _vp(v), _SRC_DTYPES[k.dtype], sb, sh, st, k.shape[2], _vp(self.k_res),
                 _vp(self.v_res), self.res_dtype_code, self.B, self.H, self.D, self.R, slot,
@@ -324,7 +325,7 @@ class PackedKVStore:
         """Quantise ``n_chunks`` chunks from [ring window ; k/v] (one launch)."""
         hist_cap = self.capacity * self.G if self.keep_history else 0
         sb, sh, st, _ = k.stride()
-        with torch.cuda.device(self.device):
+        with on_device(self.device):
             _native.check(_lib.kivi_store_flush_chunks(
                 _vp(self.k_res), _vp(self.v_res), self.res_dtype_code, _vp(k), _vp(v),
                 _SRC_DTYPES[k.dtype],
@@ -351,7 +352,7 @@ class PackedKVStore:
         self._commit()
         self.reserve(self.n_chunks + 1)
         hist_cap = self.capacity * self.G if self.keep_history else 0
-        with torch.cuda.device(self.device):
+        with on_device(self.device):
             _native.check(_lib.kivi_store_flush(
                 _vp(self.k_res), _vp(self.v_res), self.res_dtype_code, _vp(self.k_codes),
                 _vp(self.k_scale),
