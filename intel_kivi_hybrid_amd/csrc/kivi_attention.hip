@@ -666,6 +666,8 @@ int attention_impl(const float* q, int32_t q_len, int32_t causal, const int32_t*
         if (rc) return rc;
     }
     const int64_t tok_stride = (int64_t)q_heads * head_dim;      // one query token
+    // One launch per group of up to 8 query heads of each kv head (h0) and
+    // per group of query tokens that fills at most 8 rows (i0).
     for (int h0 = 0; h0 < hg; h0 += hl)
     for (int i0 = 0; i0 < q_len; i0 += tpl) {
         QueryRows qr;
