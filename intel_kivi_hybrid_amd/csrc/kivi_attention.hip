@@ -366,14 +366,31 @@ struct Plan {
     int n_qsplits, chunks_per_wave, res_waves, early_per_pass_x2;   // matrix-core kernel
 };
 
+// empty_ok: the caller can give the matrix-core kernel a readable chunk 0
+// (non-null chunk arrays with capacity for one chunk) when the context has
+// no chunk yet.
 Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
-               int splits_hint) {
+               int splits_hint, bool empty_ok = true) {
     Plan p{};
     p.layout = code_layout_for(D, G, Gv);
-    // The matrix-core kernel needs at least one chunk per workgroup (its
-    // prefetch ring is filled unconditionally); a residual-only context of a
-    // matrix-core store goes to the generic kernel, which reads the ring only.
-    p.mfma = p.layout == kLayoutMfma && n_chunks > 0;
+    if (p.layout == kLayoutMfma && n_chunks == 0) {
+        // A context still wholly in the residual window (the first steps of
+        // every sequence).  The matrix-core kernel's window pass takes it: one
+        // split, all four waves on the window; the prefetch ring's loads read
+        // chunk 0 and go unused.  Without a readable chunk 0 the generic
+        // kernel takes it, also unsplit, so that the workspace (none) does
+        // not depend on which.  B=1 and 16, 32/8 heads, 100-127 tokens: 32-43
+        // us per call on the generic kernel.
+        p.mfma = empty_ok;
+        p.n_units = (res_len + kWave - 1) / kWave;
+        p.units_per_split = p.n_units;
+        p.n_qsplits = p.n_splits = 1;
+        p.chunks_per_wave = 0;
+        p.res_waves = 4;
+        p.early_per_pass_x2 = 0;
+        return p;
+    }
+    p.mfma = p.layout == kLayoutMfma;
     if (p.mfma) {
         // Aim for ~2048 chunk waves in flight (8 per CU) with >= 2 chunks per
         // wave.  Few (batch, kv-head) pairs take many splits: B=1, 32/8 heads
@@ -466,9 +483,12 @@ int check_geometry(int q_heads, int kv_heads, int head_dim, int group_size_k,
 }  // namespace
 
 int launch_attention_mfma(const AttnLaunch& a, hipStream_t st) {
-    // every workgroup's prefetch ring reads at least one real chunk
-    if (a.n_chunks <= 0 || a.chunks_per_wave <= 0 ||
-        (int64_t)(a.n_qsplits - 1) * 4 * a.chunks_per_wave >= a.n_chunks)
+    // every workgroup's prefetch ring reads at least one real chunk, or, in a
+    // context with none yet, chunk 0 of a store that has room for one (one
+    // split, its loads unused)
+    const bool empty = a.n_chunks == 0 && a.n_qsplits == 1 && a.Cmax >= 1 && a.res_len > 0;
+    if (!empty && (a.n_chunks <= 0 || a.chunks_per_wave <= 0 ||
+                   (int64_t)(a.n_qsplits - 1) * 4 * a.chunks_per_wave >= a.n_chunks))
         return set_error(kErrInvalidArgument,
                          "matrix-core attention needs a chunk in every split (chunks %d, "
                          "splits %d, chunks per wave %d)", a.n_chunks, a.n_qsplits,
@@ -639,8 +659,10 @@ int attention_impl(const float* q, int32_t q_len, int32_t causal, const int32_t*
                              "residual window (start %d, len %d) outside capacity %d",
                              res_start, res_len, res_capacity);
     }
+    const bool empty_ok = chunk_capacity >= 1 && k_codes && k_scale && k_zero && v_codes &&
+                          v_scale && v_zero;
     const Plan p = make_plan(batch, kv_heads, head_dim, group_size_k, group_size_v, num_chunks,
-                             res_len, num_splits);
+                             res_len, num_splits, empty_ok);
     const int hl = heads_per_launch(hg);
     const int tpl = tokens_per_launch(hl, q_len, p.mfma, head_dim, group_size_k, group_size_v);
     const int rows = rows_for(tpl * hl);

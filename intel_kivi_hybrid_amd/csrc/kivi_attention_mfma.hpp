@@ -650,7 +650,9 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     const int g_begin = split * kWaves * a.chunks_per_wave;
     const int g_end = min(g_begin + kWaves * a.chunks_per_wave, a.n_chunks);
     const int g_cnt = max(0, g_end - g_begin);
-    const int c_last = g_end - 1;
+    // (0 when the context has no chunk yet: the ring's loads then read chunk 0
+    // of the store, in bounds, and no step uses them)
+    const int c_last = max(g_end - 1, 0);
     // early chunks per other wave: early_per_pass_x2 / 2 per pass, rounded
     const int early = min((a.early_per_pass_x2 * split_passes + 1) / 2, a.chunks_per_wave / 2);
     const int s_early = res_one ? min((kWaves - 1) * early, g_cnt) : 0;
@@ -668,9 +670,10 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     int cid[PF];     // the chunk in each ring slot; -1 past the end (its load re-reads c_last)
     const ChunkSrc<S> src = chunk_src<S, PAIRED>(a, bh * a.Cmax, lane, NG);
     const PairSlots<S> pslots = pair_slots<S>(lane, NG);
-    // (the launch gives every workgroup at least one chunk, so c_last is a
-    // valid chunk and these loads need no branch: a branch here would make the
-    // compiler wait for them before the query's LDS stores)
+    // (the launch gives every workgroup at least one chunk, or the store room
+    // for chunk 0, so c_last is a readable chunk and these loads need no
+    // branch: a branch here would make the compiler wait for them before the
+    // query's LDS stores)
 #pragma unroll
     for (int k = 0; k < PF; ++k) {
         cid[k] = chunk_of(k);

@@ -44,7 +44,7 @@ CASES = [
     (2, 16, 2, 128, 32, 32, 128, 900, 2, 3),     # GQA 8: one token per launch, 3 splits
     (1, 8, 2, 128, 32, 128, 128, 2200, 8, 1),    # one split: a wave takes the window, Gv = D
     (1, 2, 2, 64, 16, 16, 32, 100, 4, 0),        # plain layout: the generic kernel
-    (2, 8, 2, 64, 32, 32, 64, 40, 3, 0),         # no chunk yet: the generic kernel
+    (2, 8, 2, 64, 32, 32, 64, 40, 3, 0),         # no chunk yet: the window pass alone
     (1, 4, 1, 128, 64, 64, 128, 1300, 6, 4),     # G = 64, GQA 4, 4 splits
     (1, 6, 2, 128, 32, 32, 128, 600, 3, 0),      # GQA 3: 2 tokens per launch, 2 padding rows
     (2, 24, 2, 64, 32, 32, 64, 300, 2, 2),       # GQA 12: head groups of 8 and 4, 2 splits

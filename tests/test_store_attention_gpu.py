@@ -112,6 +112,52 @@ def test_fused_append_any_head_ratio(store_cls, Hq, Hkv):
     assert err <= ATTN_TOL
 
 
+@pytest.mark.parametrize("T", [1, 40, 127])
+@pytest.mark.parametrize("ring", [torch.float32, torch.bfloat16])
+def test_window_only_context(store_cls, T, ring):
+    """A context still wholly in the residual window (no chunk yet) runs on
+    the matrix-core kernel's window pass; the same call through the C ABI
+    with no chunk arrays at all (null pointers, no capacity) runs on the
+    generic kernel.  Both against the oracle; then a decode step whose token
+    the launch files itself, bit-identical to reading it from the ring."""
+    import ctypes
+    from intel_kivi_hybrid_amd import _native
+    B, Hq, Hkv, D, G, R = 2, 8, 2, 128, 32, 128
+    print(f"[attn] window only T={T} ring={ring}", flush=True)
+    k, v = make_kv(B, Hkv, T + 1, D, seed=60 + T)
+    st = store_cls(B, Hkv, D, G, R, "cuda:0", residual_dtype=ring)
+    st.extend(k[:, :, :T].cuda().to(ring), v[:, :, :T].cuda().to(ring), flush_at=R)
+    assert (st.n_chunks, st.res_len) == (0, T)
+    kq, vq = k.to(ring).float(), v.to(ring).float()     # what the ring holds
+    q = seeded_q(B, Hq, D, seed=61).cuda()
+    out = st.attention(q).cpu().numpy()
+    empty = np.zeros((B, Hkv, 0, D), np.float32)
+    ref = decode_attention(q.cpu().numpy(), empty, empty, kq[:, :, :T].numpy(),
+                           vq[:, :, :T].numpy())
+    err = rel_err(out, ref)
+    print(f"[attn]   matrix-core window pass rel_err={err:.3e}", flush=True)
+    assert err <= ATTN_TOL
+    lib = _native.load()
+    gen = torch.full_like(q, float("nan"))
+    vp = lambda x: ctypes.c_void_p(x.data_ptr())       # noqa: E731
+    _native.check(lib.kivi_packed_decode_attention(
+        vp(q), None, None, None, None, None, None, vp(st.k_res), vp(st.v_res),
+        st.res_dtype_code, vp(gen), None, 0, B, Hq, Hkv, D, G, G, 0, 0, R, st.res_start,
+        st.res_len, float(D ** -0.5), 0, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+        "kivi_packed_decode_attention")
+    err = rel_err(gen.cpu().numpy(), ref)
+    print(f"[attn]   generic kernel (no chunk arrays) rel_err={err:.3e}", flush=True)
+    assert err <= ATTN_TOL
+    st.stage_token(k[:, :, T:].cuda().to(ring), v[:, :, T:].cuda().to(ring))
+    fused = st.attention(q).cpu().numpy()
+    again = st.attention(q).cpu().numpy()
+    assert np.array_equal(fused.view(np.uint32), again.view(np.uint32))
+    ref = decode_attention(q.cpu().numpy(), empty, empty, kq.numpy(), vq.numpy())
+    err = rel_err(fused, ref)
+    print(f"[attn]   fused append rel_err={err:.3e}", flush=True)
+    assert err <= ATTN_TOL
+
+
 @pytest.mark.parametrize("G,Gv,R,T", [
     (16, 16, 32, 100), (32, 128, 128, 400), (64, 64, 64, 400), (32, 32, 32, 32),
     (32, 32, 128, 127),   # residual only, no chunk yet
