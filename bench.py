@@ -502,13 +502,15 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 counter passes behind roofline.traffic")
-    ap.add_argument("--only", choices=["config4", "attention", "gqa8", "ring16", "config3",
-                                       "config5", "codec", "prefill", "copy", "traffic"],
+    ap.add_argument("--only", choices=["config4", "attention", "gqa8", "ring16", "b1",
+                                       "config3", "config5", "codec", "prefill", "copy",
+                                       "traffic"],
                     default=None,
                     help="run one workload (for profiling); 'gqa8' is attention of 64 query "
                          "heads over config 4's store (8 query heads per kv head); 'ring16' "
                          "is config-4 attention over a store whose residual ring is bf16 (a "
-                         "bf16 model's packed cache); 'copy' is "
+                         "bf16 model's packed cache); 'b1' is config 4's shape for one "
+                         "sequence (B=1: the split plan and its merge); 'copy' is "
                          "a plain 512 MiB device copy for calibrating the FETCH_SIZE / "
                          "WRITE_SIZE counters; 'traffic' is the workload of the counter passes")
     args = ap.parse_args()
@@ -616,6 +618,23 @@ def main():
         torch.cuda.empty_cache()
         if only == "config4":
             return
+
+    if only in (None, "b1"):
+        # ---- one sequence at config 4's shape: 8 (b, kv-head) pairs, so the
+        # plan splits the context (32 splits) and merges the partials
+        B1, Hq1, H1, D1, T1, R1, G1 = 1, *CONFIG4[1:]
+        k, v = synth_kv(B1, H1, T1, D1, 1234 + 41)
+        s1 = make_store(k[:, :, :T1 - 1], v[:, :, :T1 - 1], G1, G1, R1, dev)
+        s1.append(k[:, :, -1:].to(dev), v[:, :, -1:].to(dev))
+        del k, v
+        q = (torch.randn(B1, Hq1, D1, generator=torch.Generator().manual_seed(41))
+             * D1 ** -0.5).to(dev)
+        a1 = time_attention(s1, q, args.attn_iters)
+        log(f"[bench] one sequence (B=1, config 4's heads, context {T1}): {a1['avg_us']:.1f} us "
+            f"per call, {a1['splits']} splits + merge")
+        extra["attention_b1"] = {k_: a1[k_] for k_ in ("avg_us", "gbs", "Tq", "Tr", "splits")}
+        del s1
+        torch.cuda.empty_cache()
 
     if only in (None, "config3"):
         # ---- config 3: MHA, 4096 quantised + 128 residual tokens -----------
