@@ -31,6 +31,8 @@ CASES = [
     (2, 16, 2, 128, 32, 128, 128, 3000, 1, 1, (2500, 17)),           # one split, Gv = D
     (2, 2, 2, 64, 16, 16, 32, 200, 1, 0, (7, 170)),                  # plain layout (generic)
     (2, 8, 2, 64, 16, 16, 32, 200, 4, 3, (0, 150)),                  # generic, multi-token, splits
+    (2, 8, 2, 128, 32, 32, 128, 100, 1, 0, (0, 60)),                 # no chunk yet: window pass
+    (2, 8, 2, 128, 32, 32, 128, 100, 3, 0, (5, 90)),                 # the same, 3 query tokens
 ]
 
 
