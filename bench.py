@@ -635,6 +635,15 @@ def main():
             f"per call, {a1['splits']} splits + merge")
         extra["attention_b1"] = {k_: a1[k_] for k_ in ("avg_us", "gbs", "Tq", "Tr", "splits")}
         del s1
+        # the first steps of a sequence: a 100-token context, all of it still
+        # in the residual window (no chunk yet)
+        k, v = synth_kv(B1, H1, 100, D1, 1234 + 42)
+        s0 = make_store(k, v, G1, G1, R1, dev)
+        assert (s0.n_chunks, s0.res_len) == (0, 100)
+        a0 = time_attention(s0, q, args.attn_iters)
+        log(f"[bench] one sequence, 100 tokens all in the window: {a0['avg_us']:.1f} us per call")
+        extra["attention_b1_window_only"] = {k_: a0[k_] for k_ in ("avg_us", "Tq", "Tr")}
+        del s0, k, v
         torch.cuda.empty_cache()
 
     if only in (None, "config3"):
