@@ -30,7 +30,7 @@ __all__ = [
     "quant_dequant_roundtrip_keys", "quant_dequant_roundtrip_values",
     "quantize_keys_async", "quantize_values_async", "dequantize_keys_async",
     "dequantize_values_async", "quant_dequant_roundtrip_keys_async",
-    "quant_dequant_roundtrip_values_async",
+    "quant_dequant_roundtrip_values_async", "set_lazy_events",
 ]
 
 _DEVICE_TYPE = "cuda"   # ROCm torch reports HIP devices as "cuda"
@@ -219,14 +219,17 @@ class KiviEvent:
 
     ``wait()`` blocks until the work completes and raises ``RuntimeError`` on
     a device-side error; ``query()`` tells, without blocking, whether it has.
-    The HIP event is recorded on the op's stream at the first ``wait()`` or
-    ``query()``, not at submission: the op precedes that point on its stream,
-    so the event completing implies the op has, and an op whose event is
-    never consulted puts no marker between kernels (one per submission cost
-    ~3.7 us of GPU time between two config-2 quantise kernels).  So
-    ``wait()`` also covers work enqueued on the same stream after the op and
-    before the call.  The op's tensors and its stream are kept alive until
-    then."""
+    As in the reference, where the event wraps the submitted kernel's own
+    ``sycl::event`` (kv_cache_ops.cpp:245-303), the HIP event is recorded on
+    the op's stream right after the op is enqueued, so ``wait()`` and
+    ``query()`` cover that op alone, whatever is queued behind it later.
+
+    Lazy recording is opt-in (:func:`set_lazy_events`): the event is then
+    recorded at the first ``wait()`` or ``query()``, which covers the op and
+    any work queued on the same stream after it.  An op whose event is never
+    consulted then puts no marker between kernels (one marker per submission
+    cost ~3.7 us of GPU time between two config-2 quantise kernels).  The
+    op's tensors and its stream are kept alive until the event is released."""
 
     __slots__ = ("_device", "_stream", "_ev", "_keep", "_done")
 
@@ -291,7 +294,23 @@ def _run(device: torch.device, blocking: bool, what: str, fn, *args, keep=()):
         if blocking:
             _native.check(_lib.kivi_stream_synchronize(ctypes.c_void_p(stream.cuda_stream)), what)
             return None
-        return KiviEvent(device, stream, keep)
+        ev = KiviEvent(device, stream, keep)
+        if not _lazy_events:
+            ev._record()
+        return ev
+
+
+_lazy_events = False
+
+
+def set_lazy_events(lazy: bool) -> bool:
+    """Chooses when the ``*_async`` ops record their :class:`KiviEvent`:
+    at submission (the default, the reference's per-op semantics) or, with
+    ``lazy=True``, at the event's first ``wait()``/``query()``.  Returns the
+    previous setting.  Not part of the reference's API."""
+    global _lazy_events
+    prev, _lazy_events = _lazy_events, bool(lazy)
+    return prev
 
 
 # --------------------------------------------------------------------------

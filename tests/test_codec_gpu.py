@@ -258,10 +258,11 @@ def test_async_ops_and_event(C):
                           codec.roundtrip_groups(v.cpu().numpy(), 32).view(np.uint32))
 
 
-def test_event_recorded_at_first_use(C):
-    """An async op's event is recorded at its first wait()/query(), after
-    the op on its stream: waiting then covers the op (and any work queued
-    behind it), repeated calls return at once, and results are exact."""
+def test_event_recorded_at_submission(C):
+    """By default an async op's event is recorded right after the op, as the
+    reference's per-op sycl::event (kv_cache_ops.cpp:245-303): it exists
+    before any wait(), waiting covers that op, repeated calls return at once,
+    and results are exact."""
     import time
     x = seeded_kv((4, 8, 128, 256), seed=23, kind="key")
     xd = x.cuda()
@@ -270,9 +271,10 @@ def test_event_recorded_at_first_use(C):
     scales = torch.empty(n // 32, device="cuda:0")
     zeros = torch.empty(n // 32, device="cuda:0")
     ev = C.quantize_keys_async(xd, packed, scales, zeros, 32)
-    assert ev._ev is None                      # no marker put on the stream yet
+    assert ev._ev is not None                  # marker recorded at submission
     out = torch.empty_like(xd)
     ev2 = C.dequantize_keys_async(packed, scales, zeros, out, 32)   # queued behind it
+    assert ev2._ev is not None and ev2._ev.value != ev._ev.value
     ev.wait()
     assert ev.query() and ev._ev is None       # released after the wait
     ev.wait()                                  # a second wait returns at once
@@ -284,3 +286,36 @@ def test_event_recorded_at_first_use(C):
     ev2.wait()
     ref = codec.dequantize_groups(op, os_, oz, 32).reshape(x.shape)
     assert np.array_equal(_bits(out.cpu()).reshape(-1), ref.view(np.uint32).reshape(-1))
+
+
+def test_lazy_event_recorded_at_first_use(C):
+    """With lazy events switched on, an async op's event is recorded at its
+    first wait()/query(), after the op on its stream: waiting then covers the
+    op (and any work queued behind it), repeated calls return at once, and
+    results are exact."""
+    import time
+    prev = C.set_lazy_events(True)
+    try:
+        x = seeded_kv((4, 8, 128, 256), seed=23, kind="key")
+        xd = x.cuda()
+        n = xd.numel()
+        packed = torch.empty(n // 4, dtype=torch.uint8, device="cuda:0")
+        scales = torch.empty(n // 32, device="cuda:0")
+        zeros = torch.empty(n // 32, device="cuda:0")
+        ev = C.quantize_keys_async(xd, packed, scales, zeros, 32)
+        assert ev._ev is None                      # no marker put on the stream yet
+        out = torch.empty_like(xd)
+        ev2 = C.dequantize_keys_async(packed, scales, zeros, out, 32)   # queued behind it
+        ev.wait()
+        assert ev.query() and ev._ev is None       # released after the wait
+        ev.wait()                                  # a second wait returns at once
+        op, os_, oz = codec.quantize_groups(x.numpy(), 32)
+        assert np.array_equal(packed.cpu().numpy(), op)
+        deadline = time.monotonic() + 30.0
+        while not ev2.query():
+            assert time.monotonic() < deadline, "dequantize never completed"
+        ev2.wait()
+        ref = codec.dequantize_groups(op, os_, oz, 32).reshape(x.shape)
+        assert np.array_equal(_bits(out.cpu()).reshape(-1), ref.view(np.uint32).reshape(-1))
+    finally:
+        C.set_lazy_events(prev)
