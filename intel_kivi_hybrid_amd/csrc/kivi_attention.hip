@@ -456,10 +456,19 @@ int max_lds_bytes() {
 // Rows per kv head of one launch: qlen * hg rounded up to a power of two.
 int rows_for(int n) { return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : 8; }
 
-// Query heads per kv head that one launch covers: all of them up to 8 (the
-// kernels' widest instance); more (multi-query models) take one launch per
-// group of 8, each streaming the store once.
-int heads_per_launch(int hg) { return hg < 8 ? hg : 8; }
+// Widest rows per kv head of one launch: 8 (the kernels' widest instance),
+// except on the matrix-core kernel at head_dim 256 with G = 64 and a run-time
+// value-group count (group_size_v 64 or 128), whose 8-row instance needs more
+// registers than a wave has (it spilled 264 bytes per lane): launches there
+// take 4 rows.
+int max_rows(bool mfma, int D, int G, int Gv) {
+    return (mfma && D == 256 && G == 64 && Gv != 32 && Gv != D) ? 4 : 8;
+}
+
+// Query heads per kv head that one launch covers: all of them up to
+// max_rows; more (multi-query models) take one launch per group of that
+// many, each streaming the store once.
+int heads_per_launch(int hg, int max_r) { return hg < max_r ? hg : max_r; }
 
 // Head and group geometry every decode launch needs, whatever its context.
 int check_geometry(int q_heads, int kv_heads, int head_dim, int group_size_k,
@@ -555,7 +564,8 @@ int kivi_packed_decode_attention_supported(int32_t q_heads, int32_t kv_heads,
                              "group_size_k %d (supported: multiple of 16, <= 64)", group_size_k);
         return kOk;
     }
-    const int lds = attention_mfma_lds_bytes(rows_for(heads_per_launch(q_heads / kv_heads)),
+    const int mr = max_rows(true, head_dim, group_size_k, group_size_v);
+    const int lds = attention_mfma_lds_bytes(rows_for(heads_per_launch(q_heads / kv_heads, mr)),
                                              head_dim, group_size_k, head_dim / group_size_v);
     const int limit = max_lds_bytes();
     if (lds < 0 || lds > limit)
@@ -571,10 +581,10 @@ int kivi_packed_decode_attention_supported(int32_t q_heads, int32_t kv_heads,
 
 namespace {
 
-// Query tokens per launch: as many as fill at most 8 rows per kv head (the
-// kernels' widest instance) and, on the matrix-core kernel, fit its LDS.
+// Query tokens per launch: as many as fill at most max_rows rows per kv head
+// and, on the matrix-core kernel, fit its LDS.
 int tokens_per_launch(int hg, int q_len, bool mfma, int D, int G, int Gv) {
-    int t = max(1, min(8 / hg, q_len));
+    int t = max(1, min(max_rows(mfma, D, G, Gv) / hg, q_len));
     if (mfma) {
         static const int limit = max_lds_bytes();
         while (t > 1 && attention_mfma_lds_bytes(rows_for(t * hg), D, G, D / Gv) > limit) t /= 2;
@@ -591,7 +601,8 @@ size_t workspace_for(int batch, int q_len, int q_heads, int kv_heads, int head_d
     const Plan p = make_plan(batch, kv_heads, head_dim, group_size_k, group_size_v, num_chunks,
                              res_len, num_splits);
     if (!needs_workspace(p)) return 0;
-    const int hl = heads_per_launch(q_heads / kv_heads);
+    const int hl = heads_per_launch(q_heads / kv_heads,
+                                    max_rows(p.mfma, head_dim, group_size_k, group_size_v));
     const int rows = rows_for(
         tokens_per_launch(hl, q_len, p.mfma, head_dim, group_size_k, group_size_v) * hl);
     return (size_t)batch * kv_heads * rows * p.n_splits * (head_dim + 2) * sizeof(float);
@@ -663,7 +674,7 @@ int attention_impl(const float* q, int32_t q_len, int32_t causal, const int32_t*
                           v_scale && v_zero;
     const Plan p = make_plan(batch, kv_heads, head_dim, group_size_k, group_size_v, num_chunks,
                              res_len, num_splits, empty_ok);
-    const int hl = heads_per_launch(hg);
+    const int hl = heads_per_launch(hg, max_rows(p.mfma, head_dim, group_size_k, group_size_v));
     const int tpl = tokens_per_launch(hl, q_len, p.mfma, head_dim, group_size_k, group_size_v);
     const int rows = rows_for(tpl * hl);
     float* part_o = nullptr;
@@ -688,8 +699,8 @@ int attention_impl(const float* q, int32_t q_len, int32_t causal, const int32_t*
         if (rc) return rc;
     }
     const int64_t tok_stride = (int64_t)q_heads * head_dim;      // one query token
-    // One launch per group of up to 8 query heads of each kv head (h0) and
-    // per group of query tokens that fills at most 8 rows (i0).
+    // One launch per group of up to hl query heads of each kv head (h0) and
+    // per group of query tokens that fills at most max_rows rows (i0).
     for (int h0 = 0; h0 < hg; h0 += hl)
     for (int i0 = 0; i0 < q_len; i0 += tpl) {
         QueryRows qr;

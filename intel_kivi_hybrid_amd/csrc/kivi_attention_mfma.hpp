@@ -122,6 +122,26 @@ __device__ __forceinline__ void split_pair(float a, float b, uint32_t& hi, uint3
     lo = pack_bf16x2(la, lb);
 }
 
+// Three pieces: a ~ hi.x + mid.x + lo.x, b likewise (~2^-25 relative).  Each
+// residual is exact in fp32 (the piece taken off is the value rounded to 8
+// significant bits), so only lo's rounding remains.
+__device__ __forceinline__ void split3_pair(float a, float b, uint32_t& hi, uint32_t& mid,
+                                            uint32_t& lo, SplitConsts k) {
+    hi = pack_bf16x2(a, b);
+    const bf16x2_t h2 = __builtin_bit_cast(bf16x2_t, hi);
+    const float ra = __builtin_amdgcn_fdot2_f32_bf16(h2, __builtin_bit_cast(bf16x2_t, k.neg_x), a,
+                                                     false);
+    const float rb = __builtin_amdgcn_fdot2_f32_bf16(h2, __builtin_bit_cast(bf16x2_t, k.neg_y), b,
+                                                     false);
+    mid = pack_bf16x2(ra, rb);
+    const bf16x2_t m2 = __builtin_bit_cast(bf16x2_t, mid);
+    const float sa = __builtin_amdgcn_fdot2_f32_bf16(m2, __builtin_bit_cast(bf16x2_t, k.neg_x), ra,
+                                                     false);
+    const float sb = __builtin_amdgcn_fdot2_f32_bf16(m2, __builtin_bit_cast(bf16x2_t, k.neg_y), rb,
+                                                     false);
+    lo = pack_bf16x2(sa, sb);
+}
+
 // (x & mask) | base.  With both constants opaque (read through
 // readfirstlane) LLVM selects one VOP3 v_and_or_b32 instead of two VOP2 ops
 // with literal operands.  No inline asm here: the result feeds matrix-core
@@ -263,20 +283,34 @@ struct Shape {
     static constexpr int WA_ROW = D + 16;            // bf16 per key A row
     static constexpr int BA_ROW = 32 * NBB + 16;     // bf16 per correction A row
     static constexpr int PA_ROW = G + 16;            // bf16 per value A row
-    // A operands have 16 rows, of which only 2*HG (hi / lo per head) carry
-    // data: the rest are stored once, as one zero row that those lanes read.
+    // Key A factors are split into KP bf16 pieces: hi + mid + lo (~2^-25
+    // relative) with up to 4 query heads per kv head, hi + lo (~2^-17) with
+    // 8, where the 16 A rows are all taken, and in the head_dim-64 G=32
+    // instances with up to 2 query heads per kv head, which run four waves
+    // per SIMD in 128 VGPRs (a third piece spilled there: 16 % slower).
+    // Every code enters the key product as 8 + c and the correction cancels
+    // the 8, so the factors' rounding is amplified ~8x in the scores: with
+    // two pieces at config 4's shape the output error grew with the logits,
+    // to ~1e-3 at a largest score of 64 (natural units); with three it stays
+    // at ~5e-5 up to 256.
+    static constexpr int KP = (HG <= 4 && !(D <= 64 && G <= 32 && HG <= 2)) ? 3 : 2;
+    static constexpr int KROWS = KP * HG;            // key A rows holding data
+    // A operands have 16 rows, of which only KROWS (key) or 2*HG (value: hi
+    // / lo per head) carry data: the rest are stored once, as one zero row
+    // that those lanes read.
+    static constexpr int KAROWS = KROWS < 16 ? KROWS + 1 : 16;
     static constexpr int AROWS = 2 * HG < 16 ? 2 * HG + 1 : 16;
     static constexpr int PA_MAT = AROWS * PA_ROW;    // bf16 per value A matrix (one group)
     static constexpr int PL_ROW = G + 8;             // floats per probability row
     static constexpr int OFF_WA = 0;
-    static constexpr int OFF_BA = OFF_WA + AROWS * WA_ROW * 2;
-    static constexpr int OFF_PA = OFF_BA + AROWS * BA_ROW * 2;
+    static constexpr int OFF_BA = OFF_WA + KAROWS * WA_ROW * 2;
+    static constexpr int OFF_PA = OFF_BA + KAROWS * BA_ROW * 2;
     // The rest depends on the number of value groups NG = D / Gv.
     __host__ __device__ static constexpr int off_pl(int NG) { return OFF_PA + NG * PA_MAT * 2; }
     __host__ __device__ static constexpr int off_al(int NG) { return off_pl(NG) + 2 * HG * PL_ROW * 4; }
     // The value corrections [HG][NG][G/8] fp32 are staged only between
     // whole rings and after the chunk loop, when the key A operands are dead
-    // (every step's key operand build rewrites all 2*HG data rows before its
+    // (every step's key operand build rewrites all KROWS data rows before its
     // scores read them), so they share the key A rows.  That keeps a
     // workgroup at 8 query heads per kv head (head_dim 128, G=32) within
     // 80 KB of LDS: two workgroups per CU instead of one.
@@ -315,7 +349,7 @@ struct Shape {
     static_assert(NP >= 1 && LPH * CPL == D && CPL % 2 == 0, "shape");
     // NG = 1 gives the smallest per-wave region
     static_assert(QRES_LDS <= wave_lds(1) && MERGE_LDS <= qres_off(1), "residual buffers");
-    static_assert(HG * NGMAX * (G / 8) * 4 <= 2 * HG * WA_ROW * 2,
+    static_assert(HG * NGMAX * (G / 8) * 4 <= KROWS * WA_ROW * 2,
                   "value corrections fit in the key A data rows");
 };
 
@@ -699,10 +733,29 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
 #pragma unroll
     for (int i = 0; i < S::NBV; ++i) O[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const int gq = lane / 16, col = lane % 16;
-    const int arow = col < 2 * HG ? col : 2 * HG;     // A-operand row this lane reads
-    float m_run[2] = {-INFINITY, -INFINITY}, l_part[2] = {0.f, 0.f};
-    float m_thr[2] = {-INFINITY, -INFINITY};     // m_run + kRescaleThreshold
-    const bool hvalid[2] = {2 * gq < HG, 2 * gq + 1 < HG};
+    // Value A operands: row 2h / 2h+1 = hi / lo of head h; this lane reads
+    // row col (or the zero row).
+    const int arow = col < 2 * HG ? col : 2 * HG;
+    // Key A operands: with three pieces, row 4h + p holds piece p of head h
+    // and row 4h + 3 reads the zero row, so a lane's four output rows
+    // (4gq..4gq+3) are the pieces of one head, gq; with two, row 2h + p, and
+    // a lane's output rows hold heads 2gq and 2gq+1.  Stored compactly as
+    // rows KP*h + p, the zero row last.
+    constexpr int KP = S::KP, HPL = KP == 3 ? 1 : 2;   // key-side heads per lane
+    const int karow = KP == 3 ? ((col % 4 < 3 && col / 4 < HG) ? 3 * (col / 4) + col % 4
+                                                               : S::KROWS)
+                              : arow;
+    auto khead = [&](int e) { return KP == 3 ? gq : 2 * gq + e; };
+    // online-softmax state of the lane's key-side heads
+    float m_run[HPL], l_part[HPL], m_thr[HPL];     // m_thr = m_run + kRescaleThreshold
+    bool hvalid[HPL];
+#pragma unroll
+    for (int e = 0; e < HPL; ++e) {
+        m_run[e] = -INFINITY;
+        m_thr[e] = -INFINITY;
+        l_part[e] = 0.f;
+        hvalid[e] = khead(e) < HG;
+    }
     float vb[S::NEV];
 #pragma unroll
     for (int it = 0; it < S::NEV; ++it) vb[it] = 0.f;
@@ -743,37 +796,39 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             ks[0] = a2.x; ks[1] = a2.y;
             kz[0] = z2.x; kz[1] = z2.y;
         }
-        uint32_t hi[S::CPL / 2], lo[S::CPL / 2];
+        // pieces [KP][CPL/2] of the lane's channel pairs (hi, mid, lo or hi, lo)
+        uint32_t pc[KP][S::CPL / 2];
         float corr = 0.f;
 #pragma unroll
         for (int j = 0; j < S::CPL / 2; ++j) {
-            split_pair(qv[2 * j] * ks[2 * j], qv[2 * j + 1] * ks[2 * j + 1], hi[j], lo[j], spc);
+            const float xa = qv[2 * j] * ks[2 * j], xb = qv[2 * j + 1] * ks[2 * j + 1];
+            if constexpr (KP == 3) split3_pair(xa, xb, pc[0][j], pc[1][j], pc[2][j], spc);
+            else split_pair(xa, xb, pc[0][j], pc[1][j], spc);
             // (PAIRED: the kz slots hold kz - 8 ks already)
             corr = fmaf(qv[2 * j], PAIRED ? kz[2 * j] : fmaf(-8.f, ks[2 * j], kz[2 * j]), corr);
             corr = fmaf(qv[2 * j + 1],
                         PAIRED ? kz[2 * j + 1] : fmaf(-8.f, ks[2 * j + 1], kz[2 * j + 1]), corr);
         }
-        uint16_t* rhi = WA + (2 * wh) * S::WA_ROW + wseg * S::CPL;
-        uint16_t* rlo = rhi + S::WA_ROW;
-        if constexpr (S::CPL % 8 == 0) {
+        // head wh's rows KP*wh + p, this lane's channels
+        uint16_t* r0 = WA + (KP * wh) * S::WA_ROW + wseg * S::CPL;
 #pragma unroll
-            for (int j = 0; j < S::CPL / 8; ++j) {
-                *reinterpret_cast<u32x4_t*>(rhi + 8 * j) =
-                    u32x4_t{hi[4 * j], hi[4 * j + 1], hi[4 * j + 2], hi[4 * j + 3]};
-                *reinterpret_cast<u32x4_t*>(rlo + 8 * j) =
-                    u32x4_t{lo[4 * j], lo[4 * j + 1], lo[4 * j + 2], lo[4 * j + 3]};
-            }
-        } else {
+        for (int pi = 0; pi < KP; ++pi) {
+            uint16_t* rp = r0 + pi * S::WA_ROW;
+            if constexpr (S::CPL % 8 == 0) {
 #pragma unroll
-            for (int j = 0; j < S::CPL / 2; ++j) {
-                reinterpret_cast<uint32_t*>(rhi)[j] = hi[j];
-                reinterpret_cast<uint32_t*>(rlo)[j] = lo[j];
+                for (int j = 0; j < S::CPL / 8; ++j)
+                    *reinterpret_cast<u32x4_t*>(rp + 8 * j) =
+                        u32x4_t{pc[pi][4 * j], pc[pi][4 * j + 1], pc[pi][4 * j + 2], pc[pi][4 * j + 3]};
+            } else {
+#pragma unroll
+                for (int j = 0; j < S::CPL / 2; ++j) reinterpret_cast<uint32_t*>(rp)[j] = pc[pi][j];
             }
         }
-        uint32_t chi, clo;
-        split_pair(corr, 0.f, chi, clo, spc);
-        BA[(2 * wh) * S::BA_ROW + wseg] = (uint16_t)chi;
-        BA[(2 * wh + 1) * S::BA_ROW + wseg] = (uint16_t)clo;
+        uint32_t cc[3];
+        if constexpr (KP == 3) split3_pair(corr, 0.f, cc[0], cc[1], cc[2], spc);
+        else split_pair(corr, 0.f, cc[0], cc[1], spc);
+#pragma unroll
+        for (int pi = 0; pi < KP; ++pi) BA[(KP * wh + pi) * S::BA_ROW + wseg] = (uint16_t)cc[pi];
     };
 
     // Scores of the chunk's G tokens (matrix cores), then the online softmax:
@@ -787,10 +842,10 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         bf16x8_t Aw[S::KS], Ab[S::NBB];
 #pragma unroll
         for (int ks = 0; ks < S::KS; ++ks)
-            Aw[ks] = *reinterpret_cast<const bf16x8_t*>(WA + arow * S::WA_ROW + 32 * ks + 8 * gq);
+            Aw[ks] = *reinterpret_cast<const bf16x8_t*>(WA + karow * S::WA_ROW + 32 * ks + 8 * gq);
 #pragma unroll
         for (int kb = 0; kb < S::NBB; ++kb)
-            Ab[kb] = *reinterpret_cast<const bf16x8_t*>(BA + arow * S::BA_ROW + 32 * kb + 8 * gq);
+            Ab[kb] = *reinterpret_cast<const bf16x8_t*>(BA + karow * S::BA_ROW + 32 * kb + 8 * gq);
         // The correction is the same for every token: one accumulator, shared
         // as the starting value of every n-block's chain.
         f32x4_t s0 = {0.f, 0.f, 0.f, 0.f};
@@ -811,31 +866,34 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         // A head's running max moves only when its chunk max exceeds it by
         // more than the threshold; that happens iff some lane holds a score
         // above m_run + threshold, so the 16-lane row max is taken only then.
-        float sc[2][NB], alpha[2] = {1.f, 1.f};
+        float sc[HPL][NB], alpha[HPL];
         bool over = false;
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
+        for (int e = 0; e < HPL; ++e) {
+            alpha[e] = 1.f;
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) sc[e][nb] = Sc[nb][2 * e] + Sc[nb][2 * e + 1];
+            for (int nb = 0; nb < NB; ++nb)
+                sc[e][nb] = KP == 3 ? (Sc[nb][2] + Sc[nb][1]) + Sc[nb][0]
+                                    : Sc[nb][2 * e] + Sc[nb][2 * e + 1];
         }
         const int n_masked = kv_lo - chunk * G;       // leading tokens hidden by padding
         if (__builtin_expect(n_masked > 0, 0)) {
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
+            for (int e = 0; e < HPL; ++e) {
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb)
                     sc[e][nb] = 16 * nb + col < n_masked ? -INFINITY : sc[e][nb];
             }
         }
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
+        for (int e = 0; e < HPL; ++e) {
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) over |= hvalid[e] && sc[e][nb] > m_thr[e];
         }
         const bool any = __builtin_amdgcn_ballot_w64(over) != 0;
         if (__builtin_expect(any, 0)) {
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
+            for (int e = 0; e < HPL; ++e) {
                 float cm = sc[e][0];
 #pragma unroll
                 for (int nb = 1; nb < NB; ++nb) cm = fmaxf(cm, sc[e][nb]);
@@ -847,39 +905,58 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                 }
             }
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
+            for (int e = 0; e < HPL; ++e) {
                 l_part[e] *= alpha[e];
+                if (col == 0 && hvalid[e]) AL[slot * 16 + khead(e)] = alpha[e];
+            }
+            // O's rows (value side) are heads 2gq, 2gq+1 of the lane; with one
+            // key-side head per lane their factors come through AL.
+            if constexpr (KP == 3) {
+                wave_sync();
 #pragma unroll
-                for (int nb = 0; nb < S::NBV; ++nb) {
-                    O[nb][2 * e] *= alpha[e];
-                    O[nb][2 * e + 1] *= alpha[e];
+                for (int e = 0; e < 2; ++e) {
+                    const int h = 2 * gq + e;
+                    const float f = h < HG ? AL[slot * 16 + h] : 1.f;
+#pragma unroll
+                    for (int nb = 0; nb < S::NBV; ++nb) {
+                        O[nb][2 * e] *= f;
+                        O[nb][2 * e + 1] *= f;
+                    }
                 }
-                if (col == 0 && hvalid[e]) AL[slot * 16 + 2 * gq + e] = alpha[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+#pragma unroll
+                    for (int nb = 0; nb < S::NBV; ++nb) {
+                        O[nb][2 * e] *= alpha[e];
+                        O[nb][2 * e + 1] *= alpha[e];
+                    }
+                }
             }
         }
         float* pl = PL + slot * (HG * S::PL_ROW);
-        float pv[2][NB];
+        float pv[HPL][NB];
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
+        for (int e = 0; e < HPL; ++e) {
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) pv[e][nb] = exp2_fast(sc[e][nb] - m_run[e]);
         }
         // (a hidden token's weight is 0 even while the running max is -inf)
         if (__builtin_expect(n_masked > 0, 0)) {
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
+            for (int e = 0; e < HPL; ++e) {
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb)
                     pv[e][nb] = 16 * nb + col < n_masked ? 0.f : pv[e][nb];
             }
         }
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
+        for (int e = 0; e < HPL; ++e) {
             float lsum = 0.f;
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
                 lsum += pv[e][nb];
-                if (hvalid[e]) pl[(2 * gq + e) * S::PL_ROW + 16 * nb + col] = pv[e][nb];
+                if (hvalid[e]) pl[khead(e) * S::PL_ROW + 16 * nb + col] = pv[e][nb];
             }
             l_part[e] += lsum;
         }
@@ -1222,9 +1299,9 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         const int e = ilane + 64 * it;
         if (e < n_items) VB[e] = vb[it];          // [h][g][seg]
     }
-    float l_tot[2];
+    float l_tot[HPL];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) l_tot[e] = row_sum16(l_part[e]);
+    for (int e = 0; e < HPL; ++e) l_tot[e] = row_sum16(l_part[e]);
     wave_sync();
     // Gather this wave's value corrections before the merge slot (which
     // overlaps the per-wave LDS) is written.
@@ -1253,10 +1330,13 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
 #pragma unroll
             for (int nb = 0; nb < S::NBV; ++nb)
                 slot[h * D + 16 * nb + col] = O[nb][2 * e] + O[nb][2 * e + 1] + vcorr[e][nb];
-            if (col == 0) {
-                slot[HG * D + h] = m_run[e];
-                slot[HG * D + HG + h] = l_tot[e];
-            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < HPL; ++e) {
+        if (col == 0 && hvalid[e]) {
+            slot[HG * D + khead(e)] = m_run[e];
+            slot[HG * D + HG + khead(e)] = l_tot[e];
         }
     }
     merge_and_store<HG, D>(smem, rstate, a, split, kvh, b);
@@ -1340,7 +1420,10 @@ int launch_ng(const AttnLaunch& a, hipStream_t st) {
                          HG, D, G, Shape<HG, D, G>::lds(D / 32), kMaxLdsBytes);
     }
     if (a.Gv == D) return launch_shape<HG, D, G, 1, R16>(a, st);
-    if constexpr (D > 64) return launch_shape<HG, D, G, 0, R16>(a, st);
+    // (8 rows at head_dim 256, G = 64, would spill: the host plans at most 4
+    // rows per launch there, so this instance is not built)
+    if constexpr (D > 64 && !(HG == 8 && D == 256 && G == 64))
+        return launch_shape<HG, D, G, 0, R16>(a, st);
     return set_error(kErrUnsupported, "group_size_v=%d with head_dim=%d", a.Gv, D);
 }
 

@@ -49,6 +49,7 @@ CASES = [
     (1, 6, 2, 128, 32, 32, 128, 600, 3, 0),      # GQA 3: 2 tokens per launch, 2 padding rows
     (2, 24, 2, 64, 32, 32, 64, 300, 2, 2),       # GQA 12: head groups of 8 and 4, 2 splits
     (1, 14, 2, 64, 16, 16, 32, 100, 3, 0),       # GQA 7, plain layout: the generic kernel
+    (1, 4, 2, 256, 64, 128, 128, 700, 3, 0),     # D=256, G=64, Gv=128: at most 4 rows per launch
 ]
 
 

@@ -204,6 +204,9 @@ def test_attention_reference_cosine_gate(store_cls, kat):
     (2, 4, 2, 64, 32, 32, 64, 900),         # D=64, G=32, GQA 2 (4 waves per SIMD)
     (1, 4, 4, 64, 32, 32, 48, 700),         # D=64, G=32, MHA (4 waves per SIMD)
     (1, 16, 2, 64, 32, 32, 64, 800),        # D=64, G=32, GQA 8
+    (1, 16, 2, 256, 64, 64, 128, 1500),     # GQA 8, D=256, G=64, Gv=64: two 4-head launches
+    (2, 16, 2, 256, 64, 128, 128, 900),     # GQA 8, D=256, G=64, Gv=128: two 4-head launches
+    (1, 12, 2, 256, 64, 128, 128, 900),     # GQA 6, D=256, G=64, Gv=128: 4 + 2 heads
 ])
 def test_attention_matrix_core_shapes(store_cls, B, Hq, Hkv, D, G, Gv, R, T):
     """Every matrix-core instantiation family against float64 attention."""
