@@ -420,7 +420,39 @@ def measure_traffic(algo_bytes, log):
 # --------------------------------------------------------------------------
 # CPU baselines (the reference's CPU path, restated; test infrastructure)
 # --------------------------------------------------------------------------
-def cpu_attention_baseline(k, v, Hq, Tq, G, Gv, B_total, budget_s=10.0):
+def host_info():
+    """The host the CPU baselines ran on: CPU model, logical CPUs, the CPUs
+    this process may use, and torch's intra-op threads."""
+    import torch
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count()
+    return {"cpu_model": model, "nproc": os.cpu_count(), "usable_cpus": usable,
+            "torch_threads": torch.get_num_threads()}
+
+
+def _timed(fn, budget_s, max_n):
+    """Seconds per call of fn(), over about budget_s of calls after one
+    untimed call."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and n < max_n:
+        fn()
+        n += 1
+    return (time.perf_counter() - t0) / n, n
+
+
+def cpu_attention_baseline(k, v, Hq, Tq, G, Gv, B_total, budget_s=8.0):
     """What the reference does per decode step on the CPU: HF-style fp32
     attention (repeat_kv, QK^T*scale, softmax, PV) over the dequantised
     history + fp32 residual served by get_full_cache()
@@ -449,22 +481,25 @@ def cpu_attention_baseline(k, v, Hq, Tq, G, Gv, B_total, budget_s=10.0):
         w = torch.softmax(w, dim=-1)
         return torch.matmul(w, Vx)
 
-    step()
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s and n < 10000:
-        step()
-        n += 1
-    dt = (time.perf_counter() - t0) / n
     nbytes = attn_bytes(nb, Hq, Hkv, D, Tq, Tr, G, Gv)
-    return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+    threads = torch.get_num_threads()
+    dt, n = _timed(step, budget_s, 10000)
+    torch.set_num_threads(1)
+    try:
+        dt1, n1 = _timed(step, budget_s / 2, 10000)
+    finally:
+        torch.set_num_threads(threads)
+    return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": threads,
+            "kind": "port", "single_thread": round(nbytes / dt1 / 1e9, 4),
+            "host": host_info(),
             "sample": f"{nb} of {B_total} sequences x {Hkv} kv heads of the same K/V, context "
-                      f"{T} (Tq={Tq}, Tr={Tr}), {n} steps in {n * dt:.1f}s; torch fp32 "
+                      f"{T} (Tq={Tq}, Tr={Tr}): {n} steps in {n * dt:.1f}s on {threads} "
+                      f"threads, {n1} steps in {n1 * dt1:.1f}s on 1 thread; torch fp32 "
                       f"attention over the dequantised history as the reference's HF model "
                       f"computes it on the CPU"}
 
 
-def cpu_quantize_baseline(kt, v, G, B_total, budget_s=8.0):
+def cpu_quantize_baseline(kt, v, G, B_total, budget_s=6.0):
     """The C oracle (one group per iteration, OpenMP over groups, the
     reference kernels' loop structure) on the first sequences of config 2's
     own K/V (``kt [nb,H,D,Seq]``, ``v [nb,H,Seq,D]``)."""
@@ -472,25 +507,184 @@ def cpu_quantize_baseline(kt, v, G, B_total, budget_s=8.0):
     kn = kt.contiguous().numpy()
     vn = v.contiguous().numpy()
     nb, _, _, S = kt.shape
-    codec.quantize_groups(kn, G)
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s and n < 1000:
+
+    def both():
         codec.quantize_groups(kn, G)
         codec.quantize_groups(vn, G)
-        n += 1
-    dt = (time.perf_counter() - t0) / n
-    return {"value": nb * S / dt / 1e6, "unit": "Mtokens/s", "cores": codec.num_threads(),
-            "kind": "port",
+    threads = codec.num_threads()
+    dt, n = _timed(both, budget_s, 1000)
+    codec.set_num_threads(1)
+    try:
+        dt1, n1 = _timed(both, budget_s / 2, 1000)
+    finally:
+        codec.set_num_threads(threads)
+    return {"value": nb * S / dt / 1e6, "unit": "Mtokens/s", "cores": threads,
+            "kind": "port", "single_thread": round(nb * S / dt1 / 1e6, 4),
+            "host": host_info(),
             "sample": f"keys {list(kt.shape)} + values {list(v.shape)} ({nb} of {B_total} "
-                      f"sequences of config 2's K/V), {n} passes in {n * dt:.1f}s"}
+                      f"sequences of config 2's K/V): {n} passes in {n * dt:.1f}s on "
+                      f"{threads} threads, {n1} in {n1 * dt1:.1f}s on 1 thread"}
+
+
+def cache_loop(cache, k_all, v_all, layers, sync=None):
+    """Config 1's cache workload: one new token per layer per decode step,
+    fed to ``cache`` as a transformers model feeds it in generate()
+    (src/kivi_sycl/generation/generate.py:70-82): the served view
+    (get_full_cache), the model's in-place update of every layer, then
+    add_tokens.  Returns seconds per step."""
+    from transformers import DynamicCache
+    T = k_all.shape[2]
+    if sync:
+        sync()
+    t0 = time.perf_counter()
+    for t in range(T):
+        view = cache.get_full_cache() if t else DynamicCache()
+        for layer in range(layers):
+            view.update(k_all[:, :, t:t + 1], v_all[:, :, t:t + 1], layer)
+        cache.add_tokens(view)
+    if sync:
+        sync()
+    return (time.perf_counter() - t0) / T
+
+
+def cpu_cache_baseline(layers, B, H, D, G, R, T, reps=3):
+    """The reference's KiviCache CPU path restated (oracle/kivi_cache.py,
+    src/kivi_sycl/cache/manager.py:162-374, with the C oracle codec as its
+    round-trip) over config 1's workload; best of ``reps`` runs."""
+    import torch
+    from oracle.kivi_cache import KiviCacheOracle
+    k, v = synth_kv(B, H, T, D, 1234 + 1)
+    best = min(cache_loop(KiviCacheOracle(layers, D, None, G, R), k, v, layers)
+               for _ in range(reps))
+    return {"value": round(1.0 / best, 2), "unit": "decode steps/s",
+            "us_per_step": round(best * 1e6, 1), "cores": torch.get_num_threads(),
+            "kind": "port", "host": host_info(),
+            "sample": f"config 1: {layers} layers, B={B}, H={H}, D={D}, G={G}, R={R}, {T} "
+                      f"decode steps of one token from empty (best of {reps}); the CPU "
+                      f"KiviCache with its fp32 history and the codec round-trip per flush"}
+
+
+# --------------------------------------------------------------------------
+# End to end: the reference's one published figure (README.md:12-20, method
+# examples/benchmark.py:21-145): GPT-2 greedy decoding of 200 tokens with an
+# unquantised DynamicCache against the KIVI cache (G=32, R=64).
+# --------------------------------------------------------------------------
+GPT2_EOS = 50256
+
+
+def e2e_gpt2(dev, n_tokens=200, G=32, R=64, prompt_len=40, log=print):
+    """Seeded random-init GPT-2-small (12 layers, 12 heads, head_dim 64) in
+    fp32 on the GPU (no checkpoint exists offline), a seeded prompt of
+    ``prompt_len`` token ids (no tokenizer: the reference's default prompt is
+    about that long), three arms timed as benchmark.py times them:
+    * fp32: model() with HF's DynamicCache, ``n_tokens`` calls from the
+      prompt, greedy, the end-of-text check every step (benchmark.py:44-57);
+    * kivi: this package's KiviCache (codes, scales, zeros and the residual
+      window in HBM) driven as the reference's generate() drives its cache,
+      the prefill untimed and ``n_tokens - 1`` steps timed
+      (benchmark.py:70-104);
+    * kivi_packed: generate_packed()'s loop, attention read straight from
+      the 2-bit store by the fused kernel, timed the same way.
+    Each arm runs once untimed first.  tok/s = tokens produced / timed
+    seconds (benchmark.py:99-134)."""
+    import torch
+    from transformers import GPT2Config, GPT2LMHeadModel
+    from intel_kivi_hybrid_amd import KiviCache, KiviPackedCache
+    from intel_kivi_hybrid_amd.cache.packed_cache import packed_attention
+    torch.manual_seed(0)
+    model = GPT2LMHeadModel(GPT2Config(n_layer=12, n_head=12, n_embd=768)).eval().to(dev)
+    ids = torch.randint(0, model.config.vocab_size, (1, prompt_len),
+                        generator=torch.Generator().manual_seed(1)).to(dev)
+    nxt = lambda out: out.logits[:, -1, :].argmax(dim=-1).unsqueeze(1)   # noqa: E731
+
+    @torch.no_grad()
+    def fp32(n):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        inp, past, toks = ids, None, []
+        for _ in range(n):
+            out = model(inp, past_key_values=past, use_cache=True)
+            past = out.past_key_values
+            inp = nxt(out)
+            toks.append(inp)
+            if inp.item() == GPT2_EOS:
+                break
+        torch.cuda.synchronize()
+        return toks, time.perf_counter() - t0, None
+
+    @torch.no_grad()
+    def kivi(n):
+        cache = KiviCache.from_model(model, device=dev, group_size=G, residual_length=R)
+        out = model(ids, use_cache=True)
+        cache.add_tokens(out.past_key_values)
+        inp = nxt(out)
+        toks = [inp]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(1, n):
+            out = model(inp, past_key_values=cache.get_full_cache(), use_cache=True)
+            cache.add_tokens(out.past_key_values)
+            inp = nxt(out)
+            toks.append(inp)
+            if inp.item() == GPT2_EOS:
+                break
+        torch.cuda.synchronize()
+        return toks, time.perf_counter() - t0, cache
+
+    @torch.no_grad()
+    def kivi_packed(n):
+        cache = KiviPackedCache.from_model(model, device=dev, group_size=G, residual_length=R)
+        with packed_attention(model):
+            out = model(ids, past_key_values=cache, use_cache=True)
+            inp = nxt(out)
+            toks = [inp]
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(1, n):
+                out = model(inp, past_key_values=cache, use_cache=True)
+                inp = nxt(out)
+                toks.append(inp)
+                if inp.item() == GPT2_EOS:
+                    break
+            torch.cuda.synchronize()
+        return toks, time.perf_counter() - t0, cache
+
+    res, ref_ids = {}, None
+    for name, arm in (("fp32", fp32), ("kivi", kivi), ("kivi_packed", kivi_packed)):
+        arm(8)
+        toks, dt, cache = arm(n_tokens)
+        tids = torch.cat(toks, dim=1)[0].cpu()
+        r = {"tokens": len(toks), "seconds": round(dt, 4), "tok_s": round(len(toks) / dt, 2),
+             "ms_per_token": round(dt / len(toks) * 1e3, 3)}
+        if ref_ids is None:
+            ref_ids = tids
+        else:
+            m = min(len(ref_ids), len(tids))
+            same = (ref_ids[:m] == tids[:m])
+            r["token_match_vs_fp32"] = round(same.float().mean().item(), 4)
+            r["first_divergence"] = int(m if bool(same.all()) else (~same).nonzero()[0, 0])
+            # benchmark.py:124-131: speedup or overhead against the fp32 arm
+            ratio = res["fp32"]["tok_s"] / r["tok_s"]
+            r["overhead_pct_vs_fp32"] = round((ratio - 1) * 100, 1)
+            s0 = cache.get_stats(0)
+            r["layer0_kivi_bytes"], r["layer0_fp32_bytes"] = s0["kivi_bytes"], s0["fp32_bytes"]
+            r["compression"] = round(s0["compression"], 3)
+        res[name] = r
+        log(f"[bench] e2e gpt2 {name}: {r}")
+    res["config"] = {"model": "GPT-2-small shape (12 layers, 12 heads, head_dim 64), seeded "
+                              "random init, fp32, on the GPU", "prompt_tokens": prompt_len,
+                     "new_tokens": n_tokens, "group_size": G, "residual": R}
+    return res
 
 
 # --------------------------------------------------------------------------
 CONFIG4 = (64, 32, 8, 128, 8192, 128, 32)      # B, Hq, Hkv, D, context, R, G
 PRECISION = ("fp32 inputs and outputs; 2-bit codes with fp32 scales/zeros, bit-exact to the "
-             "reference codec; attention products on bf16 matrix cores with each fp32 factor "
-             "split into bf16 hi+lo (~2^-17 relative) and fp32 accumulation; softmax and "
-             "residual window in fp32")
+             "reference codec; attention products on bf16 matrix cores with fp32 accumulation, "
+             "each fp32 key factor split into three bf16 pieces (~2^-25 relative; two, ~2^-17, "
+             "at 8 query heads per kv head) and each value factor into two (~2^-17); softmax "
+             "and residual window in fp32")
+DTYPE = "fp32 I/O; bf16 split-factor MFMA products; fp32 accumulation"
 
 
 def main():
@@ -504,7 +698,7 @@ def main():
                     help="skip the two rocprofv3 counter passes behind roofline.traffic")
     ap.add_argument("--only", choices=["config4", "attention", "gqa8", "ring16", "b1",
                                        "config3", "config5", "codec", "prefill", "copy",
-                                       "traffic"],
+                                       "traffic", "cache1", "e2e"],
                     default=None,
                     help="run one workload (for profiling); 'gqa8' is attention of 64 query "
                          "heads over config 4's store (8 query heads per kv head); 'ring16' "
@@ -512,7 +706,9 @@ def main():
                          "bf16 model's packed cache); 'b1' is config 4's shape for one "
                          "sequence (B=1: the split plan and its merge); 'copy' is "
                          "a plain 512 MiB device copy for calibrating the FETCH_SIZE / "
-                         "WRITE_SIZE counters; 'traffic' is the workload of the counter passes")
+                         "WRITE_SIZE counters; 'traffic' is the workload of the counter passes; "
+                         "'cache1' is config 1's KiviCache loop; 'e2e' is GPT-2 greedy "
+                         "decoding with and without the KIVI cache")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the KIVI hot path here is built and "
@@ -695,6 +891,38 @@ def main():
         del st, sts
         torch.cuda.empty_cache()
 
+    if only in (None, "cache1"):
+        # ---- config 1: the KiviCache loop (12 layers, B=1, H=12, D=64,
+        # R=G=32, 200 steps of one token from empty), cache in HBM
+        from intel_kivi_hybrid_amd import KiviCache
+        L1, B1, H1, D1, G1, R1, T1 = 12, 1, 12, 64, 32, 32, 200
+        k, v = synth_kv(B1, H1, T1, D1, 1234 + 1)
+        k, v = k.to(dev), v.to(dev)
+        runs = []
+        for _ in range(3):
+            c1 = KiviCache(L1, D1, None, device=dev, group_size=G1, residual_length=R1)
+            runs.append(cache_loop(c1, k, v, L1, sync=torch.cuda.synchronize))
+        s1 = c1.get_stats(0)
+        extra["cache_config1"] = {
+            "us_per_step": round(min(runs) * 1e6, 1), "steps_per_s": round(1 / min(runs), 1),
+            "layers": L1, "steps": T1, "flushes": c1.total_flushes,
+            "layer0_kivi_bytes": s1["kivi_bytes"], "layer0_fp32_bytes": s1["fp32_bytes"],
+            "compression": round(s1["compression"], 3),
+            "note": "best of 3 runs; each step: get_full_cache, the model's in-place update "
+                    "of 12 layers (HF DynamicCache), add_tokens with its flushes"}
+        log(f"[bench] config1 KiviCache loop (HBM): {extra['cache_config1']}")
+        del k, v, c1
+        if only == "cache1":
+            if not args.no_cpu_baseline:
+                log(f"[bench] cpu baseline cache: {cpu_cache_baseline(L1, B1, H1, D1, G1, R1, T1)}")
+            return
+
+    if only in (None, "e2e"):
+        extra["e2e_gpt2"] = e2e_gpt2(dev, log=log)
+        torch.cuda.empty_cache()
+        if only == "e2e":
+            return
+
     qb = None
     cpu_kt2 = cpu_v2 = None
     if only in (None, "codec", "prefill"):
@@ -723,12 +951,14 @@ def main():
         return
 
     B, Hq, Hkv, D, T, R, G = CONFIG4
-    cpu = cpu_q = None
+    cpu = cpu_q = cpu_c = None
     if not args.no_cpu_baseline:
         cpu = cpu_attention_baseline(cpu_k4, cpu_v4, Hq, T - R, G, G, B)
         log(f"[bench] cpu baseline attention: {cpu}")
         cpu_q = cpu_quantize_baseline(cpu_kt2, cpu_v2, 32, 8)
         log(f"[bench] cpu baseline quantize: {cpu_q}")
+        cpu_c = cpu_cache_baseline(12, 1, 12, 64, 32, 32, 200)
+        log(f"[bench] cpu baseline cache: {cpu_c}")
     traffic = {"traffic": None, "traffic_note": "not measured (--no-traffic)"}
     if not args.no_traffic:
         traffic = measure_traffic(attn4["bytes"], log)
@@ -745,7 +975,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": DTYPE,
         "precision": PRECISION,
         "data": "synthetic: seeded N(0,1) K/V made on the CPU (4 key channels x10 per kv "
                 "head, 2% of value tokens x8 per sequence and head), copied to HBM before "
@@ -772,6 +1002,7 @@ def main():
                      "avg_us": round(attn4["avg_us"], 2), "bytes_per_launch": attn4["bytes"]},
         "cpu_baseline": cpu,
         "cpu_baseline_quantize": cpu_q,
+        "cpu_baseline_cache": cpu_c,
     }
     line.update(extra)
     print(json.dumps(line), flush=True)

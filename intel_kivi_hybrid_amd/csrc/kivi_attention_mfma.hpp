@@ -285,15 +285,13 @@ struct Shape {
     static constexpr int PA_ROW = G + 16;            // bf16 per value A row
     // Key A factors are split into KP bf16 pieces: hi + mid + lo (~2^-25
     // relative) with up to 4 query heads per kv head, hi + lo (~2^-17) with
-    // 8, where the 16 A rows are all taken, and in the head_dim-64 G=32
-    // instances with up to 2 query heads per kv head, which run four waves
-    // per SIMD in 128 VGPRs (a third piece spilled there: 16 % slower).
-    // Every code enters the key product as 8 + c and the correction cancels
-    // the 8, so the factors' rounding is amplified ~8x in the scores: with
-    // two pieces at config 4's shape the output error grew with the logits,
-    // to ~1e-3 at a largest score of 64 (natural units); with three it stays
-    // at ~5e-5 up to 256.
-    static constexpr int KP = (HG <= 4 && !(D <= 64 && G <= 32 && HG <= 2)) ? 3 : 2;
+    // 8, where the 16 A rows are all taken.  Every code enters the key
+    // product as 8 + c and the correction cancels the 8, so the factors'
+    // rounding is amplified ~8x in the scores: with two pieces the output
+    // error grew with the logits, to ~1e-3 at a largest score of 64 (natural
+    // units) at config 4's shape and at head_dim 64; with three it stays at
+    // ~5e-5 up to 256.
+    static constexpr int KP = HG <= 4 ? 3 : 2;
     static constexpr int KROWS = KP * HG;            // key A rows holding data
     // A operands have 16 rows, of which only KROWS (key) or 2*HG (value: hi
     // / lo per head) carry data: the rest are stored once, as one zero row
@@ -1342,11 +1340,11 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     merge_and_store<HG, D>(smem, rstate, a, split, kvh, b);
 }
 
-// Occupancy target: four waves per SIMD for head_dim 64 with G=32 and up to
-// 2 query heads per kv head (128 VGPRs; the few bytes the compiler spills
-// there are reloaded outside the chunk loop), three with 4 query heads per kv
-// head (at four, spills landed in the chunk loop: 85 us against 70 us at
-// B=64, 32/8 heads, 8K context); two where the 4-deep prefetch ring fits that
+// Occupancy target: three waves per SIMD for head_dim 64 with G=32 and up to
+// 4 query heads per kv head (at four, with up to 2 query heads per kv head
+// and 128 VGPRs, the key operands' third piece spilled: 16 % slower at B=16,
+// 12/12 heads, 8K context; with 4, spills landed in the chunk loop: 85 us
+// against 70 us at B=64, 32/8 heads); two where the 4-deep prefetch ring fits that
 // register budget without spilling (head_dim 64, or head_dim 128 with up to
 // 4 query heads per kv head), which measured faster than three waves with a
 // 2-deep ring.  Head_dim 128 with 8 query heads per kv head and G=32 also
@@ -1356,8 +1354,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
 // the full register file, as does head_dim 256 (one wave per SIMD).
 template <int HG, int D, int G>
 constexpr int attn_waves_per_eu() {
-    return (D <= 64 && G <= 32 && HG <= 2) ? 4
-           : (D <= 64 && G <= 32 && HG <= 4) ? 3
+    return (D <= 64 && G <= 32 && HG <= 4) ? 3
            : (D <= 64 || (D <= 128 && (HG <= 4 || G <= 32))) ? 2 : 1;
 }
 
