@@ -360,12 +360,12 @@ class KiviPackedCache(Cache):
         windows ``k_residual``/``v_residual`` ``[B, Hkv, r, D]`` in the
         ring's type (fp32, or bf16/fp16 for a half-precision model);
         the file metadata holds the format tag, version, cache geometry and
-        per-layer flush counts.  Flushes a multi-token step still owes are
-        done first (the file's windows hold fewer than R tokens)."""
+        per-layer flush counts.  The file holds the cache as the next update
+        will find it: flushes a multi-token step still owes are done on a
+        copy of that layer's store (the file's windows hold fewer than R
+        tokens), and the live cache is left as it was, so a crop() of that
+        step's tokens still works after a save."""
         from safetensors.torch import save_file
-        for lay in self.layers:
-            if lay.is_initialized:
-                lay.settle()
         meta = {"format": FORMAT_NAME, "version": str(FORMAT_VERSION),
                 "num_layers": str(self.num_layers), "head_dim": str(self.head_dim),
                 "num_kv_heads": str(self.num_kv_heads or 0), "group_size": str(self.G),
@@ -375,9 +375,18 @@ class KiviPackedCache(Cache):
             st = self.store(i)
             if st is None:
                 continue
-            for name, t in st.export_state().items():
+            state, flushes = st.export_state(), lay.flushes
+            if st.res_len >= self.R:
+                tmp = _STORE_CLASS.from_state(state, self.G, st.res_len, st.device,
+                                              group_size_v=self.Gv)
+                while tmp.res_len >= self.R:       # settle(), on the copy
+                    tmp.flush()
+                    flushes += 1
+                state = tmp.export_state()
+                del tmp
+            for name, t in state.items():
                 tensors[f"layers.{i}.{name}"] = t.contiguous().cpu()
-            meta[f"layers.{i}.flushes"] = str(lay.flushes)
+            meta[f"layers.{i}.flushes"] = str(flushes)
         save_file(tensors, path, metadata=meta)
 
     @classmethod

@@ -301,8 +301,10 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
 }
 
 // Merge split partials: grid (Hkv * HG, B), one block per partial row
-// (b, kv head, query row v), one thread per channel, dynamic LDS of 2*S
-// floats.  The S (m, l) pairs are read in parallel (one per thread) and
+// (b, kv head, query row v), one thread per channel rounded up to whole
+// waves (lanes past D take part in the reductions with -inf and store
+// nothing; a partial wave would feed its inactive lanes' zeros into the
+// shuffles), dynamic LDS of 2*S floats.  The S (m, l) pairs are read in parallel (one per thread) and
 // turned into weights f_s = 2^(m_s - M) in LDS; each thread then sums its
 // channel over the S partial rows with every load in flight at once (the
 // loop is unrolled), so the kernel costs about two memory round trips
@@ -745,7 +747,9 @@ int attention_impl(const float* q, int32_t q_len, int32_t causal, const int32_t*
         }
         if (rc) return rc;
         if (needs_workspace(p)) {
-            attn_merge_kernel<<<dim3(kv_heads * rows, batch), head_dim,
+            // whole waves: the (m, l) reduction reads every lane of a wave
+            const int merge_threads = (head_dim + kWave - 1) / kWave * kWave;
+            attn_merge_kernel<<<dim3(kv_heads * rows, batch), merge_threads,
                                 2 * p.n_splits * sizeof(float), st>>>(
                 part_o, part_ml, oi, qr, q_heads, rows, head_dim, p.n_splits);
             rc = check_launch("packed_attention_merge");

@@ -234,3 +234,20 @@ def test_noalloc_rejects_oversize_partials_on_host():
     assert rc == 1
     msg = _native.last_error()
     assert "allocation-free entry point holds at most 8388608" in msg, msg
+
+
+def test_noalloc_refuses_oversized_split_partials():
+    """The allocation-free entry point refuses, before anything runs (so on
+    a host without a GPU too), a launch whose split partials exceed its
+    static scratch array: an explicit 64-way split at config 4's shape needs
+    64 x 8 x 4 rows x 64 splits x (128 + 2) floats = 68 MB > 8 MiB."""
+    from intel_kivi_hybrid_amd import _native
+    lib = _native.load()
+    lib.kivi_clear_error()
+    null = ctypes.c_void_p(0)
+    rc = lib.kivi_packed_decode_attention_noalloc(
+        null, null, null, null, null, null, null, null, null, 0, null,
+        64, 32, 8, 128, 32, 32, 300, 252, 128, 0, 128, 0.088, 64, null)
+    assert rc == 1                                   # KIVI_ERR_INVALID_ARGUMENT
+    msg = _native.last_error()
+    assert "split partials" in msg and str(8 << 20) in msg, msg

@@ -260,3 +260,27 @@ def test_split_workspace_reuse(store_cls):
             if first is None:
                 first = o.copy()
             assert np.array_equal(o.view(np.uint32), first.view(np.uint32))
+
+
+def test_split_merge_head_dim_96_negative_scores(store_cls):
+    """head_dim 96 (a plain-layout store: the generic kernel) with forced
+    splits: the merge kernel's blocks are whole waves, so its (m, l)
+    reduction is right even when every split's maximum score lies far below
+    zero (here about -160 in log2 units), where a partial wave's inactive
+    lanes used to pull the maximum up to 0 and every weight underflowed."""
+    B, Hq, Hkv, D, G, R, T = 1, 2, 2, 96, 32, 32, 300
+    k, v = make_kv(B, Hkv, T, D, seed=96)
+    k = k.abs() + 5.0                                 # every key component positive
+    st = store_cls(B, Hkv, D, G, R, "cuda:0")
+    assert st.code_layout == 0
+    fill_store(st, k, v, R)
+    q = torch.full((B, Hq, D), -2.0)                  # scores ~ -2 * sum(k) / sqrt(D)
+    kh, vh = oracle_history(k, v, st.n_chunks, G, G)
+    q0 = st.n_chunks * G
+    ref = decode_attention(q.numpy(), kh, vh, k[:, :, q0:].numpy(), v[:, :, q0:].numpy())
+    for splits in (4, 7):
+        out = st.attention(q.cuda(), num_splits=splits).cpu().numpy()
+        assert np.isfinite(out).all()
+        err = rel_err(out, ref)
+        print(f"[attn] D=96 negative scores, {splits} splits: rel_err={err:.3e}", flush=True)
+        assert err <= ATTN_TOL

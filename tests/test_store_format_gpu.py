@@ -129,3 +129,53 @@ def test_saved_cache_resumes_decoding(hip_device, tmp_path):
             assert torch.equal(oa.logits, ob.logits)
             na = oa.logits[:, -1:].argmax(-1)
             nb = ob.logits[:, -1:].argmax(-1)
+
+
+def test_save_leaves_a_pending_step_croppable(hip_device, tmp_path):
+    """A multi-token step takes the window past R and leaves its flushes to
+    the next update.  save() writes the settled state (the file's windows
+    hold fewer than R tokens, and the loaded cache decodes as the settled
+    one) without settling the live cache, so a crop() of that step's
+    tokens still works after the save and the cache then continues exactly
+    as a twin that was never saved."""
+    from transformers import GPT2Config, GPT2LMHeadModel
+    from intel_kivi_hybrid_amd.cache.packed_cache import KiviPackedCache, packed_attention
+    torch.manual_seed(6)
+    model = GPT2LMHeadModel(GPT2Config(n_layer=2, n_head=4, n_embd=256)).eval().to(hip_device)
+    gen = torch.Generator().manual_seed(2)
+    ids = torch.randint(0, model.config.vocab_size, (1, 60), generator=gen).to(hip_device)
+    draft = torch.randint(0, model.config.vocab_size, (1, 7), generator=gen).to(hip_device)
+    G, R = 32, 32
+    a = KiviPackedCache.from_model(model, device="cuda:0", group_size=G, residual_length=R)
+    twin = KiviPackedCache.from_model(model, device="cuda:0", group_size=G, residual_length=R)
+    with torch.no_grad(), packed_attention(model):
+        for c in (a, twin):
+            model(ids, past_key_values=c, use_cache=True)
+            model(draft, past_key_values=c, use_cache=True)
+        res_before = a.store(0).res_len
+        assert res_before >= R                      # the step's flushes are still owed
+        path = str(tmp_path / "pending.safetensors")
+        a.save(path)
+        assert a.store(0).res_len == res_before     # the live cache is untouched
+        b = KiviPackedCache.load(path, device="cuda:0")
+        assert b.store(0).res_len < R and b.get_seq_length() == a.get_seq_length()
+        owed = (res_before - R) // G + 1              # per layer, as settle() does them
+        assert b.total_flushes == a.total_flushes + model.config.n_layer * owed
+        # the settled file decodes as the unsaved cache does after its update
+        nxt = draft[:, -1:]
+        ob = model(nxt, past_key_values=b, use_cache=True)
+        ot = model(nxt, past_key_values=twin, use_cache=True)
+        assert torch.equal(ob.logits, ot.logits)
+        # the saved cache can still drop the step's rejected tokens
+        a.crop(-5)
+        twin2 = KiviPackedCache.from_model(model, device="cuda:0", group_size=G,
+                                           residual_length=R)
+        model(ids, past_key_values=twin2, use_cache=True)
+        model(draft, past_key_values=twin2, use_cache=True)
+        twin2.crop(-5)
+        n = draft[:, 1:2]
+        for _ in range(20):
+            oa = model(n, past_key_values=a, use_cache=True)
+            o2 = model(n, past_key_values=twin2, use_cache=True)
+            assert torch.equal(oa.logits, o2.logits)
+            n = oa.logits[:, -1:].argmax(-1)

@@ -80,3 +80,14 @@ def test_noalloc_matches_workspace_entry_point(hip_device):
     assert 0 < need2 < need1
     # a single split needs no partials at all
     assert _case(lib, 1, 8, 2, 128, 32, 32, 64, 500, splits=1, seed=13) == 0
+
+
+def test_noalloc_plain_layout_and_wide_head_groups(hip_device):
+    """The generic kernel (a plain-layout store: G = 16) and more than 8
+    query heads per kv head (12: launches over head groups of 8 and 4, each
+    leaving its partials in the same scratch array before its merge), split,
+    against the workspace entry point bit for bit."""
+    from intel_kivi_hybrid_amd import _native
+    lib = _native.load()
+    _case(lib, 2, 4, 2, 64, 16, 16, 32, 600, splits=5, seed=14)
+    _case(lib, 2, 24, 2, 128, 32, 32, 64, 1500, splits=3, seed=15)
