@@ -257,7 +257,6 @@ struct Shape {
     static constexpr int CPL = D / LPH;              // channels per W-prep lane
     static constexpr int NBB = (LPH + 31) / 32;      // bias k-steps
     static constexpr int NGMAX = D / 32;             // value groups (Gv >= 32)
-    static constexpr int NEV = (HG * (G / 8) * NGMAX + 63) / 64;   // P-prep items per lane
     // chunk metadata: ks [D], kz [D], vs [NG][G], vz [NG][G] as float4s
     static constexpr int META4_MAX = (2 * D + 2 * NGMAX * G) / 4;
     static constexpr int NMETA = (META4_MAX + 63) / 64;      // float4 loads per lane
@@ -583,7 +582,20 @@ __device__ __forceinline__ void stage_meta(const ChunkRegs<S>& r, float* MT, int
 // R16: the residual ring holds bf16 or fp16 (a.res_dt) instead of fp32.
 template <class S, int NGC, bool R16>
 __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, int kvh, int b) {
-    constexpr int HG = S::HG, D = S::D, G = S::G, NSUB = S::NSUB, NB = G / 16, NSEG = G / 8;
+    constexpr int HG = S::HG, D = S::D, G = S::G, NSUB = S::NSUB, NB = G / 16;
+    // Value operand items: (head, value group, TPI tokens).  8 tokens per
+    // item where the chunk has at least 64 of them; otherwise 2, so that the
+    // operand build spreads over the wave instead of leaving most lanes idle
+    // (one value group per token at 4 query heads per kv head has 16 items
+    // of 8 tokens; MHA with 4 groups has 16).  With 2 tokens an item's
+    // (head, group) spans whole 16-lane rows (G/2 items, consecutive), whose
+    // value corrections are summed across the row before they are staged.
+    constexpr int NGI = NGC > 0 ? NGC : S::NGMAX;
+    constexpr int TPI = HG * NGI * (G / 8) >= 64 ? 8 : 2;
+    constexpr int NSEG = G / TPI;                       // items per (head, group)
+    constexpr int NSEGV = TPI == 8 ? NSEG : NSEG / 16;   // staged corrections per (head, group)
+    constexpr int NEV = (HG * NSEG * NGI + 63) / 64;    // items per lane
+    static_assert(TPI == 8 || NSEG % 16 == 0, "two-token items fill whole 16-lane rows");
     // wave-uniform in an SGPR: chunk ranges, ring indices and branches on
     // them stay scalar
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -754,9 +766,9 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         l_part[e] = 0.f;
         hvalid[e] = khead(e) < HG;
     }
-    float vb[S::NEV];
+    float vb[NEV];
 #pragma unroll
-    for (int it = 0; it < S::NEV; ++it) vb[it] = 0.f;
+    for (int it = 0; it < NEV; ++it) vb[it] = 0.f;
     const int n_items = HG * NSEG * NG;
 
     const UnpackConsts uc = unpack_consts();
@@ -962,36 +974,58 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     };
 
     // Value A operands: rows 2h / 2h+1 = hi / lo of p[h,t]*vs[t,g] for each
-    // group g, one item = (head, group, 8 tokens); value corrections p*(vz-8vs).
-    // Item geometry is fixed per lane: LDS offsets are computed once here.
-    int it_valid[S::NEV], it_h[S::NEV], it_pl[S::NEV], it_pa[S::NEV];
-    int it_mv[S::NEV], it_mv2[S::NEV], it_mz[S::NEV], it_mz2[S::NEV];
-    // Items are numbered so that the 16 lanes of each ds_read_b128 cycle take
-    // 16 consecutive items: lanes {0-3, 12-15, 20-27} -> 0-15 and
-    // {4-11, 16-19, 28-31} -> 16-31 of each half-wave.
-    const int ilane = item_lane(lane);
+    // group g, one item = (head, group, TPI tokens); value corrections
+    // p*(vz-8vs).  Item geometry is fixed per lane: LDS offsets are computed
+    // once here.
+    int it_valid[NEV], it_h[NEV], it_pl[NEV], it_pa[NEV], it_vb[NEV];
+    int it_mv[NEV], it_mv2[NEV], it_mz[NEV], it_mz2[NEV];
+    // 8-token items are numbered so that the 16 lanes of each ds_read_b128
+    // cycle take 16 consecutive items: lanes {0-3, 12-15, 20-27} -> 0-15 and
+    // {4-11, 16-19, 28-31} -> 16-31 of each half-wave.  2-token items are
+    // lane-ordered (their (head, group) rows must be DPP rows).
+    const int ilane = TPI == 8 ? item_lane(lane) : lane;
 #pragma unroll
-    for (int it = 0; it < S::NEV; ++it) {
+    for (int it = 0; it < NEV; ++it) {
         const int e = ilane + 64 * it;
         const int h = e / (NSEG * NG), rem = e % (NSEG * NG);
         const int g = rem / NSEG, seg = rem % NSEG;
         it_valid[it] = e < n_items;
         it_h[it] = h;
-        it_pl[it] = h * S::PL_ROW + 8 * seg;               // into PL[slot]
-        const int vs0 = (2 * D + g * G + 8 * seg) / 4;     // float4 slot of vs
-        it_mv[it] = 4 * S::meta_slot(vs0);                 // vs[0..3]; +4 slot for [4..7]
-        it_mv2[it] = 4 * S::meta_slot(vs0 + 1);
-        it_mz[it] = 4 * S::meta_slot(vs0 + NG * G / 4);    // vz
-        it_mz2[it] = 4 * S::meta_slot(vs0 + NG * G / 4 + 1);
-        it_pa[it] = g * S::PA_MAT + 8 * seg + 2 * h * S::PA_ROW;
+        it_pl[it] = h * S::PL_ROW + TPI * seg;             // into PL[slot]
+        // staged value correction: one per item, or per 16-item row
+        it_vb[it] = TPI == 8 ? e : (seg % 16 == 0 ? (h * NG + g) * NSEGV + seg / 16 : -1);
+        const int fv = 2 * D + g * G + TPI * seg;          // float index of vs
+        if constexpr (TPI == 8) {
+            it_mv[it] = 4 * S::meta_slot(fv / 4);          // vs[0..3]; +4 slot for [4..7]
+            it_mv2[it] = 4 * S::meta_slot(fv / 4 + 1);
+            it_mz[it] = 4 * S::meta_slot((fv + NG * G) / 4);    // vz
+            it_mz2[it] = 4 * S::meta_slot((fv + NG * G) / 4 + 1);
+        } else {                                           // a float2 within one slot
+            it_mv[it] = 4 * S::meta_slot(fv / 4) + fv % 4;
+            it_mz[it] = 4 * S::meta_slot((fv + NG * G) / 4) + (fv + NG * G) % 4;
+            it_mv2[it] = it_mz2[it] = 0;
+        }
+        it_pa[it] = g * S::PA_MAT + TPI * seg + 2 * h * S::PA_ROW;
     }
     auto pprep = [&](auto slot_c, bool any) {
         constexpr int slot = decltype(slot_c)::value;
         const float* pl = PL + slot * (HG * S::PL_ROW);
         const float* mt = MT + slot * meta_stride;
 #pragma unroll
-        for (int it = 0; it < S::NEV; ++it) {
-            if (it_valid[it]) {
+        for (int it = 0; it < NEV; ++it) {
+            if (TPI == 2 && it_valid[it]) {
+                if (any) vb[it] *= AL[slot * 16 + it_h[it]];
+                const float2 p = *reinterpret_cast<const float2*>(pl + it_pl[it]);
+                const float2 vs = *reinterpret_cast<const float2*>(mt + it_mv[it]);
+                const float2 vz = *reinterpret_cast<const float2*>(mt + it_mz[it]);
+                uint32_t h2, l2;
+                split_pair(p.x * vs.x, p.y * vs.y, h2, l2, spc);
+                float acc = fmaf(p.x, PAIRED ? vz.x : fmaf(-8.f, vs.x, vz.x), vb[it]);
+                vb[it] = fmaf(p.y, PAIRED ? vz.y : fmaf(-8.f, vs.y, vz.y), acc);
+                uint16_t* base = PA + it_pa[it];
+                *reinterpret_cast<uint32_t*>(base) = h2;
+                *reinterpret_cast<uint32_t*>(base + S::PA_ROW) = l2;
+            } else if (TPI == 8 && it_valid[it]) {
                 if (any) vb[it] *= AL[slot * 16 + it_h[it]];
                 const float4 pa = *reinterpret_cast<const float4*>(pl + it_pl[it]);
                 const float4 pb = *reinterpret_cast<const float4*>(pl + it_pl[it] + 4);
@@ -1242,16 +1276,20 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // pprep then scales zeros.
     constexpr int kFoldChunks = 16;
     constexpr int kFoldRings = kFoldChunks / PF > 0 ? kFoldChunks / PF : 1;
-    auto fold_vcorr = [&]() {
-        wave_sync();
+    // Stages the lanes' value corrections in VB ([h][g][NSEGV]) and clears
+    // them; `rescale`: apply the pending rescale of AL slot 0 first.
+    auto stage_vcorr = [&](bool rescale) {
 #pragma unroll
-        for (int it = 0; it < S::NEV; ++it) {
-            if (it_valid[it]) {
-                const float x = any_cur ? vb[it] * AL[it_h[it]] : vb[it];
-                VB[ilane + 64 * it] = x;          // [h][g][seg]
-            }
+        for (int it = 0; it < NEV; ++it) {
+            float x = it_valid[it] ? (rescale && any_cur ? vb[it] * AL[it_h[it]] : vb[it]) : 0.f;
+            if constexpr (TPI == 2) x = row_sum16(x);     // a row is one (head, group)
+            if (it_valid[it] && it_vb[it] >= 0) VB[it_vb[it]] = x;
             vb[it] = 0.f;
         }
+    };
+    auto fold_vcorr = [&]() {
+        wave_sync();
+        stage_vcorr(true);
         wave_sync();
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
@@ -1259,10 +1297,10 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             if (h < HG) {
 #pragma unroll
                 for (int nb = 0; nb < S::NBV; ++nb) {
-                    const float* pv = VB + (h * NG + (16 * nb + col) / Gv) * NSEG;
+                    const float* pv = VB + (h * NG + (16 * nb + col) / Gv) * NSEGV;
                     float v = 0.f;
 #pragma unroll
-                    for (int sg = 0; sg < NSEG; ++sg) v += pv[sg];
+                    for (int sg = 0; sg < NSEGV; ++sg) v += pv[sg];
                     O[nb][2 * e] += v;
                 }
             }
@@ -1292,11 +1330,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     });
     // ---- wave state -> merge slot --------------------------------------------
     wave_sync();
-#pragma unroll
-    for (int it = 0; it < S::NEV; ++it) {
-        const int e = ilane + 64 * it;
-        if (e < n_items) VB[e] = vb[it];          // [h][g][seg]
-    }
+    stage_vcorr(false);
     float l_tot[HPL];
 #pragma unroll
     for (int e = 0; e < HPL; ++e) l_tot[e] = row_sum16(l_part[e]);
@@ -1312,9 +1346,9 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             float v = 0.f;
             if (h < HG) {
                 const int g = (16 * nb + col) / Gv;
-                const float* pv = VB + (h * NG + g) * NSEG;
+                const float* pv = VB + (h * NG + g) * NSEGV;
 #pragma unroll
-                for (int sg = 0; sg < NSEG; ++sg) v += pv[sg];
+                for (int sg = 0; sg < NSEGV; ++sg) v += pv[sg];
             }
             vcorr[e][nb] = v;
         }
