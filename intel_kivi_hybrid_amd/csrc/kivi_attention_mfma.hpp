@@ -16,19 +16,32 @@
 // contractions run as bf16 MFMAs (v_mfma_f32_16x16x32_bf16) with fp32
 // accumulation:
 //
-// * B operands are the codes themselves.  The store keeps each lane's codes
-//   in MFMA operand order (kLayoutMfma), and a code c becomes the bf16 value
-//   8 + c (exponent of 8, c in mantissa bits 5:4) with one shift and one
-//   and-or per two codes.  Integers 8..11 are exact in bf16.
-// * A operands carry the fp32 factors split into bf16 hi + lo rows
-//   (x ~ hi + lo to 2^-17 relative): rows 2h/2h+1 of the key A matrix are
-//   q[h,d]*ks[d], rows of the value A matrix are p[h,t]*vs[t,g].
-// * The constant parts fold into corrections that are linear in the data:
-//     s[h,t] = sum_d (q ks)[h,d] (8 + c) + sum_d q[h,d] (kz[d] - 8 ks[d])
-//     o[h,d] = sum_t (p vs)[h,t] (8 + c') + sum_t p[h,t] (vz[t] - 8 vs[t])
-//   The key correction enters the MFMA as extra k-steps against a B of ones
-//   (so it is summed across lanes by the matrix core); the value correction
-//   is accumulated per lane and added once at the end.
+// * B operands are the codes themselves, read in place.  The store keeps each
+//   lane's codes in MFMA operand order (kLayoutMfma): the codes of operand
+//   dword k sit at bits 2k..2k+1 of the low byte of each 16-bit half (tile
+//   0; tile 1 one byte up).  A half holding nothing but c << 2k is the bf16
+//   bit pattern of c * 2^(2k-133), exactly: bf16 patterns below 256 are the
+//   integers 0..255 times 2^-133 (subnormals, continued by the first normal
+//   binade).  So an operand dword is one AND of the code word (tile 1: of
+//   the word shifted down a byte), and the matrix cores, which take
+//   subnormal bf16 inputs exactly on gfx950, multiply by c itself.
+// * A operands carry the fp32 factors split into bf16 pieces (hi + mid + lo,
+//   ~2^-25 relative, or hi + lo, ~2^-17): the key A matrix holds
+//   q[h,d]*ks[d], the value A matrix p[h,t]*vs[t,g], each scaled by
+//   2^(133-2k-64) for its operand position k (kCodeScale), so that products
+//   come out in units of 2^-64.  The scales are multiplied by those powers of
+//   two once, when a chunk's metadata is staged.
+// * The zeros fold into corrections that are linear in the data:
+//     s[h,t] = sum_d (q ks)[h,d] c + sum_d q[h,d] kz[d]
+//     o[h,d] = sum_t (p vs)[h,t] c' + sum_t p[h,t] vz[t]
+//   The key correction enters the MFMA as extra k-steps against a B operand
+//   of 2^-64s (so it is summed across lanes by the matrix core, in the same
+//   units); the value correction is accumulated per lane and added at the
+//   end.  Scores and the output are scaled back by 2^64.
+//   The units bound the factors: the key product q*ks*softmax_scale*log2(e)
+//   and the key scale below 2^59, value scales below 2^51 (larger ones
+//   overflow the A operand to inf).  Value codes' products below ~2^-38
+//   lose relative precision (fp32 subnormals).
 //
 // Work split: each wave owns a contiguous range of chunks of one
 // (batch, kv-head) and keeps an online softmax over it in the log2 domain
@@ -142,54 +155,32 @@ __device__ __forceinline__ void split3_pair(float a, float b, uint32_t& hi, uint
     lo = pack_bf16x2(sa, sb);
 }
 
-// (x & mask) | base.  With both constants opaque (read through
-// readfirstlane) LLVM selects one VOP3 v_and_or_b32 instead of two VOP2 ops
-// with literal operands.  No inline asm here: the result feeds matrix-core
-// operands, and the compiler must see the VALU write to insert the wait
-// states a VALU-write -> MFMA-read dependency needs.
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t base) {
-    return (x & mask) | base;
-}
-
-// Code word -> B operand (four dwords of two bf16 "8 + c" each) for tile
-// 2w + M of the word (element j at bit mfma_code_bit(M, j)).
-// The mask lives in an SGPR and the base in a VGPR (a VOP3 op reads at most
-// one SGPR); both come from unpack_consts(), called once per wave.
-struct UnpackConsts {
-    uint32_t mask, base;
-};
-__device__ __forceinline__ UnpackConsts unpack_consts() {
-    UnpackConsts c;
-    c.mask = __builtin_amdgcn_readfirstlane(0x00300030u);
-    c.base = 0x41004100u;
-    // emits nothing; hides the base's value so that it stays in one VGPR
-    // instead of being rematerialised at every use
-    asm("" : "+v"(c.base));
-    return c;
-}
-
-// Code word -> B operand of tile M (four dwords of two bf16 "8 + c" each).
-// Element j of the tile sits at bit 8M + 2(j/2) of the low (j even) or high
-// (j odd) half of the word and is moved to mantissa bits 5:4.  (Reading some
-// codes at lower mantissa bits saves shifts but needs an MFMA against -8 per
-// operand to keep the precision; at ~8 VALU ops per MFMA of issue time that
-// measured slower.)
+// Code word -> B operand of tile M (four dwords of two bf16 each).  Element j
+// of the tile sits at bit 8M + 2(j/2) of the low (j even) or high (j odd)
+// half of the word; dword k keeps bits 2k..2k+1 of each half of the word
+// (tile 1: shifted down 8 bits), i.e. the values c * 2^(2k-133).  Plain
+// C++, no inline asm: the result feeds matrix-core operands, and the
+// compiler must see the VALU write to insert the wait states a VALU-write ->
+// MFMA-read dependency needs.  (The earlier form, 8 + c with c moved to
+// mantissa bits 5:4, took a shift and an and-or per dword: 15 VALU per word
+// against 9.)
 template <int M>
-__device__ __forceinline__ bf16x8_t unpack_codes(uint32_t x, UnpackConsts k) {
-    u32x4_t o;
-    if constexpr (M == 0) {
-        o[0] = and_or(x << 4, k.mask, k.base);
-        o[1] = and_or(x << 2, k.mask, k.base);
-        o[2] = and_or(x, k.mask, k.base);
-        o[3] = and_or(x >> 2, k.mask, k.base);
-    } else {
-        o[0] = and_or(x >> 4, k.mask, k.base);
-        o[1] = and_or(x >> 6, k.mask, k.base);
-        o[2] = and_or(x >> 8, k.mask, k.base);
-        o[3] = and_or(x >> 10, k.mask, k.base);
-    }
+__device__ __forceinline__ bf16x8_t unpack_codes(uint32_t x) {
+    const uint32_t y = M == 0 ? x : x >> 8;
+    const u32x4_t o = {y & 0x00030003u, y & 0x000c000cu, y & 0x00300030u, y & 0x00c000c0u};
     return __builtin_bit_cast(bf16x8_t, o);
 }
+
+// Units of the products: A factors at operand position k carry
+// 2^(kCodeExp - 2k - kProdExp) (kCodeExp = 133 undoes the code operand's
+// 2^(2k-133)), so every matrix-core product and accumulator is the true
+// value times 2^-kProdExp.
+constexpr int kCodeExp = 133;
+constexpr int kProdExp = 64;
+constexpr float kProdUnit = 0x1p-64f;      // 2^-kProdExp
+constexpr float kProdScale = 0x1p64f;      // 2^kProdExp
+constexpr uint32_t kProdUnitBf16x2 = 0x1F801F80u;   // (2^-64, 2^-64) in bf16
+static_assert(kCodeExp - kProdExp == 69, "code scale constants below");
 
 __device__ __forceinline__ f32x4_t mfma(bf16x8_t a, bf16x8_t b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -255,7 +246,7 @@ struct Shape {
     static constexpr int NBV = D / 16;               // value n-blocks
     static constexpr int LPH = (64 / HG < D / 2) ? 64 / HG : D / 2;   // W-prep lanes per head
     static constexpr int CPL = D / LPH;              // channels per W-prep lane
-    static constexpr int NBB = (LPH + 31) / 32;      // bias k-steps
+    static constexpr int NBB = (LPH + 31) / 32;      // correction k-steps
     static constexpr int NGMAX = D / 32;             // value groups (Gv >= 32)
     // chunk metadata: ks [D], kz [D], vs [NG][G], vz [NG][G] as float4s
     static constexpr int META4_MAX = (2 * D + 2 * NGMAX * G) / 4;
@@ -284,12 +275,11 @@ struct Shape {
     static constexpr int PA_ROW = G + 16;            // bf16 per value A row
     // Key A factors are split into KP bf16 pieces: hi + mid + lo (~2^-25
     // relative) with up to 4 query heads per kv head, hi + lo (~2^-17) with
-    // 8, where the 16 A rows are all taken.  Every code enters the key
-    // product as 8 + c and the correction cancels the 8, so the factors'
-    // rounding is amplified ~8x in the scores: with two pieces the output
-    // error grew with the logits, to ~1e-3 at a largest score of 64 (natural
-    // units) at config 4's shape and at head_dim 64; with three it stays at
-    // ~5e-5 up to 256.
+    // 8, where the 16 A rows are all taken.  The scores' error grows with
+    // their size: with codes entering as 8 + c (an earlier operand form,
+    // whose correction cancelled the 8 and so amplified the factors' rounding
+    // ~8x) and two pieces, the output error reached ~1e-3 at a largest score
+    // of 64 (natural units) at config 4's shape and at head_dim 64.
     static constexpr int KP = HG <= 4 ? 3 : 2;
     static constexpr int KROWS = KP * HG;            // key A rows holding data
     // A operands have 16 rows, of which only KROWS (key) or 2*HG (value: hi
@@ -442,9 +432,9 @@ struct ChunkSrc {
 
 // Paired metadata sweep (PAIRED): the first NMETA/2 float4s of a lane are
 // scales, from [ks | vs], and the last NMETA/2 the zeros of the same
-// channels or tokens, from [kz | vz], so that the lane can stage
-// zero - 8*scale (the correction terms' factor) in place of the zero.  Used
-// where it needs no more loads per lane than the plain sweep.
+// channels or tokens, from [kz | vz]: a lane's scale float4s are then known
+// at compile time (they alone are multiplied when staged).  Used where it
+// needs no more loads per lane than the plain sweep.
 template <class S>
 constexpr bool paired_meta(int NG) {
     return NG > 0 && 2 * ((S::D / 4 + NG * S::G / 4 + 63) / 64) <= S::NMETA && S::NMETA % 2 == 0;
@@ -542,22 +532,40 @@ __device__ __forceinline__ PairSlots<S> pair_slots(int lane, int NG) {
     return p;
 }
 
+// Code-scale multipliers of the lane's i-th metadata float4 (its elements
+// 0-1 and 2-3): a scale float4 covers the four consecutive channels or tokens
+// 4e..4e+3, at operand positions k = 2(e%2) + i/2, and is multiplied by
+// 2^(kCodeExp - kProdExp - 2k); zeros by 1.  e = lane + 64i, so e%2 is the
+// lane's parity (the ks and vs arrays start at even float4s).
+template <class S, bool PAIRED>
+__device__ __forceinline__ float2 meta_mul(int lane, int i, int NG) {
+    const float2 m = (lane & 1) ? make_float2(0x1p65f, 0x1p63f) : make_float2(0x1p69f, 0x1p67f);
+    if constexpr (PAIRED) return m;
+    const int kq = S::D / 4, vq = NG * S::G / 4;
+    const int e = min(lane + 64 * i, 2 * kq + 2 * vq - 1);    // as chunk_src clamps it
+    const bool scale = e < kq || (e >= 2 * kq && e < 2 * kq + vq);
+    return scale ? m : make_float2(1.f, 1.f);
+}
+
 // Stages a chunk's metadata in LDS as [ks | kz | vs | vz] float4 slots
-// (meta_slot).  PAIRED: the zero slots receive zero - 8*scale instead.
+// (meta_slot), the scales multiplied by their code-scale factors (mul[i],
+// from meta_mul).
 template <class S, bool PAIRED>
 __device__ __forceinline__ void stage_meta(const ChunkRegs<S>& r, float* MT, int lane, int NG,
-                                           int meta_floats, const PairSlots<S>& ps) {
+                                           int meta_floats, const PairSlots<S>& ps,
+                                           const float2* mul) {
     float4* mt = reinterpret_cast<float4*>(MT);
+    auto scaled = [&](float4 x, float2 m) {
+        return make_float4(x.x * m.x, x.y * m.x, x.z * m.y, x.w * m.y);
+    };
     if constexpr (PAIRED) {
         constexpr int HALF = S::NMETA / 2;
 #pragma unroll
         for (int i = 0; i < HALF; ++i) {
-            const float4 sc = r.meta[i], z = r.meta[i + HALF];
-            const float4 u = make_float4(fmaf(-8.f, sc.x, z.x), fmaf(-8.f, sc.y, z.y),
-                                         fmaf(-8.f, sc.z, z.z), fmaf(-8.f, sc.w, z.w));
+            const float4 sc = scaled(r.meta[i], mul[i]);
             if (ps.sc[i] >= 0) {
                 mt[ps.sc[i]] = sc;
-                mt[ps.zr[i]] = u;
+                mt[ps.zr[i]] = r.meta[i + HALF];
             }
         }
         return;
@@ -572,7 +580,7 @@ __device__ __forceinline__ void stage_meta(const ChunkRegs<S>& r, float* MT, int
 #pragma unroll
     for (int i = 0; i < S::NMETA; ++i) {
         const int e = min(lane + 64 * i, n4 - 1);
-        mt[S::meta_slot(e)] = r.meta[i];
+        mt[S::meta_slot(e)] = scaled(r.meta[i], mul[i]);
     }
 }
 
@@ -714,6 +722,9 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     int cid[PF];     // the chunk in each ring slot; -1 past the end (its load re-reads c_last)
     const ChunkSrc<S> src = chunk_src<S, PAIRED>(a, bh * a.Cmax, lane, NG);
     const PairSlots<S> pslots = pair_slots<S>(lane, NG);
+    float2 smul[S::NMETA];
+#pragma unroll
+    for (int i = 0; i < S::NMETA; ++i) smul[i] = meta_mul<S, PAIRED>(lane, i, NG);
     // (the launch gives every workgroup at least one chunk, or the store room
     // for chunk 0, so c_last is a readable chunk and these loads need no
     // branch: a branch here would make the compiler wait for them before the
@@ -771,14 +782,15 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     for (int it = 0; it < NEV; ++it) vb[it] = 0.f;
     const int n_items = HG * NSEG * NG;
 
-    const UnpackConsts uc = unpack_consts();
     const SplitConsts spc = split_consts();
-    const bf16x8_t ones = __builtin_bit_cast(
-        bf16x8_t, u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+    // B operand of the key correction: 2^-64 everywhere, the products' unit
+    const bf16x8_t unit = __builtin_bit_cast(
+        bf16x8_t, u32x4_t{kProdUnitBf16x2, kProdUnitBf16x2, kProdUnitBf16x2, kProdUnitBf16x2});
 
     // ---- phases of one chunk --------------------------------------------------
-    // Key A operand: rows 2h / 2h+1 = hi / lo of q[h,d]*ks[d]; correction
-    // column: hi / lo of sum_d q[h,d]*(kz[d] - 8 ks[d]) over the lane's channels.
+    // Key A operand: rows KP*h + p = piece p of q[h,d]*ks'[d] (ks' the staged,
+    // code-scaled key scale); correction column: the pieces of
+    // sum_d q[h,d]*kz[d] over the lane's channels.
     // Float offsets (within one metadata buffer) of this lane's ks / kz float4s.
     int wks[S::CPL / 4 > 0 ? S::CPL / 4 : 1], wkz[S::CPL / 4 > 0 ? S::CPL / 4 : 1];
 #pragma unroll
@@ -814,10 +826,8 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             const float xa = qv[2 * j] * ks[2 * j], xb = qv[2 * j + 1] * ks[2 * j + 1];
             if constexpr (KP == 3) split3_pair(xa, xb, pc[0][j], pc[1][j], pc[2][j], spc);
             else split_pair(xa, xb, pc[0][j], pc[1][j], spc);
-            // (PAIRED: the kz slots hold kz - 8 ks already)
-            corr = fmaf(qv[2 * j], PAIRED ? kz[2 * j] : fmaf(-8.f, ks[2 * j], kz[2 * j]), corr);
-            corr = fmaf(qv[2 * j + 1],
-                        PAIRED ? kz[2 * j + 1] : fmaf(-8.f, ks[2 * j + 1], kz[2 * j + 1]), corr);
+            corr = fmaf(qv[2 * j], kz[2 * j], corr);
+            corr = fmaf(qv[2 * j + 1], kz[2 * j + 1], corr);
         }
         // head wh's rows KP*wh + p, this lane's channels
         uint16_t* r0 = WA + (KP * wh) * S::WA_ROW + wseg * S::CPL;
@@ -860,7 +870,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         // as the starting value of every n-block's chain.
         f32x4_t s0 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kb = 0; kb < S::NBB; ++kb) s0 = mfma(Ab[kb], ones, s0);
+        for (int kb = 0; kb < S::NBB; ++kb) s0 = mfma(Ab[kb], unit, s0);
         f32x4_t Sc[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
@@ -868,7 +878,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
 #pragma unroll
             for (int ks = 0; ks < S::KS; ++ks) {
                 const uint32_t word = r.kc[ks * NSUB + nb / 2];
-                acc = mfma(Aw[ks], (nb % 2) == 0 ? unpack_codes<0>(word, uc) : unpack_codes<1>(word, uc),
+                acc = mfma(Aw[ks], (nb % 2) == 0 ? unpack_codes<0>(word) : unpack_codes<1>(word),
                            acc);
             }
             Sc[nb] = acc;
@@ -883,8 +893,8 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             alpha[e] = 1.f;
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
-                sc[e][nb] = KP == 3 ? (Sc[nb][2] + Sc[nb][1]) + Sc[nb][0]
-                                    : Sc[nb][2 * e] + Sc[nb][2 * e + 1];
+                sc[e][nb] = (KP == 3 ? (Sc[nb][2] + Sc[nb][1]) + Sc[nb][0]
+                                     : Sc[nb][2 * e] + Sc[nb][2 * e + 1]) * kProdScale;
         }
         const int n_masked = kv_lo - chunk * G;       // leading tokens hidden by padding
         if (__builtin_expect(n_masked > 0, 0)) {
@@ -973,10 +983,10 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         return any;
     };
 
-    // Value A operands: rows 2h / 2h+1 = hi / lo of p[h,t]*vs[t,g] for each
-    // group g, one item = (head, group, TPI tokens); value corrections
-    // p*(vz-8vs).  Item geometry is fixed per lane: LDS offsets are computed
-    // once here.
+    // Value A operands: rows 2h / 2h+1 = hi / lo of p[h,t]*vs'[t,g] for each
+    // group g (vs' the staged, code-scaled value scale), one item = (head,
+    // group, TPI tokens); value corrections p*vz.  Item geometry is fixed per
+    // lane: LDS offsets are computed once here.
     int it_valid[NEV], it_h[NEV], it_pl[NEV], it_pa[NEV], it_vb[NEV];
     int it_mv[NEV], it_mv2[NEV], it_mz[NEV], it_mz2[NEV];
     // 8-token items are numbered so that the 16 lanes of each ds_read_b128
@@ -1020,8 +1030,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                 const float2 vz = *reinterpret_cast<const float2*>(mt + it_mz[it]);
                 uint32_t h2, l2;
                 split_pair(p.x * vs.x, p.y * vs.y, h2, l2, spc);
-                float acc = fmaf(p.x, PAIRED ? vz.x : fmaf(-8.f, vs.x, vz.x), vb[it]);
-                vb[it] = fmaf(p.y, PAIRED ? vz.y : fmaf(-8.f, vs.y, vz.y), acc);
+                vb[it] = fmaf(p.y, vz.y, fmaf(p.x, vz.x, vb[it]));
                 uint16_t* base = PA + it_pa[it];
                 *reinterpret_cast<uint32_t*>(base) = h2;
                 *reinterpret_cast<uint32_t*>(base + S::PA_ROW) = l2;
@@ -1047,7 +1056,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                 float acc = vb[it];
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    acc = fmaf(p[j], PAIRED ? vz[j] : fmaf(-8.f, vs[j], vz[j]), acc);
+                    acc = fmaf(p[j], vz[j], acc);
                 vb[it] = acc;
                 uint16_t* base = PA + it_pa[it];
                 *reinterpret_cast<u32x4_t*>(base) = hi;
@@ -1071,7 +1080,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                     g_loaded = g;
                 }
                 const uint32_t word = r.vc[kt * (D / 32) + nb / 2];
-                O[nb] = mfma(Ap, (nb % 2) == 0 ? unpack_codes<0>(word, uc) : unpack_codes<1>(word, uc),
+                O[nb] = mfma(Ap, (nb % 2) == 0 ? unpack_codes<0>(word) : unpack_codes<1>(word),
                              O[nb]);
             }
         }
@@ -1230,7 +1239,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // chunk, so no load is inside a branch and the compiler waits only for
     // the chunk about to be used).
     if (cid[0] >= 0) {
-        stage_meta<S, PAIRED>(buf[0], MT, lane, NG, meta_floats, pslots);
+        stage_meta<S, PAIRED>(buf[0], MT, lane, NG, meta_floats, pslots, smul);
         wave_sync();
         wprep(Int<0>{});
         wave_sync();
@@ -1243,7 +1252,8 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                     int nxt_chunk) {
         constexpr int slot = decltype(slot_c)::value, nslot = slot ^ 1;
         if (has_next)
-            stage_meta<S, PAIRED>(nxt, MT + nslot * meta_stride, lane, NG, meta_floats, pslots);
+            stage_meta<S, PAIRED>(nxt, MT + nslot * meta_stride, lane, NG, meta_floats, pslots,
+                                  smul);
         wave_sync();
         if (has_next) wprep(Int<nslot>{});
         pprep(Int<slot>{}, any_cur);
@@ -1263,14 +1273,15 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     };
     static_assert(PF % 2 == 0, "the slot parity of a ring step must be static");
 
-    // O accumulates (p vs)(8 + c), which carries a bias of 8 sum_t p vs
-    // beside the output itself; the per-item correction sum_t p (vz - 8 vs)
-    // in vb cancels it.  Cancelled only at the end, that bias lets O's
-    // rounding grow with the whole context: each chunk adds ~2^-24 of the
-    // biased sum, which over long contexts of near-uniform weights reaches
-    // the size of the output itself (3e-3 relative at 1025 chunks per wave).
-    // Folding vb into O every kFoldChunks chunks keeps the bias in O to that
-    // of at most kFoldChunks chunks.  Called after a whole ring, where the
+    // O accumulates sum_t (p vs) c (in units of 2^-64), which exceeds the
+    // output by -sum_t p vz, the per-item correction kept in vb (with zeros
+    // near a group's minimum, ~1.5 sum_t p vs).  Cancelled only at the end,
+    // that excess lets O's rounding grow with the whole context: each chunk
+    // adds ~2^-24 of it, which over long contexts of near-uniform weights
+    // approaches the size of the output itself (measured 3e-3 relative at
+    // 1025 chunks per wave when codes entered as 8 + c, a ~5x larger excess).
+    // Folding vb into O every kFoldChunks chunks keeps the excess in O to
+    // that of at most kFoldChunks chunks.  Called after a whole ring, where the
     // pending rescale (if the last scores moved the running max) is in AL
     // slot 0 and has not reached vb yet: it is applied here, and the next
     // pprep then scales zeros.
@@ -1301,7 +1312,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                     float v = 0.f;
 #pragma unroll
                     for (int sg = 0; sg < NSEGV; ++sg) v += pv[sg];
-                    O[nb][2 * e] += v;
+                    O[nb][2 * e] = fmaf(v, kProdUnit, O[nb][2 * e]);
                 }
             }
         }
@@ -1361,7 +1372,8 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         if (h < HG) {
 #pragma unroll
             for (int nb = 0; nb < S::NBV; ++nb)
-                slot[h * D + 16 * nb + col] = O[nb][2 * e] + O[nb][2 * e + 1] + vcorr[e][nb];
+                slot[h * D + 16 * nb + col] =
+                    fmaf(O[nb][2 * e] + O[nb][2 * e + 1], kProdScale, vcorr[e][nb]);
         }
     }
 #pragma unroll
