@@ -155,6 +155,24 @@ __device__ __forceinline__ void split3_pair(float a, float b, uint32_t& hi, uint
     lo = pack_bf16x2(sa, sb);
 }
 
+// One value: the pieces in the low halves (high halves 0), five ops.
+__device__ __forceinline__ void split3_one(float a, uint32_t& hi, uint32_t& mid, uint32_t& lo,
+                                           SplitConsts k) {
+    hi = pack_bf16x2(a, 0.f);
+    const float r = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, hi),
+                                                    __builtin_bit_cast(bf16x2_t, k.neg_x), a, false);
+    mid = pack_bf16x2(r, 0.f);
+    const float s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, mid),
+                                                    __builtin_bit_cast(bf16x2_t, k.neg_x), r, false);
+    lo = pack_bf16x2(s, 0.f);
+}
+__device__ __forceinline__ void split_one(float a, uint32_t& hi, uint32_t& lo, SplitConsts k) {
+    hi = pack_bf16x2(a, 0.f);
+    const float r = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, hi),
+                                                    __builtin_bit_cast(bf16x2_t, k.neg_x), a, false);
+    lo = pack_bf16x2(r, 0.f);
+}
+
 // Code word -> B operand of tile M (four dwords of two bf16 each).  Element j
 // of the tile sits at bit 8M + 2(j/2) of the low (j even) or high (j odd)
 // half of the word; dword k keeps bits 2k..2k+1 of each half of the word
@@ -224,6 +242,22 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// A per-lane LDS address, computed once and kept in a VGPR (PIN).  Left to
+// itself the compiler rebuilds such addresses (a multiply and an add of the
+// wave's base) at every use in the chunk loop; the empty asm hides the
+// value.  The pointer stays an LDS pointer, so constant offsets added to it
+// fold into the ds instructions' offset field.  Each pinned address holds a
+// VGPR for the whole loop: instances without the registers to spare
+// (Shape::PIN false) leave the addresses to the compiler.
+template <bool PIN, class T>
+__device__ __forceinline__ T* pin_lds(T* p) {
+    if constexpr (!PIN) return p;
+    typedef __attribute__((address_space(3))) T lds_t;
+    lds_t* q = (lds_t*)p;
+    asm("" : "+v"(q));
+    return (T*)q;
+}
+
 // Item number of a lane for the value operand build (a permutation of 0..63).
 __device__ __forceinline__ int item_lane(int lane) {
     const int r = lane & 31;
@@ -281,6 +315,10 @@ struct Shape {
     // ~8x) and two pieces, the output error reached ~1e-3 at a largest score
     // of 64 (natural units) at config 4's shape and at head_dim 64.
     static constexpr int KP = HG <= 4 ? 3 : 2;
+    // Keep loop addresses and the correction's B operand in VGPRs (pin_lds):
+    // ~13 VALU per chunk fewer for ~11 VGPRs, which the 8-head instances
+    // (at the 256-register limit of two waves per SIMD) do not have.
+    static constexpr bool PIN = HG <= 4;
     static constexpr int KROWS = KP * HG;            // key A rows holding data
     // A operands have 16 rows, of which only KROWS (key) or 2*HG (value: hi
     // / lo per head) carry data: the rest are stored once, as one zero row
@@ -767,6 +805,15 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                                                                : S::KROWS)
                               : arow;
     auto khead = [&](int e) { return KP == 3 ? gq : 2 * gq + e; };
+    // the lane's LDS addresses in the chunk loop: key operand rows written
+    // (W-prep lanes) and read, the value operand rows read, the probability
+    // rows written
+    uint16_t* const wa_w = pin_lds<S::PIN>(WA + (KP * wh) * S::WA_ROW + wseg * S::CPL);
+    uint16_t* const ba_w = pin_lds<S::PIN>(BA + (KP * wh) * S::BA_ROW + wseg);
+    const uint16_t* const wa_r = pin_lds<S::PIN>(WA + karow * S::WA_ROW + 8 * gq);
+    const uint16_t* const ba_r = pin_lds<S::PIN>(BA + karow * S::BA_ROW + 8 * gq);
+    const uint16_t* const pa_r = pin_lds<S::PIN>(PA + arow * S::PA_ROW + 8 * gq);
+    float* const pl_w = pin_lds<S::PIN>(PL + khead(0) * S::PL_ROW + col);
     // online-softmax state of the lane's key-side heads
     float m_run[HPL], l_part[HPL], m_thr[HPL];     // m_thr = m_run + kRescaleThreshold
     bool hvalid[HPL];
@@ -784,8 +831,11 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
 
     const SplitConsts spc = split_consts();
     // B operand of the key correction: 2^-64 everywhere, the products' unit
-    const bf16x8_t unit = __builtin_bit_cast(
-        bf16x8_t, u32x4_t{kProdUnitBf16x2, kProdUnitBf16x2, kProdUnitBf16x2, kProdUnitBf16x2});
+    // (hidden from the compiler, which would otherwise rebuild it with four
+    // moves at every use)
+    u32x4_t unit_u = {kProdUnitBf16x2, kProdUnitBf16x2, kProdUnitBf16x2, kProdUnitBf16x2};
+    if constexpr (S::PIN) asm("" : "+v"(unit_u));
+    const bf16x8_t unit = __builtin_bit_cast(bf16x8_t, unit_u);
 
     // ---- phases of one chunk --------------------------------------------------
     // Key A operand: rows KP*h + p = piece p of q[h,d]*ks'[d] (ks' the staged,
@@ -830,10 +880,9 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             corr = fmaf(qv[2 * j + 1], kz[2 * j + 1], corr);
         }
         // head wh's rows KP*wh + p, this lane's channels
-        uint16_t* r0 = WA + (KP * wh) * S::WA_ROW + wseg * S::CPL;
 #pragma unroll
         for (int pi = 0; pi < KP; ++pi) {
-            uint16_t* rp = r0 + pi * S::WA_ROW;
+            uint16_t* rp = wa_w + pi * S::WA_ROW;
             if constexpr (S::CPL % 8 == 0) {
 #pragma unroll
                 for (int j = 0; j < S::CPL / 8; ++j)
@@ -845,10 +894,10 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             }
         }
         uint32_t cc[3];
-        if constexpr (KP == 3) split3_pair(corr, 0.f, cc[0], cc[1], cc[2], spc);
-        else split_pair(corr, 0.f, cc[0], cc[1], spc);
+        if constexpr (KP == 3) split3_one(corr, cc[0], cc[1], cc[2], spc);
+        else split_one(corr, cc[0], cc[1], spc);
 #pragma unroll
-        for (int pi = 0; pi < KP; ++pi) BA[(KP * wh + pi) * S::BA_ROW + wseg] = (uint16_t)cc[pi];
+        for (int pi = 0; pi < KP; ++pi) ba_w[pi * S::BA_ROW] = (uint16_t)cc[pi];
     };
 
     // Scores of the chunk's G tokens (matrix cores), then the online softmax:
@@ -862,10 +911,10 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         bf16x8_t Aw[S::KS], Ab[S::NBB];
 #pragma unroll
         for (int ks = 0; ks < S::KS; ++ks)
-            Aw[ks] = *reinterpret_cast<const bf16x8_t*>(WA + karow * S::WA_ROW + 32 * ks + 8 * gq);
+            Aw[ks] = *reinterpret_cast<const bf16x8_t*>(wa_r + 32 * ks);
 #pragma unroll
         for (int kb = 0; kb < S::NBB; ++kb)
-            Ab[kb] = *reinterpret_cast<const bf16x8_t*>(BA + karow * S::BA_ROW + 32 * kb + 8 * gq);
+            Ab[kb] = *reinterpret_cast<const bf16x8_t*>(ba_r + 32 * kb);
         // The correction is the same for every token: one accumulator, shared
         // as the starting value of every n-block's chain.
         f32x4_t s0 = {0.f, 0.f, 0.f, 0.f};
@@ -954,7 +1003,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                 }
             }
         }
-        float* pl = PL + slot * (HG * S::PL_ROW);
+        float* pl = pl_w + slot * (HG * S::PL_ROW);
         float pv[HPL][NB];
 #pragma unroll
         for (int e = 0; e < HPL; ++e) {
@@ -976,7 +1025,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
                 lsum += pv[e][nb];
-                if (hvalid[e]) pl[khead(e) * S::PL_ROW + 16 * nb + col] = pv[e][nb];
+                if (hvalid[e]) pl[(khead(e) - khead(0)) * S::PL_ROW + 16 * nb] = pv[e][nb];
             }
             l_part[e] += lsum;
         }
@@ -987,7 +1036,9 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // group g (vs' the staged, code-scaled value scale), one item = (head,
     // group, TPI tokens); value corrections p*vz.  Item geometry is fixed per
     // lane: LDS offsets are computed once here.
-    int it_valid[NEV], it_h[NEV], it_pl[NEV], it_pa[NEV], it_vb[NEV];
+    int it_valid[NEV], it_h[NEV], it_vb[NEV];
+    const float* it_pl[NEV];      // the item's probabilities in PL slot 0
+    uint16_t* it_pa[NEV];         // the item's hi row in the value A operand
     int it_mv[NEV], it_mv2[NEV], it_mz[NEV], it_mz2[NEV];
     // 8-token items are numbered so that the 16 lanes of each ds_read_b128
     // cycle take 16 consecutive items: lanes {0-3, 12-15, 20-27} -> 0-15 and
@@ -1001,7 +1052,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         const int g = rem / NSEG, seg = rem % NSEG;
         it_valid[it] = e < n_items;
         it_h[it] = h;
-        it_pl[it] = h * S::PL_ROW + TPI * seg;             // into PL[slot]
+        it_pl[it] = pin_lds<S::PIN>(PL + min(h, HG - 1) * S::PL_ROW + TPI * seg);
         // staged value correction: one per item, or per 16-item row
         it_vb[it] = TPI == 8 ? e : (seg % 16 == 0 ? (h * NG + g) * NSEGV + seg / 16 : -1);
         const int fv = 2 * D + g * G + TPI * seg;          // float index of vs
@@ -1015,29 +1066,30 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             it_mz[it] = 4 * S::meta_slot((fv + NG * G) / 4) + (fv + NG * G) % 4;
             it_mv2[it] = it_mz2[it] = 0;
         }
-        it_pa[it] = g * S::PA_MAT + TPI * seg + 2 * h * S::PA_ROW;
+        it_pa[it] = pin_lds<S::PIN>(PA + min(g, NG - 1) * S::PA_MAT + TPI * seg +
+                                    2 * min(h, HG - 1) * S::PA_ROW);
     }
     auto pprep = [&](auto slot_c, bool any) {
         constexpr int slot = decltype(slot_c)::value;
-        const float* pl = PL + slot * (HG * S::PL_ROW);
+        constexpr int pl_off = slot * (HG * S::PL_ROW);
         const float* mt = MT + slot * meta_stride;
 #pragma unroll
         for (int it = 0; it < NEV; ++it) {
             if (TPI == 2 && it_valid[it]) {
                 if (any) vb[it] *= AL[slot * 16 + it_h[it]];
-                const float2 p = *reinterpret_cast<const float2*>(pl + it_pl[it]);
+                const float2 p = *reinterpret_cast<const float2*>(it_pl[it] + pl_off);
                 const float2 vs = *reinterpret_cast<const float2*>(mt + it_mv[it]);
                 const float2 vz = *reinterpret_cast<const float2*>(mt + it_mz[it]);
                 uint32_t h2, l2;
                 split_pair(p.x * vs.x, p.y * vs.y, h2, l2, spc);
                 vb[it] = fmaf(p.y, vz.y, fmaf(p.x, vz.x, vb[it]));
-                uint16_t* base = PA + it_pa[it];
+                uint16_t* base = it_pa[it];
                 *reinterpret_cast<uint32_t*>(base) = h2;
                 *reinterpret_cast<uint32_t*>(base + S::PA_ROW) = l2;
             } else if (TPI == 8 && it_valid[it]) {
                 if (any) vb[it] *= AL[slot * 16 + it_h[it]];
-                const float4 pa = *reinterpret_cast<const float4*>(pl + it_pl[it]);
-                const float4 pb = *reinterpret_cast<const float4*>(pl + it_pl[it] + 4);
+                const float4 pa = *reinterpret_cast<const float4*>(it_pl[it] + pl_off);
+                const float4 pb = *reinterpret_cast<const float4*>(it_pl[it] + pl_off + 4);
                 const float4 sa = *reinterpret_cast<const float4*>(mt + it_mv[it]);
                 const float4 sb = *reinterpret_cast<const float4*>(mt + it_mv2[it]);
                 const float4 za = *reinterpret_cast<const float4*>(mt + it_mz[it]);
@@ -1058,7 +1110,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                 for (int j = 0; j < 8; ++j)
                     acc = fmaf(p[j], vz[j], acc);
                 vb[it] = acc;
-                uint16_t* base = PA + it_pa[it];
+                uint16_t* base = it_pa[it];
                 *reinterpret_cast<u32x4_t*>(base) = hi;
                 *reinterpret_cast<u32x4_t*>(base + S::PA_ROW) = lo;
             }
@@ -1075,8 +1127,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             for (int nb = 0; nb < S::NBV; ++nb) {
                 const int g = (16 * nb) / Gv;
                 if (g != g_loaded) {
-                    Ap = *reinterpret_cast<const bf16x8_t*>(PA + g * S::PA_MAT + arow * S::PA_ROW +
-                                                            32 * kt + 8 * gq);
+                    Ap = *reinterpret_cast<const bf16x8_t*>(pa_r + g * S::PA_MAT + 32 * kt);
                     g_loaded = g;
                 }
                 const uint32_t word = r.vc[kt * (D / 32) + nb / 2];
