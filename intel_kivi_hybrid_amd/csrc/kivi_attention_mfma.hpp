@@ -532,6 +532,27 @@ __device__ __forceinline__ ChunkSrc<S> chunk_src(const AttnLaunch& a, int64_t ci
 // 1-2 % faster at 8K context (B=64, 32/8 heads), 2-3 % at 128K (split-K) and
 // 12 % at 4K with B=16 and 32 heads, where the 336 MB store would otherwise
 // half fit the MALL and evict itself.
+// The key codes and metadata (load_chunk_km) and the value codes
+// (load_chunk_v) are issued separately: a ring slot's key codes and metadata
+// are consumed one step before its value codes.
+template <class S>
+__device__ __forceinline__ void load_chunk_km(ChunkRegs<S>& r, const ChunkSrc<S>& src, int c) {
+    const uint32_t* kc = src.kc + (int64_t)c * (64 * S::NP);
+#pragma unroll
+    for (int i = 0; i < S::NP; ++i) r.kc[i] = __builtin_nontemporal_load(kc + i);
+#pragma unroll
+    for (int i = 0; i < S::NMETA; ++i) {
+        const kivi_f4v x = __builtin_nontemporal_load(
+            reinterpret_cast<const kivi_f4v*>(src.meta[i] + (int64_t)c * src.meta_stride[i]));
+        r.meta[i] = make_float4(x.x, x.y, x.z, x.w);
+    }
+}
+template <class S>
+__device__ __forceinline__ void load_chunk_v(ChunkRegs<S>& r, const ChunkSrc<S>& src, int c) {
+    const uint32_t* vc = src.vc + (int64_t)c * (64 * S::NP);
+#pragma unroll
+    for (int i = 0; i < S::NP; ++i) r.vc[i] = __builtin_nontemporal_load(vc + i);
+}
 template <class S>
 __device__ __forceinline__ void load_chunk(ChunkRegs<S>& r, const ChunkSrc<S>& src, int c) {
     const uint32_t* kc = src.kc + (int64_t)c * (64 * S::NP);
@@ -1299,8 +1320,9 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // Step i (of the wave's chunks, counted from 0) uses double-buffer
     // slot i & 1; PF is even, so within the unrolled ring the slot of step k
     // is k & 1, a compile-time constant.
+    // `after_v` runs once the value products have read cur's value codes.
     auto step = [&](const ChunkRegs<S>& cur, const ChunkRegs<S>& nxt, bool has_next, auto slot_c,
-                    int nxt_chunk) {
+                    int nxt_chunk, auto&& after_v) {
         constexpr int slot = decltype(slot_c)::value, nslot = slot ^ 1;
         if (has_next)
             stage_meta<S, PAIRED>(nxt, MT + nslot * meta_stride, lane, NG, meta_floats, pslots,
@@ -1319,6 +1341,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         // instead, did not help.
         __builtin_amdgcn_s_setprio(2);
         vside(cur);
+        after_v();
         if (has_next) any_cur = kside(nxt, Int<nslot>{}, nxt_chunk);
         __builtin_amdgcn_s_setprio(0);
     };
@@ -1371,15 +1394,22 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // The ring holds the wave's chunks in order, valid ones first.  The main
     // loop runs whole rings while every slot holds a chunk (no branch inside,
     // so the compiler schedules across the steps); the last partial ring is
-    // the tail, which loads nothing.
+    // the tail, which loads nothing.  Slot k is refilled with the chunk PF
+    // ahead in two parts: its key codes and metadata, last used by the
+    // previous step (stage_meta and kside of the slot's chunk), before step
+    // k, and its value codes once step k's value products have read them.
+    // The refill then leads its use by three steps for three quarters of
+    // the bytes (two when the whole slot waited for the end of the step).
     int rings = 0;
     while (cid[PF - 1] >= 0) {
         static_for<0, PF>([&](auto kc) {
             constexpr int k = decltype(kc)::value;
+            const int c_new = chunk_of(next_j++);
+            const int c_ld = c_new >= 0 ? c_new : c_last;
+            load_chunk_km<S>(buf[k], src, c_ld);
             step(buf[k], buf[(k + 1) % PF], k + 1 < PF || cid[0] >= 0, Int<k & 1>{},
-                 cid[(k + 1) % PF]);
-            cid[k] = chunk_of(next_j++);
-            load_chunk<S>(buf[k], src, cid[k] >= 0 ? cid[k] : c_last);
+                 cid[(k + 1) % PF], [&] { load_chunk_v<S>(buf[k], src, c_ld); });
+            cid[k] = c_new;
         });
         if (++rings == kFoldRings) {
             rings = 0;
@@ -1388,7 +1418,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     }
     static_for<0, PF - 1>([&](auto kc) {
         constexpr int k = decltype(kc)::value;
-        if (cid[k] >= 0) step(buf[k], buf[k + 1], cid[k + 1] >= 0, Int<k & 1>{}, cid[k + 1]);
+        if (cid[k] >= 0) step(buf[k], buf[k + 1], cid[k + 1] >= 0, Int<k & 1>{}, cid[k + 1], [] {});
     });
     // ---- wave state -> merge slot --------------------------------------------
     wave_sync();
