@@ -75,6 +75,11 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// lane l's value of v, for every lane (l wave-uniform)
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
 __device__ __forceinline__ int ring_slot(int start, int t, int cap) {
     int s = start + t;
     return s >= cap ? s - cap : s;
@@ -359,6 +364,46 @@ __global__ __launch_bounds__(kMaxD) void attn_merge_kernel(const float* __restri
         }
         orow[d] = acc / L;
     }
+}
+
+// The same merge for at most SM <= 64 splits in one memory round trip:
+// each thread loads its channel's S partial outputs while lane s of each wave
+// loads the row's pair (m_s, l_s); each wave then forms the maximum and the
+// weights f_s = 2^(m_s - M) across its lanes and reads them back one split
+// at a time (readlane): no LDS, no barrier between two dependent rounds.
+// The operations and their order are attn_merge_kernel's (the fmaf sums run
+// in split order), so the output bits are the same.  Threads past D load
+// channel D-1 and store nothing.
+template <int SM>
+__global__ __launch_bounds__(kMaxD) void attn_merge_regs_kernel(const float* __restrict__ part_o,
+                                                                const float* __restrict__ part_ml,
+                                                                float* __restrict__ out,
+                                                                QueryRows qr, int Hq, int HG,
+                                                                int D, int S) {
+    static_assert(SM <= kWave, "one split per lane");
+    const int kvh = blockIdx.x / HG, v = blockIdx.x % HG;
+    if (!qr.real(v)) return;                      // a padding row
+    const int64_t row = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+    const int lane = threadIdx.x % kWave;
+    const float* ml = part_ml + row * S * 2 + 2 * min(lane, S - 1);
+    const float m_s = ml[0], l_s = ml[1];
+    const int d = min((int)threadIdx.x, D - 1);
+    const float* po = part_o + row * S * D + d;
+    float o[SM];
+#pragma unroll
+    for (int s = 0; s < SM; ++s) o[s] = po[(int64_t)min(s, S - 1) * D];
+    const float M = wave_max(lane < S ? m_s : -INFINITY);
+    const float f_s = lane < S && m_s != -INFINITY ? exp2f(m_s - M) : 0.f;
+    float acc = 0.f, L = 0.f;
+#pragma unroll
+    for (int s = 0; s < SM; ++s) {
+        if (s < S) {
+            const float w = lane_f(f_s, s);
+            acc = fmaf(w, o[s], acc);
+            L = fmaf(w, lane_f(l_s, s), L);
+        }
+    }
+    if ((int)threadIdx.x < D) out[qr.row(blockIdx.y, kvh, v, Hq, D) + d] = acc / L;
 }
 
 struct Plan {
@@ -749,9 +794,20 @@ int attention_impl(const float* q, int32_t q_len, int32_t causal, const int32_t*
         if (needs_workspace(p)) {
             // whole waves: the (m, l) reduction reads every lane of a wave
             const int merge_threads = (head_dim + kWave - 1) / kWave * kWave;
-            attn_merge_kernel<<<dim3(kv_heads * rows, batch), merge_threads,
-                                2 * p.n_splits * sizeof(float), st>>>(
-                part_o, part_ml, oi, qr, q_heads, rows, head_dim, p.n_splits);
+            const dim3 mgrid(kv_heads * rows, batch);
+            const int S = p.n_splits;
+            if (S <= 8)
+                attn_merge_regs_kernel<8><<<mgrid, merge_threads, 0, st>>>(
+                    part_o, part_ml, oi, qr, q_heads, rows, head_dim, S);
+            else if (S <= 16)
+                attn_merge_regs_kernel<16><<<mgrid, merge_threads, 0, st>>>(
+                    part_o, part_ml, oi, qr, q_heads, rows, head_dim, S);
+            else if (S <= 32)
+                attn_merge_regs_kernel<32><<<mgrid, merge_threads, 0, st>>>(
+                    part_o, part_ml, oi, qr, q_heads, rows, head_dim, S);
+            else
+                attn_merge_kernel<<<mgrid, merge_threads, 2 * S * sizeof(float), st>>>(
+                    part_o, part_ml, oi, qr, q_heads, rows, head_dim, S);
             rc = check_launch("packed_attention_merge");
             if (rc) return rc;
         }

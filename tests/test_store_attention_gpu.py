@@ -173,6 +173,13 @@ def test_attention_split_counts_agree(store_cls, splits):
     _attention_case(store_cls, 1, 8, 2, 128, 32, 32, 128, 2000, splits=splits, seed=3)
 
 
+# Up to 32 splits merge in registers, more through LDS: 6000 tokens give 183
+# chunks, room for 46 splits of four chunks.
+@pytest.mark.parametrize("splits", [16, 17, 32, 33, 46])
+def test_attention_merge_paths(store_cls, splits):
+    _attention_case(store_cls, 1, 8, 2, 128, 32, 32, 128, 6000, splits=splits, seed=4)
+
+
 def test_attention_reference_cosine_gate(store_cls, kat):
     """The reference's only attention check (test_attention_fix.py:33-115):
     KIVI attention vs fp32 attention cosine > 0.85 at B=1, H=2, cache 32,
