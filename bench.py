@@ -681,9 +681,9 @@ def e2e_gpt2(dev, n_tokens=200, G=32, R=64, prompt_len=40, log=print):
 CONFIG4 = (64, 32, 8, 128, 8192, 128, 32)      # B, Hq, Hkv, D, context, R, G
 PRECISION = ("fp32 inputs and outputs; 2-bit codes with fp32 scales/zeros, bit-exact to the "
              "reference codec; attention products on bf16 matrix cores with fp32 accumulation, "
-             "each fp32 key factor split into three bf16 pieces (~2^-25 relative; two, ~2^-17, "
-             "at 8 query heads per kv head) and each value factor into two (~2^-17); softmax "
-             "and residual window in fp32")
+             "the codes exact as subnormal bf16 operands, each fp32 key factor split into three "
+             "bf16 pieces (~2^-25 relative; two, ~2^-17, at 8 query heads per kv head) and each "
+             "value factor into two (~2^-17); softmax and residual window in fp32")
 DTYPE = "fp32 I/O; bf16 split-factor MFMA products; fp32 accumulation"
 
 

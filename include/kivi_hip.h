@@ -188,7 +188,11 @@ int kivi_store_code_layout(int32_t head_dim, int32_t group_size_k, int32_t group
  * per group of 8, each streaming the store once), head_dim % 16 == 0 and
  * <= 256; plain-layout stores also need
  * group_size_k % 16 == 0 and <= 64.  Matrix-core-layout stores run on the
- * bf16 MFMA units with fp32 accumulation (relative error ~1e-5). */
+ * bf16 MFMA units with fp32 accumulation (relative error ~1e-5), forming
+ * products in units of 2^-64: key scales and key products
+ * q*k_scale*softmax_scale*log2(e) must stay below 2^59 and value scales
+ * below 2^51 (beyond, the output is inf or NaN); value products below
+ * ~2^-38 lose relative precision. */
 /* 0 if kivi_packed_decode_attention can run a store of this geometry (for
  * any context length), else the KIVI_ERR_* code its launch would return, with
  * the message in kivi_last_error().  No reference counterpart; it lets a
