@@ -34,10 +34,10 @@
 // * The zeros fold into corrections that are linear in the data:
 //     s[h,t] = sum_d (q ks)[h,d] c + sum_d q[h,d] kz[d]
 //     o[h,d] = sum_t (p vs)[h,t] c' + sum_t p[h,t] vz[t]
-//   The key correction enters the MFMA as extra k-steps against a B operand
-//   of 2^-64s (so it is summed across lanes by the matrix core, in the same
-//   units); the value correction is accumulated per lane and added at the
-//   end.  Scores and the output are scaled back by 2^64.
+//   The key correction is summed over each head's operand-build lanes with
+//   DPP, which leaves it in the lanes holding that head's scores, and added
+//   in fp32 as the scores are scaled back by 2^64; the value correction is
+//   accumulated per lane and added to the output.
 //   The units bound the factors: the key product q*ks*softmax_scale*log2(e)
 //   and the key scale below 2^59, value scales below 2^51 (larger ones
 //   overflow the A operand to inf).  Value codes' products below ~2^-38
@@ -155,24 +155,6 @@ __device__ __forceinline__ void split3_pair(float a, float b, uint32_t& hi, uint
     lo = pack_bf16x2(sa, sb);
 }
 
-// One value: the pieces in the low halves (high halves 0), five ops.
-__device__ __forceinline__ void split3_one(float a, uint32_t& hi, uint32_t& mid, uint32_t& lo,
-                                           SplitConsts k) {
-    hi = pack_bf16x2(a, 0.f);
-    const float r = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, hi),
-                                                    __builtin_bit_cast(bf16x2_t, k.neg_x), a, false);
-    mid = pack_bf16x2(r, 0.f);
-    const float s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, mid),
-                                                    __builtin_bit_cast(bf16x2_t, k.neg_x), r, false);
-    lo = pack_bf16x2(s, 0.f);
-}
-__device__ __forceinline__ void split_one(float a, uint32_t& hi, uint32_t& lo, SplitConsts k) {
-    hi = pack_bf16x2(a, 0.f);
-    const float r = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, hi),
-                                                    __builtin_bit_cast(bf16x2_t, k.neg_x), a, false);
-    lo = pack_bf16x2(r, 0.f);
-}
-
 // Code word -> B operand of tile M (four dwords of two bf16 each).  Element j
 // of the tile sits at bit 8M + 2(j/2) of the low (j even) or high (j odd)
 // half of the word; dword k keeps bits 2k..2k+1 of each half of the word
@@ -197,7 +179,6 @@ constexpr int kCodeExp = 133;
 constexpr int kProdExp = 64;
 constexpr float kProdUnit = 0x1p-64f;      // 2^-kProdExp
 constexpr float kProdScale = 0x1p64f;      // 2^kProdExp
-constexpr uint32_t kProdUnitBf16x2 = 0x1F801F80u;   // (2^-64, 2^-64) in bf16
 static_assert(kCodeExp - kProdExp == 69, "code scale constants below");
 
 __device__ __forceinline__ f32x4_t mfma(bf16x8_t a, bf16x8_t b, f32x4_t c) {
@@ -280,7 +261,6 @@ struct Shape {
     static constexpr int NBV = D / 16;               // value n-blocks
     static constexpr int LPH = (64 / HG < D / 2) ? 64 / HG : D / 2;   // W-prep lanes per head
     static constexpr int CPL = D / LPH;              // channels per W-prep lane
-    static constexpr int NBB = (LPH + 31) / 32;      // correction k-steps
     static constexpr int NGMAX = D / 32;             // value groups (Gv >= 32)
     // chunk metadata: ks [D], kz [D], vs [NG][G], vz [NG][G] as float4s
     static constexpr int META4_MAX = (2 * D + 2 * NGMAX * G) / 4;
@@ -305,7 +285,6 @@ struct Shape {
     // An A-operand read takes row l%16 and k-group l/16: with rows 2 (mod 4)
     // 16-byte slots apart, each read cycle hits 16 distinct slots (mod 16).
     static constexpr int WA_ROW = D + 16;            // bf16 per key A row
-    static constexpr int BA_ROW = 32 * NBB + 16;     // bf16 per correction A row
     static constexpr int PA_ROW = G + 16;            // bf16 per value A row
     // Key A factors are split into KP bf16 pieces: hi + mid + lo (~2^-25
     // relative) with up to 4 query heads per kv head, hi + lo (~2^-17) with
@@ -328,8 +307,7 @@ struct Shape {
     static constexpr int PA_MAT = AROWS * PA_ROW;    // bf16 per value A matrix (one group)
     static constexpr int PL_ROW = G + 8;             // floats per probability row
     static constexpr int OFF_WA = 0;
-    static constexpr int OFF_BA = OFF_WA + KAROWS * WA_ROW * 2;
-    static constexpr int OFF_PA = OFF_BA + KAROWS * BA_ROW * 2;
+    static constexpr int OFF_PA = OFF_WA + KAROWS * WA_ROW * 2;
     // The rest depends on the number of value groups NG = D / Gv.
     __host__ __device__ static constexpr int off_pl(int NG) { return OFF_PA + NG * PA_MAT * 2; }
     __host__ __device__ static constexpr int off_al(int NG) { return off_pl(NG) + 2 * HG * PL_ROW * 4; }
@@ -676,7 +654,6 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
 
     unsigned char* wl = smem + wave * S::wave_lds(NG);
     uint16_t* WA = reinterpret_cast<uint16_t*>(wl + S::OFF_WA);
-    uint16_t* BA = reinterpret_cast<uint16_t*>(wl + S::OFF_BA);
     uint16_t* PA = reinterpret_cast<uint16_t*>(wl + S::OFF_PA);
     float* PL = reinterpret_cast<float*>(wl + S::off_pl(NG));      // [2][HG][G]
     float* AL = reinterpret_cast<float*>(wl + S::off_al(NG));      // [2][16]
@@ -830,9 +807,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // (W-prep lanes) and read, the value operand rows read, the probability
     // rows written
     uint16_t* const wa_w = pin_lds<S::PIN>(WA + (KP * wh) * S::WA_ROW + wseg * S::CPL);
-    uint16_t* const ba_w = pin_lds<S::PIN>(BA + (KP * wh) * S::BA_ROW + wseg);
     const uint16_t* const wa_r = pin_lds<S::PIN>(WA + karow * S::WA_ROW + 8 * gq);
-    const uint16_t* const ba_r = pin_lds<S::PIN>(BA + karow * S::BA_ROW + 8 * gq);
     const uint16_t* const pa_r = pin_lds<S::PIN>(PA + arow * S::PA_ROW + 8 * gq);
     float* const pl_w = pin_lds<S::PIN>(PL + khead(0) * S::PL_ROW + col);
     // online-softmax state of the lane's key-side heads
@@ -851,17 +826,11 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     const int n_items = HG * NSEG * NG;
 
     const SplitConsts spc = split_consts();
-    // B operand of the key correction: 2^-64 everywhere, the products' unit
-    // (hidden from the compiler, which would otherwise rebuild it with four
-    // moves at every use)
-    u32x4_t unit_u = {kProdUnitBf16x2, kProdUnitBf16x2, kProdUnitBf16x2, kProdUnitBf16x2};
-    if constexpr (S::PIN) asm("" : "+v"(unit_u));
-    const bf16x8_t unit = __builtin_bit_cast(bf16x8_t, unit_u);
 
     // ---- phases of one chunk --------------------------------------------------
     // Key A operand: rows KP*h + p = piece p of q[h,d]*ks'[d] (ks' the staged,
-    // code-scaled key scale); correction column: the pieces of
-    // sum_d q[h,d]*kz[d] over the lane's channels.
+    // code-scaled key scale).  Returns the lane's part of the key correction,
+    // sum_d q[h,d]*kz[d] over its channels (0 on lanes that build nothing).
     // Float offsets (within one metadata buffer) of this lane's ks / kz float4s.
     int wks[S::CPL / 4 > 0 ? S::CPL / 4 : 1], wkz[S::CPL / 4 > 0 ? S::CPL / 4 : 1];
 #pragma unroll
@@ -870,9 +839,9 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         wks[i] = 4 * S::meta_slot(s0) + (S::CPL >= 4 ? 0 : (wseg * S::CPL) % 4);
         wkz[i] = 4 * S::meta_slot(D / 4 + s0) + (S::CPL >= 4 ? 0 : (wseg * S::CPL) % 4);
     }
-    auto wprep = [&](auto slot_c) {
+    auto wprep = [&](auto slot_c) -> float {
         constexpr int slot = decltype(slot_c)::value;
-        if (!wlane) return;
+        if (!wlane) return 0.f;
         const float* mt = MT + slot * meta_stride;
         float ks[S::CPL], kz[S::CPL];
         if constexpr (S::CPL % 4 == 0) {
@@ -914,12 +883,33 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                 for (int j = 0; j < S::CPL / 2; ++j) reinterpret_cast<uint32_t*>(rp)[j] = pc[pi][j];
             }
         }
-        uint32_t cc[3];
-        if constexpr (KP == 3) split3_one(corr, cc[0], cc[1], cc[2], spc);
-        else split_one(corr, cc[0], cc[1], spc);
-#pragma unroll
-        for (int pi = 0; pi < KP; ++pi) ba_w[pi * S::BA_ROW] = (uint16_t)cc[pi];
+        return corr;
     };
+    // The key correction of each of the lane's key-side heads (khead(e)),
+    // summed over that head's W-prep lanes (wh*LPH .. wh*LPH+LPH-1).  With 16
+    // per head they are the DPP row of the head, which (three key pieces:
+    // lane group gq = head gq) is where its scores are; with 8 (8 query
+    // heads per kv head) half rows, heads 2gq and 2gq+1 being the two halves
+    // of row gq; with 32 or 64, whole rows combined through readlane.  Every
+    // lane takes part (wave-uniform control flow).
+    auto head_corr = [&](float part, float* kc) {
+        if constexpr (S::LPH == 16) {
+            kc[0] = row_sum16(part);
+        } else if constexpr (S::LPH == 8) {
+            float v = part + dpp<0xB1>(part);          // quad_perm [1,0,3,2]
+            v += dpp<0x4E>(v);                           // quad_perm [2,3,0,1]
+            v += dpp<0x141>(v);                          // row_half_mirror: the half row
+            const float other = dpp<0x128>(v);           // row_ror 8: the other half
+            kc[0] = col < 8 ? v : other;
+            kc[1] = col < 8 ? other : v;
+        } else {
+            const float r = row_sum16(part);
+            const float c01 = lane_f(r, 0) + lane_f(r, 16), c23 = lane_f(r, 32) + lane_f(r, 48);
+            kc[0] = HG == 1 ? c01 + c23 : (gq == 0 ? c01 : c23);
+        }
+    };
+    static_assert(S::LPH == 16 || S::LPH == 8 || HG <= 2, "key correction lanes");
+    static_assert(S::LPH != 16 || KP == 3, "16 correction lanes per head need one head per lane");
 
     // Scores of the chunk's G tokens (matrix cores), then the online softmax:
     // lane group gq holds heads 2gq, 2gq+1.  Returns whether any running max
@@ -927,24 +917,17 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // `chunk` is the chunk's index: its tokens before kv_lo (a left-padded
     // sequence) get score -inf and weight 0, on a wave-uniform branch that
     // unpadded sequences never take.
-    auto kside = [&](const ChunkRegs<S>& r, auto slot_c, int chunk) -> bool {
+    // kc: the key corrections of the lane's key-side heads (head_corr).
+    auto kside = [&](const ChunkRegs<S>& r, auto slot_c, int chunk, const float* kc) -> bool {
         constexpr int slot = decltype(slot_c)::value;
-        bf16x8_t Aw[S::KS], Ab[S::NBB];
+        bf16x8_t Aw[S::KS];
 #pragma unroll
         for (int ks = 0; ks < S::KS; ++ks)
             Aw[ks] = *reinterpret_cast<const bf16x8_t*>(wa_r + 32 * ks);
-#pragma unroll
-        for (int kb = 0; kb < S::NBB; ++kb)
-            Ab[kb] = *reinterpret_cast<const bf16x8_t*>(ba_r + 32 * kb);
-        // The correction is the same for every token: one accumulator, shared
-        // as the starting value of every n-block's chain.
-        f32x4_t s0 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kb = 0; kb < S::NBB; ++kb) s0 = mfma(Ab[kb], unit, s0);
         f32x4_t Sc[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            f32x4_t acc = s0;
+            f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < S::KS; ++ks) {
                 const uint32_t word = r.kc[ks * NSUB + nb / 2];
@@ -963,8 +946,9 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             alpha[e] = 1.f;
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
-                sc[e][nb] = (KP == 3 ? (Sc[nb][2] + Sc[nb][1]) + Sc[nb][0]
-                                     : Sc[nb][2 * e] + Sc[nb][2 * e + 1]) * kProdScale;
+                sc[e][nb] = fmaf(KP == 3 ? (Sc[nb][2] + Sc[nb][1]) + Sc[nb][0]
+                                         : Sc[nb][2 * e] + Sc[nb][2 * e + 1],
+                                 kProdScale, kc[e]);
         }
         const int n_masked = kv_lo - chunk * G;       // leading tokens hidden by padding
         if (__builtin_expect(n_masked > 0, 0)) {
@@ -1313,9 +1297,10 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     if (cid[0] >= 0) {
         stage_meta<S, PAIRED>(buf[0], MT, lane, NG, meta_floats, pslots, smul);
         wave_sync();
-        wprep(Int<0>{});
+        float kc0[HPL];
+        head_corr(wprep(Int<0>{}), kc0);
         wave_sync();
-        any_cur = kside(buf[0], Int<0>{}, cid[0]);
+        any_cur = kside(buf[0], Int<0>{}, cid[0], kc0);
     }
     // Step i (of the wave's chunks, counted from 0) uses double-buffer
     // slot i & 1; PF is even, so within the unrolled ring the slot of step k
@@ -1328,7 +1313,8 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             stage_meta<S, PAIRED>(nxt, MT + nslot * meta_stride, lane, NG, meta_floats, pslots,
                                   smul);
         wave_sync();
-        if (has_next) wprep(Int<nslot>{});
+        float kc[HPL];
+        if (has_next) head_corr(wprep(Int<nslot>{}), kc);
         pprep(Int<slot>{}, any_cur);
         any_cur = false;            // vb now follows the current running max
         wave_sync();
@@ -1342,7 +1328,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         __builtin_amdgcn_s_setprio(2);
         vside(cur);
         after_v();
-        if (has_next) any_cur = kside(nxt, Int<nslot>{}, nxt_chunk);
+        if (has_next) any_cur = kside(nxt, Int<nslot>{}, nxt_chunk, kc);
         __builtin_amdgcn_s_setprio(0);
     };
     static_assert(PF % 2 == 0, "the slot parity of a ring step must be static");
