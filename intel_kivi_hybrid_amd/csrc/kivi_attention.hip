@@ -455,8 +455,10 @@ Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
         // The residual window is taken in whole 16-token passes.  With
         // enough chunks per wave, the last wave of each workgroup takes all of
         // its split's passes while the other three start on chunks, taking
-        // 3 chunks each per pass up front (measured best at config 4);
-        // otherwise every wave takes passes before its chunks.
+        // 3 chunks each per pass up front (measured best at config 4; the
+        // launch doubles it for 8 query rows per kv head, whose passes cost
+        // twice the score work); otherwise every wave takes passes before
+        // its chunks.
         // every split gets at least one chunk
         S = max(1, min(min(S, kMaxSplits), (n_chunks + kWavesPerGroup - 1) / kWavesPerGroup));
         p.chunks_per_wave = (n_chunks + kWavesPerGroup * S - 1) / (kWavesPerGroup * S);
@@ -769,7 +771,11 @@ int attention_impl(const float* q, int32_t q_len, int32_t causal, const int32_t*
                          oi, part_o, part_ml, batch, q_heads, kv_heads, head_dim, group_size_k,
                          group_size_v, chunk_capacity, num_chunks, res_capacity, res_start,
                          res_len, p.n_qsplits, p.chunks_per_wave, p.res_waves,
-                         p.early_per_pass_x2, p.n_splits, softmax_scale * kLog2e, k_new, v_new,
+                         // 8 rows: 6 chunks per pass (B=64, 64/8 heads, 8K
+                         // context: 134.2 -> 130.6 us; 5 and 7 per pass
+                         // 132.4 and 132.6 us)
+                         p.early_per_pass_x2 * (rows >= 8 ? 2 : 1), p.n_splits,
+                         softmax_scale * kLog2e, k_new, v_new,
                          new_sb, new_sh, new_slot, res_dtype, qr, kv_start};
             rc = launch_attention_mfma(L, st);
         } else {
