@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define KIVI_HIP_ABI_VERSION 4
+#define KIVI_HIP_ABI_VERSION 5
 
 #define KIVI_OK 0
 #define KIVI_ERR_INVALID_ARGUMENT 1
@@ -86,6 +86,34 @@ int kivi_quant_dequant_roundtrip_keys(const float* input, float* output,
 int kivi_quant_dequant_roundtrip_values(const float* input, float* output,
                                         int64_t num_tokens, int32_t head_dim,
                                         int32_t group_size, void* stream);
+
+/* The six ops above, each also returning in *event_out a new event handle
+ * (owned by the caller: kivi_event_wait / kivi_event_query /
+ * kivi_event_destroy) that is the completion event of the op's own kernel
+ * launch: the *_async ops of the reference, whose KiviEvent wraps the
+ * submitted kernel's sycl::event (kv_cache_ops.cpp:245-303, event.hpp:16-31).
+ * No marker is queued after the kernel, unlike kivi_event_record.  On error
+ * *event_out is NULL. */
+int kivi_quantize_keys_per_channel_ev(const float* input, uint8_t* output, float* scales,
+                                      float* zeros, int64_t num_channels, int32_t group_size,
+                                      void* stream, void** event_out);
+int kivi_quantize_values_per_token_ev(const float* input, uint8_t* output, float* scales,
+                                      float* zeros, int64_t num_tokens, int32_t head_dim,
+                                      int32_t group_size, void* stream, void** event_out);
+int kivi_dequantize_keys_per_channel_ev(const uint8_t* input, const float* scales,
+                                        const float* zeros, float* output,
+                                        int64_t num_channels, int32_t group_size, void* stream,
+                                        void** event_out);
+int kivi_dequantize_values_per_token_ev(const uint8_t* input, const float* scales,
+                                        const float* zeros, float* output, int64_t num_groups,
+                                        int32_t group_size, void* stream, void** event_out);
+int kivi_quant_dequant_roundtrip_keys_ev(const float* input, float* output,
+                                         int64_t num_channels, int32_t group_size,
+                                         void* stream, void** event_out);
+int kivi_quant_dequant_roundtrip_values_ev(const float* input, float* output,
+                                           int64_t num_tokens, int32_t head_dim,
+                                           int32_t group_size, void* stream,
+                                           void** event_out);
 
 /* ---- HBM-resident packed store --------------------------------------------
  * Replaces KiviCache._flush_group (src/kivi_sycl/cache/manager.py:309-374):

@@ -220,16 +220,15 @@ class KiviEvent:
     ``wait()`` blocks until the work completes and raises ``RuntimeError`` on
     a device-side error; ``query()`` tells, without blocking, whether it has.
     As in the reference, where the event wraps the submitted kernel's own
-    ``sycl::event`` (kv_cache_ops.cpp:245-303), the HIP event is recorded on
-    the op's stream right after the op is enqueued, so ``wait()`` and
-    ``query()`` cover that op alone, whatever is queued behind it later.
+    ``sycl::event`` (kv_cache_ops.cpp:245-303), the HIP event is the
+    completion event of the op's own kernel launch (hipExtLaunchKernel), so
+    ``wait()`` and ``query()`` cover that op alone, whatever is queued behind
+    it later, and no marker sits between it and the next kernel.
 
     Lazy recording is opt-in (:func:`set_lazy_events`): the event is then
-    recorded at the first ``wait()`` or ``query()``, which covers the op and
-    any work queued on the same stream after it.  An op whose event is never
-    consulted then puts no marker between kernels (one marker per submission
-    cost ~3.7 us of GPU time between two config-2 quantise kernels).  The
-    op's tensors and its stream are kept alive until the event is released."""
+    recorded (as a marker) at the first ``wait()`` or ``query()``, which
+    covers the op and any work queued on the same stream after it.  The op's
+    tensors and its stream are kept alive until the event is released."""
 
     __slots__ = ("_device", "_stream", "_ev", "_keep", "_done")
 
@@ -288,26 +287,37 @@ class KiviEvent:
 
 
 def _run(device: torch.device, blocking: bool, what: str, fn, *args, keep=()):
+    """Runs the C-ABI op ``fn`` on the device's current stream.  Blocking:
+    synchronise the stream.  Async (per-op events): the op's ``_ev`` entry
+    point, whose event is the completion event of the op's own kernel launch
+    (no marker queued behind it).  Async with lazy events: the plain entry
+    point, the event recorded at first use."""
     with torch.cuda.device(device):
         stream = torch.cuda.current_stream(device)
-        _native.check(fn(*args, ctypes.c_void_p(stream.cuda_stream)), what)
+        sp = ctypes.c_void_p(stream.cuda_stream)
+        if not blocking and not _lazy_events:
+            handle = ctypes.c_void_p()
+            _native.check(getattr(_lib, fn.__name__ + "_ev")(*args, sp, ctypes.byref(handle)),
+                          what)
+            ev = KiviEvent(device, stream, keep)
+            ev._ev = handle
+            return ev
+        _native.check(fn(*args, sp), what)
         if blocking:
-            _native.check(_lib.kivi_stream_synchronize(ctypes.c_void_p(stream.cuda_stream)), what)
+            _native.check(_lib.kivi_stream_synchronize(sp), what)
             return None
-        ev = KiviEvent(device, stream, keep)
-        if not _lazy_events:
-            ev._record()
-        return ev
+        return KiviEvent(device, stream, keep)
 
 
 _lazy_events = False
 
 
 def set_lazy_events(lazy: bool) -> bool:
-    """Chooses when the ``*_async`` ops record their :class:`KiviEvent`:
-    at submission (the default, the reference's per-op semantics) or, with
-    ``lazy=True``, at the event's first ``wait()``/``query()``.  Returns the
-    previous setting.  Not part of the reference's API."""
+    """Chooses the ``*_async`` ops' :class:`KiviEvent`: the completion event
+    of the op's own kernel launch (the default, the reference's per-op
+    semantics) or, with ``lazy=True``, a marker recorded at the event's first
+    ``wait()``/``query()``.  Returns the previous setting.  Not part of the
+    reference's API."""
     global _lazy_events
     prev, _lazy_events = _lazy_events, bool(lazy)
     return prev

@@ -18,6 +18,7 @@ _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
 _int = ctypes.c_int
+_pvp = ctypes.POINTER(ctypes.c_void_p)
 
 # name -> argtypes; every entry point returns int (status) unless listed in
 # _RESTYPES.
@@ -36,6 +37,12 @@ SIGNATURES = {
     "kivi_dequantize_values_per_token": [_vp, _vp, _vp, _vp, _i64, _i32, _vp],
     "kivi_quant_dequant_roundtrip_keys": [_vp, _vp, _i64, _i32, _vp],
     "kivi_quant_dequant_roundtrip_values": [_vp, _vp, _i64, _i32, _i32, _vp],
+    "kivi_quantize_keys_per_channel_ev": [_vp, _vp, _vp, _vp, _i64, _i32, _vp, _pvp],
+    "kivi_quantize_values_per_token_ev": [_vp, _vp, _vp, _vp, _i64, _i32, _i32, _vp, _pvp],
+    "kivi_dequantize_keys_per_channel_ev": [_vp, _vp, _vp, _vp, _i64, _i32, _vp, _pvp],
+    "kivi_dequantize_values_per_token_ev": [_vp, _vp, _vp, _vp, _i64, _i32, _vp, _pvp],
+    "kivi_quant_dequant_roundtrip_keys_ev": [_vp, _vp, _i64, _i32, _vp, _pvp],
+    "kivi_quant_dequant_roundtrip_values_ev": [_vp, _vp, _i64, _i32, _i32, _vp, _pvp],
     "kivi_store_flush": [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                          _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     "kivi_store_flush_chunks": [_vp, _vp, _i32, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _vp, _vp,

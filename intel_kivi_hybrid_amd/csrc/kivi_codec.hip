@@ -16,6 +16,8 @@
 // lanes).  Each lane turns its 4 floats into one packed byte in registers.
 // Group sizes whose G/4 is not a power of two <= 64 take a one-thread-per-
 // group kernel with the same arithmetic.
+#include <tuple>
+
 #include "kivi_common.hpp"
 #include "../../include/kivi_hip.h"
 
@@ -267,10 +269,35 @@ int check_common(const void* a, const void* b, int64_t n_groups, int32_t G) {
 }  // namespace
 
 // ----------------------------------------------------------------------------
-// Launchers shared with the store kernels.
+// Launchers.
 // ----------------------------------------------------------------------------
+// One kernel launch of kBlock threads per block on `stream`.  With `stop`
+// non-null it goes through hipExtLaunchKernel with `stop` as the launch's
+// completion event: the event is then signalled by the kernel's own
+// dispatch, with no marker packet queued after it (a hipEventRecord marker
+// cost ~3.3 us of GPU time between two back-to-back kernels).  Returns the
+// extended launch's error; the <<<>>> form's is left for check_launch.
+template <class... P, class... A>
+int launch(void (*kernel)(P...), unsigned grid, hipStream_t stream, hipEvent_t stop,
+           A... args) {
+    if (stop == nullptr) {
+        kernel<<<grid, kBlock, 0, stream>>>(static_cast<P>(args)...);
+        return kOk;
+    }
+    std::tuple<P...> vals{static_cast<P>(args)...};
+    void* ptrs[sizeof...(P)];
+    std::apply([&](auto&... v) {
+        int i = 0;
+        ((ptrs[i++] = static_cast<void*>(&v)), ...);
+    }, vals);
+    return check_hip(hipExtLaunchKernel(reinterpret_cast<const void*>(kernel), dim3(grid),
+                                        dim3(kBlock), ptrs, 0, stream, nullptr, stop, 0),
+                     "hipExtLaunchKernel");
+}
+
 int launch_quantize_groups(const float* in, uint8_t* packed, float* scales, float* zeros,
-                           int64_t n_groups, int32_t G, hipStream_t stream) {
+                           int64_t n_groups, int32_t G, hipStream_t stream,
+                           hipEvent_t stop = nullptr) {
     int rc = check_common(in, packed, n_groups, G);
     if (rc) return rc;
     if (scales == nullptr || zeros == nullptr)
@@ -286,8 +313,8 @@ int launch_quantize_groups(const float* in, uint8_t* packed, float* scales, floa
         const bool pair = kQuantVPL == 2 && lanes / kQuantVPL >= 2 && ((uintptr_t)packed % 4) == 0;
         switch (lanes / kQuantVPL) {
 #define KIVI_QV(L) case L: \
-        if (pair) quantize_vec_kernel<L, kQuantVPL, kQuantIters, true><<<grid, kBlock, 0, stream>>>(in4, packed, scales, zeros, n_seg); \
-        else quantize_vec_kernel<L, kQuantVPL, kQuantIters, false><<<grid, kBlock, 0, stream>>>(in4, packed, scales, zeros, n_seg); \
+        if (pair) rc = launch(quantize_vec_kernel<L, kQuantVPL, kQuantIters, true>, grid, stream, stop, in4, packed, scales, zeros, n_seg); \
+        else rc = launch(quantize_vec_kernel<L, kQuantVPL, kQuantIters, false>, grid, stream, stop, in4, packed, scales, zeros, n_seg); \
         break;
             KIVI_QV(1) KIVI_QV(2) KIVI_QV(4) KIVI_QV(8) KIVI_QV(16) KIVI_QV(32) KIVI_QV(64)
 #undef KIVI_QV
@@ -296,19 +323,19 @@ int launch_quantize_groups(const float* in, uint8_t* packed, float* scales, floa
         const unsigned grid = grid_for(n_vec, kBlock * kUnroll);
         const float4* in4 = reinterpret_cast<const float4*>(in);
         switch (lanes) {
-#define KIVI_Q(L) case L: quantize_seg_kernel<L><<<grid, kBlock, 0, stream>>>(in4, packed, scales, zeros, n_vec); break;
+#define KIVI_Q(L) case L: rc = launch(quantize_seg_kernel<L>, grid, stream, stop, in4, packed, scales, zeros, n_vec); break;
             KIVI_Q(1) KIVI_Q(2) KIVI_Q(4) KIVI_Q(8) KIVI_Q(16) KIVI_Q(32) KIVI_Q(64)
 #undef KIVI_Q
         }
     } else {
-        quantize_serial_kernel<<<grid_for(n_groups, kBlock), kBlock, 0, stream>>>(
-            in, packed, scales, zeros, n_groups, G);
+        rc = launch(quantize_serial_kernel, grid_for(n_groups, kBlock), stream, stop, in, packed, scales, zeros, n_groups, G);
     }
+    if (rc) return rc;
     return check_launch("quantize");
 }
 
 int launch_roundtrip_groups(const float* in, float* out, int64_t n_groups, int32_t G,
-                            hipStream_t stream) {
+                            hipStream_t stream, hipEvent_t stop = nullptr) {
     int rc = check_common(in, out, n_groups, G);
     if (rc) return rc;
     const int lanes = G / 4;
@@ -319,19 +346,20 @@ int launch_roundtrip_groups(const float* in, float* out, int64_t n_groups, int32
         const float4* in4 = reinterpret_cast<const float4*>(in);
         float4* out4 = reinterpret_cast<float4*>(out);
         switch (lanes) {
-#define KIVI_R(L) case L: roundtrip_seg_kernel<L><<<grid, kBlock, 0, stream>>>(in4, out4, n_vec); break;
+#define KIVI_R(L) case L: rc = launch(roundtrip_seg_kernel<L>, grid, stream, stop, in4, out4, n_vec); break;
             KIVI_R(1) KIVI_R(2) KIVI_R(4) KIVI_R(8) KIVI_R(16) KIVI_R(32) KIVI_R(64)
 #undef KIVI_R
         }
     } else {
-        roundtrip_serial_kernel<<<grid_for(n_groups, kBlock), kBlock, 0, stream>>>(
-            in, out, n_groups, G);
+        rc = launch(roundtrip_serial_kernel, grid_for(n_groups, kBlock), stream, stop, in, out, n_groups, G);
     }
+    if (rc) return rc;
     return check_launch("quant_dequant_roundtrip");
 }
 
 int launch_dequantize_groups(const uint8_t* packed, const float* scales, const float* zeros,
-                             float* out, int64_t n_groups, int32_t G, hipStream_t stream) {
+                             float* out, int64_t n_groups, int32_t G, hipStream_t stream,
+                             hipEvent_t stop = nullptr) {
     int rc = check_common(packed, out, n_groups, G);
     if (rc) return rc;
     if (scales == nullptr || zeros == nullptr)
@@ -342,15 +370,16 @@ int launch_dequantize_groups(const uint8_t* packed, const float* scales, const f
     const bool al = aligned16(out);
     switch (bpg) {
 #define KIVI_D(L) case L: \
-        if (al) dequantize_kernel<L, true><<<grid, kBlock, 0, stream>>>(packed, scales, zeros, out, n_bytes, bpg); \
-        else dequantize_kernel<L, false><<<grid, kBlock, 0, stream>>>(packed, scales, zeros, out, n_bytes, bpg); \
+        if (al) rc = launch(dequantize_kernel<L, true>, grid, stream, stop, packed, scales, zeros, out, n_bytes, bpg); \
+        else rc = launch(dequantize_kernel<L, false>, grid, stream, stop, packed, scales, zeros, out, n_bytes, bpg); \
         break;
         KIVI_D(1) KIVI_D(2) KIVI_D(4) KIVI_D(8) KIVI_D(16) KIVI_D(32) KIVI_D(64)
 #undef KIVI_D
         default:
-            if (al) dequantize_kernel<0, true><<<grid, kBlock, 0, stream>>>(packed, scales, zeros, out, n_bytes, bpg);
-            else dequantize_kernel<0, false><<<grid, kBlock, 0, stream>>>(packed, scales, zeros, out, n_bytes, bpg);
+            if (al) rc = launch(dequantize_kernel<0, true>, grid, stream, stop, packed, scales, zeros, out, n_bytes, bpg);
+            else rc = launch(dequantize_kernel<0, false>, grid, stream, stop, packed, scales, zeros, out, n_bytes, bpg);
     }
+    if (rc) return rc;
     return check_launch("dequantize");
 }
 
@@ -417,6 +446,93 @@ int kivi_quant_dequant_roundtrip_values(const float* input, float* output,
     if (rc) return rc;
     return launch_roundtrip_groups(input, output, num_tokens * (head_dim / group_size),
                                    group_size, (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+// A new event (timing disabled) handed to `fn` as the stop event of the op's
+// kernel launch, and to the caller through *event_out on success.
+template <class F>
+static int with_stop_event(void** event_out, F&& fn) {
+    if (event_out == nullptr)
+        return set_error(kErrInvalidArgument, "event_out must not be null");
+    *event_out = nullptr;
+    hipEvent_t ev = nullptr;
+    int rc = check_hip(hipEventCreateWithFlags(&ev, hipEventDisableTiming),
+                       "hipEventCreateWithFlags");
+    if (rc) return rc;
+    rc = fn(ev);
+    if (rc) {
+        (void)hipEventDestroy(ev);
+        return rc;
+    }
+    *event_out = (void*)ev;
+    return kOk;
+}
+
+extern "C" {
+
+int kivi_quantize_keys_per_channel_ev(const float* input, uint8_t* output, float* scales,
+                                      float* zeros, int64_t num_channels, int32_t group_size,
+                                      void* stream, void** event_out) {
+    return with_stop_event(event_out, [&](hipEvent_t ev) {
+        return launch_quantize_groups(input, output, scales, zeros, num_channels, group_size,
+                                      (hipStream_t)stream, ev);
+    });
+}
+
+int kivi_quantize_values_per_token_ev(const float* input, uint8_t* output, float* scales,
+                                      float* zeros, int64_t num_tokens, int32_t head_dim,
+                                      int32_t group_size, void* stream, void** event_out) {
+    if (event_out) *event_out = nullptr;
+    int rc = check_values(num_tokens, head_dim, group_size);
+    if (rc) return rc;
+    return with_stop_event(event_out, [&](hipEvent_t ev) {
+        return launch_quantize_groups(input, output, scales, zeros,
+                                      num_tokens * (head_dim / group_size), group_size,
+                                      (hipStream_t)stream, ev);
+    });
+}
+
+int kivi_dequantize_keys_per_channel_ev(const uint8_t* input, const float* scales,
+                                        const float* zeros, float* output,
+                                        int64_t num_channels, int32_t group_size, void* stream,
+                                        void** event_out) {
+    return with_stop_event(event_out, [&](hipEvent_t ev) {
+        return launch_dequantize_groups(input, scales, zeros, output, num_channels, group_size,
+                                        (hipStream_t)stream, ev);
+    });
+}
+
+int kivi_dequantize_values_per_token_ev(const uint8_t* input, const float* scales,
+                                        const float* zeros, float* output, int64_t num_groups,
+                                        int32_t group_size, void* stream, void** event_out) {
+    return with_stop_event(event_out, [&](hipEvent_t ev) {
+        return launch_dequantize_groups(input, scales, zeros, output, num_groups, group_size,
+                                        (hipStream_t)stream, ev);
+    });
+}
+
+int kivi_quant_dequant_roundtrip_keys_ev(const float* input, float* output,
+                                         int64_t num_channels, int32_t group_size,
+                                         void* stream, void** event_out) {
+    return with_stop_event(event_out, [&](hipEvent_t ev) {
+        return launch_roundtrip_groups(input, output, num_channels, group_size,
+                                       (hipStream_t)stream, ev);
+    });
+}
+
+int kivi_quant_dequant_roundtrip_values_ev(const float* input, float* output,
+                                           int64_t num_tokens, int32_t head_dim,
+                                           int32_t group_size, void* stream,
+                                           void** event_out) {
+    if (event_out) *event_out = nullptr;
+    int rc = check_values(num_tokens, head_dim, group_size);
+    if (rc) return rc;
+    return with_stop_event(event_out, [&](hipEvent_t ev) {
+        return launch_roundtrip_groups(input, output, num_tokens * (head_dim / group_size),
+                                       group_size, (hipStream_t)stream, ev);
+    });
 }
 
 }  // extern "C"

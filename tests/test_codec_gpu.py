@@ -319,3 +319,45 @@ def test_lazy_event_recorded_at_first_use(C):
         assert np.array_equal(_bits(out.cpu()).reshape(-1), ref.view(np.uint32).reshape(-1))
     finally:
         C.set_lazy_events(prev)
+
+
+def test_launch_event_entry_points(C):
+    """The ``*_ev`` C-ABI entry points (the ``*_async`` ops' path) hand back
+    the completion event of the op's own kernel launch: a live handle whose
+    wait returns once the op is done, with exact results; on a rejected
+    argument the handle stays NULL and the error code comes back."""
+    import ctypes
+    lib = C._lib
+    x = seeded_kv((2, 4, 64, 128), seed=29, kind="key")
+    xd = x.cuda()
+    n = xd.numel()
+    packed = torch.empty(n // 4, dtype=torch.uint8, device="cuda:0")
+    scales = torch.empty(n // 32, device="cuda:0")
+    zeros = torch.empty(n // 32, device="cuda:0")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ev = ctypes.c_void_p()
+    rc = lib.kivi_quantize_keys_per_channel_ev(xd.data_ptr(), packed.data_ptr(),
+                                               scales.data_ptr(), zeros.data_ptr(), n // 32, 32,
+                                               stream, ctypes.byref(ev))
+    assert rc == 0 and ev.value
+    assert lib.kivi_event_wait(ev) == 0
+    assert lib.kivi_event_query(ev) == 1
+    assert lib.kivi_event_destroy(ev) == 0
+    op, os_, oz = codec.quantize_groups(x.numpy(), 32)
+    assert np.array_equal(packed.cpu().numpy(), op)
+    assert np.array_equal(scales.cpu().numpy(), os_)
+    out = torch.empty_like(xd)
+    ev = ctypes.c_void_p()
+    rc = lib.kivi_quant_dequant_roundtrip_values_ev(xd.data_ptr(), out.data_ptr(), n // 128, 128,
+                                                    32, stream, ctypes.byref(ev))
+    assert rc == 0 and ev.value
+    assert lib.kivi_event_wait(ev) == 0
+    lib.kivi_event_destroy(ev)
+    ref = codec.roundtrip_groups(x.numpy(), 32)
+    assert np.array_equal(_bits(out.cpu()).reshape(-1), ref.view(np.uint32).reshape(-1))
+    ev = ctypes.c_void_p(1234)
+    rc = lib.kivi_quantize_values_per_token_ev(xd.data_ptr(), packed.data_ptr(), scales.data_ptr(),
+                                               zeros.data_ptr(), n // 128, 128, 3, stream,
+                                               ctypes.byref(ev))
+    assert rc == 1                          # KIVI_ERR_INVALID_ARGUMENT
+    assert ev.value is None
