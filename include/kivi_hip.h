@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define KIVI_HIP_ABI_VERSION 5
+#define KIVI_HIP_ABI_VERSION 6
 
 #define KIVI_OK 0
 #define KIVI_ERR_INVALID_ARGUMENT 1
@@ -306,6 +306,33 @@ int kivi_packed_attention(const float* q, int32_t q_len, int32_t causal,
                           int32_t group_size_v, int32_t chunk_capacity, int32_t num_chunks,
                           int32_t res_capacity, int32_t res_start, int32_t res_len,
                           float softmax_scale, int32_t num_splits, void* stream);
+
+/* kivi_packed_attention with any padding pattern: hidden (NULL: none) holds
+ * one row of hidden_stride uint32 words per sequence, bit p % 32 of word
+ * p / 32 of row b set when context position p (0 .. num_chunks*G + res_len
+ * - 1: the quantised tokens, then the window oldest first) is hidden from
+ * every query token of sequence b; hidden_stride >= ceil(context / 32).
+ * Positions before kv_start[b] (if given) are hidden as well, and causal
+ * queries see the window up to themselves as in kivi_packed_attention.  A
+ * query row that sees no position at all (padding rows) gets zeros.  Covers
+ * HF attention masks of right-padded batches and batches with holes: a
+ * key-padding mask combined with the causal rule (the reference feeds any
+ * such mask to HF attention over get_full_cache(),
+ * src/kivi_sycl/generation/generate.py:76 and
+ * src/kivi_sycl/cache/manager.py:251-290). */
+int kivi_packed_attention_masked(const float* q, int32_t q_len, int32_t causal,
+                                 const int32_t* kv_start, const uint32_t* hidden,
+                                 int64_t hidden_stride, const uint8_t* k_codes,
+                                 const float* k_scale, const float* k_zero,
+                                 const uint8_t* v_codes, const float* v_scale,
+                                 const float* v_zero, const void* k_res, const void* v_res,
+                                 int32_t res_dtype, float* out, void* workspace,
+                                 size_t workspace_bytes, int32_t batch, int32_t q_heads,
+                                 int32_t kv_heads, int32_t head_dim, int32_t group_size_k,
+                                 int32_t group_size_v, int32_t chunk_capacity,
+                                 int32_t num_chunks, int32_t res_capacity, int32_t res_start,
+                                 int32_t res_len, float softmax_scale, int32_t num_splits,
+                                 void* stream);
 
 /* kivi_packed_decode_attention with this step's new token appended in the
  * same launch: the window (res_start, res_len) already counts the new token

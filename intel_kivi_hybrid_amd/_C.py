@@ -16,6 +16,7 @@ through the C ABI of ``libkivi_hip.so``; nothing here computes on the host.
 from __future__ import annotations
 
 import ctypes
+import functools
 
 import torch
 
@@ -518,8 +519,26 @@ def packed_decode_attention(q, store, softmax_scale=None, out=None, num_splits=0
     return out
 
 
+def hidden_positions(key_mask, device=None):
+    """The hidden-position words of kivi_packed_attention_masked from a
+    key-padding mask ``[B, T]`` (HF's 2-D ``attention_mask`` convention:
+    nonzero / True = the position is attended): ``[B, ceil(T / 32)]`` int32,
+    bit ``p % 32`` of word ``p // 32`` of row b set when position p of
+    sequence b is hidden.  Computed on ``device`` (default: the mask's)."""
+    _check(torch.is_tensor(key_mask) and key_mask.dim() == 2,
+           "key_mask must be a [B, T] tensor")
+    dev = key_mask.device if device is None else torch.device(device)
+    vis = key_mask.to(dev) != 0
+    B, T = vis.shape
+    W = (T + 31) // 32
+    bits = torch.zeros(B, W * 32, dtype=torch.int64, device=dev)
+    bits[:, :T] = (~vis).to(torch.int64)
+    words = (bits.view(B, W, 32) << torch.arange(32, device=dev)).sum(-1)    # < 2^32
+    return torch.where(words >= 2 ** 31, words - 2 ** 32, words).to(torch.int32)
+
+
 def packed_attention(q, store, causal=True, softmax_scale=None, out=None, num_splits=0,
-                     workspace=None, kv_start=None):
+                     workspace=None, kv_start=None, key_mask=None, hidden=None):
     """Attention of ``L`` query tokens per sequence over a
     :class:`PackedKVStore`, ``q [B, Hq, L, D]`` fp32 (the layout HF attention
     functions receive); returns ``[B, L, Hq, D]`` fp32 (the layout they
@@ -529,8 +548,13 @@ def packed_attention(q, store, causal=True, softmax_scale=None, out=None, num_sp
     context (one query token sees it either way).  ``kv_start`` (B ints, a
     list or an int32 tensor): sequence b's first visible context position,
     for a left-padded batch; positions before it take no weight.  Checked
-    against the context length when given on the host.  Launched on the
-    current stream."""
+    against the context length when given on the host.  ``key_mask``
+    ``[B, T]`` over the whole context (T = quantised + window tokens; nonzero
+    = attended, HF's 2-D padding mask), or ``hidden`` (its words,
+    :func:`hidden_positions`, computed once for many calls): any other
+    padding pattern (right padding, holes), hidden from every query token;
+    a query row that sees no position gets zeros.  Launched on the current
+    stream."""
     _check(q.dtype == torch.float32, "q must be float32, got ", _dtype_name(q.dtype))
     _check(q.dim() == 4 and q.shape[0] == store.B and q.shape[3] == store.D,
            "q must be [B, Hq, L, D] matching the store, got ", tuple(q.shape))
@@ -554,6 +578,18 @@ def packed_attention(q, store, causal=True, softmax_scale=None, out=None, num_sp
                kv_start.is_contiguous(), "kv_start must be a contiguous int32 tensor of ", B,
                " positions")
         ks_ptr = kv_start.data_ptr()
+    if key_mask is not None:
+        _check(hidden is None, "pass key_mask or hidden, not both")
+        T = store.quantized_tokens + store.res_len
+        _check(tuple(key_mask.shape) == (B, T), "key_mask must be [B=", B, ", T=", T,
+               "] over the whole context, got ", tuple(key_mask.shape))
+        hidden = hidden_positions(key_mask, q.device)
+    if hidden is not None:
+        W = (store.quantized_tokens + store.res_len + 31) // 32
+        _check(hidden.dtype == torch.int32 and hidden.dim() == 2 and hidden.shape[0] == B and
+               hidden.shape[1] >= W and hidden.stride(1) == 1 and hidden.device == q.device,
+               "hidden must be an int32 [B, >=", W, "] tensor with contiguous rows on the "
+               "query's device")
     qk = q.transpose(1, 2).contiguous()                                  # [B, L, Hq, D]
     if out is None:
         out = torch.empty(B, L, Hq, D, dtype=torch.float32, device=q.device)
@@ -569,9 +605,16 @@ def packed_attention(q, store, causal=True, softmax_scale=None, out=None, num_sp
         _check(workspace.is_contiguous() and workspace.numel() * workspace.element_size() >= need,
                "workspace must be contiguous and hold ", need, " bytes")
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    if hidden is not None:
+        entry = functools.partial(_lib.kivi_packed_attention_masked,
+                                  ctypes.c_void_p(qk.data_ptr()), L, 1 if causal else 0,
+                                  ctypes.c_void_p(ks_ptr), ctypes.c_void_p(hidden.data_ptr()),
+                                  hidden.stride(0))
+    else:
+        entry = functools.partial(_lib.kivi_packed_attention, ctypes.c_void_p(qk.data_ptr()),
+                                  L, 1 if causal else 0, ctypes.c_void_p(ks_ptr))
     with on_device(q.device):
-        _native.check(_lib.kivi_packed_attention(
-            ctypes.c_void_p(qk.data_ptr()), L, 1 if causal else 0, ctypes.c_void_p(ks_ptr),
+        _native.check(entry(
             ctypes.c_void_p(store.k_codes.data_ptr()),
             ctypes.c_void_p(store.k_scale.data_ptr()), ctypes.c_void_p(store.k_zero.data_ptr()),
             ctypes.c_void_p(store.v_codes.data_ptr()), ctypes.c_void_p(store.v_scale.data_ptr()),

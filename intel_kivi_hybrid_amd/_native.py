@@ -66,6 +66,10 @@ SIGNATURES = {
     "kivi_packed_attention": [_vp, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
                               _vp, _vp, ctypes.c_size_t, _i32, _i32, _i32, _i32, _i32, _i32,
                               _i32, _i32, _i32, _i32, _i32, _f32, _i32, _vp],
+    "kivi_packed_attention_masked": [_vp, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp,
+                                     _vp, _vp, _vp, _i32, _vp, _vp, ctypes.c_size_t, _i32, _i32,
+                                     _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
+                                     _i32, _vp],
     "kivi_packed_decode_attention_noalloc": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
                                              _vp, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                              _i32, _i32, _i32, _i32, _f32, _i32, _vp],

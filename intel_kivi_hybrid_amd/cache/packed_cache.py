@@ -27,7 +27,12 @@ the 128 B the 2-bit store holds.  Here the cache plugs into the model's own
   the reference's flow computes when the model is handed
   get_full_cache() and a multi-token input.  Its flushes wait for the next
   update, so crop() can still drop any of those tokens (assisted decoding
-  discards the rejected drafts that way).
+  discards the rejected drafts that way);
+* a padded batch's mask (HF's ``[B, 1, q_len, kv_len]``: hidden key
+  positions, causal among the new tokens) reaches the kernels as each
+  sequence's first visible position (left padding) or as hidden-position
+  bits (right padding, holes); the reference hands any mask to HF attention
+  over get_full_cache() (generate.py:76).
 
 The served-cache path (:class:`KiviCache` with ``get_full_cache()``) stays the
 drop-in for the reference's control flow; this class is the fast path for
@@ -45,6 +50,7 @@ from transformers.integrations.sdpa_attention import sdpa_attention_forward
 from transformers.masking_utils import AttentionMaskInterface, causal_mask_function, sdpa_mask
 from transformers.modeling_utils import AttentionInterface
 
+from .. import _C
 from ..config.model_config import detect_model_config
 from ..extension.loader import kivi_native  # noqa: F401  (fails loudly without the HIP library)
 from ..store import PackedKVStore, decode_geometry_error
@@ -202,21 +208,26 @@ class KiviPackedLayer(CacheLayerMixin):
 
     # --------------------------------------------------------- attention
     def attend(self, query: torch.Tensor, scaling: Optional[float],
-               kv_start: Optional[torch.Tensor] = None) -> torch.Tensor:
+               kv_start: Optional[torch.Tensor] = None,
+               hidden: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Attention of ``query [B, Hq, L, D]`` (the step's L new tokens, the
         window's newest) over this layer's store, causal among them; returns
         ``[B, L, Hq, D]`` in the query's dtype and device.  ``kv_start``
         (int32 ``[B]`` on the store's device): each sequence's first visible
-        position, for a left-padded batch.  A one-token step does its flushes
-        now; a longer one leaves them to the next update."""
+        position, for a left-padded batch; ``hidden`` (int32 words,
+        ``_C.hidden_positions``): any other padding pattern.  A one-token
+        step does its flushes now; a longer one leaves them to the next
+        update."""
         st = self.store
         L = query.shape[2]
         if L == 1:
             q = query[:, :, 0, :].to(st.device, torch.float32).contiguous()
-            o = st.attention(q, softmax_scale=scaling, kv_start=kv_start).unsqueeze(1)
+            o = st.attention(q, softmax_scale=scaling, kv_start=kv_start,
+                             hidden=hidden).unsqueeze(1)
         else:
             q = query.to(st.device, torch.float32)
-            o = st.attention(q, softmax_scale=scaling, causal=True, kv_start=kv_start)
+            o = st.attention(q, softmax_scale=scaling, causal=True, kv_start=kv_start,
+                             hidden=hidden)
         self._awaiting_attention = False
         if L == 1:
             self.settle()
@@ -464,40 +475,54 @@ def kivi_packed_attention_forward(module, query, key, value, attention_mask, sca
     for name in ("sliding_window", "softcap", "s_aux"):
         if kwargs.get(name) is not None:
             raise NotImplementedError(f"'{KIVI_ATTENTION}' attention does not support {name}")
-    kv_start = None
+    kv_start = hidden = None
     if attention_mask is not None:
-        kv_start = _padding_starts(owner, attention_mask, query.shape[2],
-                                   layer.get_seq_length(), layer.store.device)
-    return layer.attend(query, scaling, kv_start), None
+        kv_start, hidden = _mask_plan(owner, attention_mask, query.shape[2],
+                                      layer.get_seq_length(), layer.store.device)
+    return layer.attend(query, scaling, kv_start, hidden), None
 
 
-def _padding_starts(owner: "KiviPackedCache", mask: torch.Tensor, q_len: int, kv_len: int,
-                    device) -> torch.Tensor:
-    """Each sequence's first visible position from HF's boolean mask
-    ``[B, 1, q_len, kv_len]`` (True = attend) of a left-padded batch: the
-    mask must be exactly "position >= start[b], and causal among the new
-    tokens", which is checked (one device sync per forward: every layer gets
-    the same mask object, read once).  Anything else -- right padding, holes,
-    a float mask -- is refused."""
+def _mask_plan(owner: "KiviPackedCache", mask: torch.Tensor, q_len: int, kv_len: int, device):
+    """How the packed kernels apply HF's attention mask ``[B, 1, q_len,
+    kv_len]`` (bool: True = attend; float: 0 = attend, at most half the
+    dtype's lowest value = hidden): ``(kv_start, None)`` with each
+    sequence's first visible position for a left-padded batch, else
+    ``(None, hidden)`` with the hidden-position words of any other
+    key-padding pattern (right padding, holes).  The mask must be exactly
+    "the newest token's visible positions, causal among the new tokens",
+    which is checked (one device sync per forward: every layer gets the same
+    mask object, read once); anything else -- an additive bias, a
+    per-query pattern other than causal -- is refused."""
     memo = owner._mask_memo
     if memo is not None and memo[0] is mask:
         return memo[1]
-    starts = None
-    if mask.dtype == torch.bool and mask.dim() == 4 and mask.shape[1] == 1 and \
-            tuple(mask.shape[2:]) == (q_len, kv_len):
-        s = mask[:, 0, -1, :].int().argmax(-1)                    # first visible of the newest
-        t = torch.arange(kv_len, device=mask.device)
-        newest = kv_len - q_len + torch.arange(q_len, device=mask.device)
-        expect = (t[None, None, :] >= s[:, None, None]) & (t[None, None, :] <= newest[None, :, None])
-        if torch.equal(mask[:, 0], expect):
-            starts = s.to(device=device, dtype=torch.int32)
-    if starts is None:
+    plan = None
+    if mask.dim() == 4 and mask.shape[1] == 1 and tuple(mask.shape[2:]) == (q_len, kv_len):
+        m = mask[:, 0]
+        attend = None
+        if m.dtype == torch.bool:
+            attend = m
+        elif m.is_floating_point():
+            low = torch.finfo(m.dtype).min / 2
+            if bool(((m == 0) | (m <= low)).all()):
+                attend = m == 0
+        if attend is not None:
+            vis = attend[:, -1, :]                      # the newest token's visible positions
+            t = torch.arange(kv_len, device=mask.device)
+            newest = kv_len - q_len + torch.arange(q_len, device=mask.device)
+            if torch.equal(attend, vis[:, None, :] & (t[None, None, :] <= newest[None, :, None])):
+                s = vis.int().argmax(-1)                # first visible position
+                if torch.equal(vis, t[None, :] >= s[:, None]):
+                    plan = (s.to(device=device, dtype=torch.int32), None)
+                else:
+                    plan = (None, _C.hidden_positions(vis, device))
+    if plan is None:
         raise NotImplementedError(
-            f"'{KIVI_ATTENTION}' attention over the cache takes the mask of a left-padded batch "
-            f"(each sequence hides its first positions, causal among the new tokens); this "
-            f"mask is something else (shape {tuple(mask.shape)}, dtype {mask.dtype})")
-    owner._mask_memo = (mask, starts)
-    return starts
+            f"'{KIVI_ATTENTION}' attention over the cache takes HF's mask of a padded batch "
+            f"(hidden key positions, causal among the new tokens); this mask is something "
+            f"else (shape {tuple(mask.shape)}, dtype {mask.dtype})")
+    owner._mask_memo = (mask, plan)
+    return plan
 
 
 def kivi_causal_mask(batch_size: int, q_length: int, kv_length: int, q_offset: int = 0,

@@ -55,6 +55,8 @@ struct AttnArgs {
     int res_dt;        // 0 fp32, 1 bf16, 2 fp16
     QueryRows qr;      // HG query rows per kv head (kivi_attention.hpp)
     const int32_t* kv_start;   // [B] first visible position, or nullptr
+    const uint32_t* hidden;    // per-sequence hidden-position bits (AttnLaunch), or nullptr
+    int64_t hidden_stride;
 };
 
 __device__ __forceinline__ void wave_sync() {
@@ -98,6 +100,8 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
     const int64_t bh = (int64_t)b * a.Hkv + kvh;
     // left padding: context positions before kv_lo take no weight
     const int kv_lo = a.kv_start ? a.kv_start[b] : 0;
+    // any other padding pattern: the sequence's hidden-position bits
+    const uint32_t* hid_row = a.hidden ? a.hidden + b * a.hidden_stride : nullptr;
 
     for (int e = threadIdx.x; e < HG * D; e += kAttnBlock) {
         const int h = e / D, d = e % D;
@@ -141,7 +145,8 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
             for (int h = 0; h < HG; ++h) bias[h] = wave_sum(bpart[h]);
             wave_sync();
             const int t = lane;
-            valid = t < G && u * G + t >= kv_lo;
+            valid = t < G && u * G + t >= kv_lo &&
+                    !(hid_row && position_hidden(hid_row, u * G + t));
             float acc[HG];
 #pragma unroll
             for (int h = 0; h < HG; ++h) acc[h] = 0.f;
@@ -175,7 +180,8 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
             rbase = (u - a.n_chunks) * kWave;
             rcount = min(kWave, a.res_len - rbase);
             const int t = rbase + lane;
-            valid = lane < rcount && a.n_chunks * G + t >= kv_lo;
+            valid = lane < rcount && a.n_chunks * G + t >= kv_lo &&
+                    !(hid_row && position_hidden(hid_row, a.n_chunks * G + t));
             float acc[HG];
 #pragma unroll
             for (int h = 0; h < HG; ++h) acc[h] = 0.f;
@@ -293,7 +299,8 @@ __global__ __launch_bounds__(kAttnBlock) void attn_generic_kernel(AttnArgs a) {
         }
         if (!a.qr.real(h)) continue;     // a padding row
         if (a.n_splits == 1) {
-            a.out[a.qr.row(b, kvh, h, a.Hq, D) + d] = acc / L;
+            // (a row with no visible position -- every one hidden -- gives 0)
+            a.out[a.qr.row(b, kvh, h, a.Hq, D) + d] = L > 0.f ? acc / L : 0.f;
         } else {
             const int64_t row = (prow0 + h) * a.n_splits + split;
             a.part_o[row * D + d] = acc;
@@ -362,7 +369,7 @@ __global__ __launch_bounds__(kMaxD) void attn_merge_kernel(const float* __restri
             acc = fmaf(wl[s], po[(int64_t)s * D], acc);
             L = fmaf(wl[s], wl[S + s], L);
         }
-        orow[d] = acc / L;
+        orow[d] = L > 0.f ? acc / L : 0.f;      // 0: every position hidden
     }
 }
 
@@ -403,7 +410,8 @@ __global__ __launch_bounds__(kMaxD) void attn_merge_regs_kernel(const float* __r
             L = fmaf(w, lane_f(l_s, s), L);
         }
     }
-    if ((int)threadIdx.x < D) out[qr.row(blockIdx.y, kvh, v, Hq, D) + d] = acc / L;
+    if ((int)threadIdx.x < D)        // 0: every position hidden
+        out[qr.row(blockIdx.y, kvh, v, Hq, D) + d] = L > 0.f ? acc / L : 0.f;
 }
 
 struct Plan {
@@ -665,7 +673,7 @@ size_t workspace_for(int batch, int q_len, int q_heads, int kv_heads, int head_d
 // query heads of a kv head in groups of 8 when there are more; each launch
 // streams the store once.
 int attention_impl(const float* q, int32_t q_len, int32_t causal, const int32_t* kv_start,
-                   const uint8_t* k_codes,
+                   const uint32_t* hidden, int64_t hidden_stride, const uint8_t* k_codes,
                    const float* k_scale, const float* k_zero, const uint8_t* v_codes,
                    const float* v_scale, const float* v_zero, const void* k_res,
                    const void* v_res, int32_t res_dtype, float* out, void* workspace,
@@ -695,6 +703,13 @@ int attention_impl(const float* q, int32_t q_len, int32_t causal, const int32_t*
                          "window (res_len %d)", q_len, res_len);
     if (k_new && q_len != 1)
         return set_error(kErrInvalidArgument, "the fused append takes one query token");
+    if (hidden) {
+        const int64_t words = ((int64_t)num_chunks * group_size_k + res_len + 31) / 32;
+        if ((uintptr_t)hidden % 4 || hidden_stride < words)
+            return set_error(kErrInvalidArgument,
+                             "hidden-position rows need %lld 4-byte-aligned words per sequence "
+                             "(stride %lld)", (long long)words, (long long)hidden_stride);
+    }
     const int layout = code_layout_for(head_dim, group_size_k, group_size_v);
     if (num_chunks > 0) {
         if (!k_codes || !k_scale || !k_zero || !v_codes || !v_scale || !v_zero)
@@ -776,14 +791,15 @@ int attention_impl(const float* q, int32_t q_len, int32_t causal, const int32_t*
                          // 132.4 and 132.6 us)
                          p.early_per_pass_x2 * (rows >= 8 ? 2 : 1), p.n_splits,
                          softmax_scale * kLog2e, k_new, v_new,
-                         new_sb, new_sh, new_slot, res_dtype, qr, kv_start};
+                         new_sb, new_sh, new_slot, res_dtype, qr, kv_start, hidden,
+                         hidden_stride};
             rc = launch_attention_mfma(L, st);
         } else {
             AttnArgs a{qi, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res, v_res, oi,
                        part_o, part_ml, q_heads, kv_heads, head_dim, group_size_k, group_size_v,
                        chunk_capacity, num_chunks, res_capacity, res_start, res_len, p.n_units,
                        p.n_splits, p.units_per_split, softmax_scale * kLog2e, res_dtype, qr,
-                       kv_start};
+                       kv_start, hidden, hidden_stride};
             const dim3 grid(p.n_splits, kv_heads, batch);
             const size_t lds = (size_t)(rows * head_dim +
                                         kAttnWaves * (rows * head_dim + rows * kWave)) *
@@ -853,11 +869,32 @@ int kivi_packed_attention(const float* q, int32_t q_len, int32_t causal,
                           int32_t group_size_v, int32_t chunk_capacity, int32_t num_chunks,
                           int32_t res_capacity, int32_t res_start, int32_t res_len,
                           float softmax_scale, int32_t num_splits, void* stream) {
-    return attention_impl(q, q_len, causal, kv_start, k_codes, k_scale, k_zero, v_codes,
-                          v_scale, v_zero, k_res, v_res, res_dtype, out, workspace,
+    return attention_impl(q, q_len, causal, kv_start, nullptr, 0, k_codes, k_scale, k_zero,
+                          v_codes, v_scale, v_zero, k_res, v_res, res_dtype, out, workspace,
                           workspace_bytes, batch, q_heads, kv_heads, head_dim, group_size_k,
                           group_size_v, chunk_capacity, num_chunks, res_capacity, res_start,
                           res_len, softmax_scale, num_splits, nullptr, nullptr, 0, 0, stream);
+}
+
+int kivi_packed_attention_masked(const float* q, int32_t q_len, int32_t causal,
+                                 const int32_t* kv_start, const uint32_t* hidden,
+                                 int64_t hidden_stride, const uint8_t* k_codes,
+                                 const float* k_scale, const float* k_zero,
+                                 const uint8_t* v_codes, const float* v_scale,
+                                 const float* v_zero, const void* k_res, const void* v_res,
+                                 int32_t res_dtype, float* out, void* workspace,
+                                 size_t workspace_bytes, int32_t batch, int32_t q_heads,
+                                 int32_t kv_heads, int32_t head_dim, int32_t group_size_k,
+                                 int32_t group_size_v, int32_t chunk_capacity,
+                                 int32_t num_chunks, int32_t res_capacity, int32_t res_start,
+                                 int32_t res_len, float softmax_scale, int32_t num_splits,
+                                 void* stream) {
+    return attention_impl(q, q_len, causal, kv_start, hidden, hidden_stride, k_codes, k_scale,
+                          k_zero, v_codes, v_scale, v_zero, k_res, v_res, res_dtype, out,
+                          workspace, workspace_bytes, batch, q_heads, kv_heads, head_dim,
+                          group_size_k, group_size_v, chunk_capacity, num_chunks, res_capacity,
+                          res_start, res_len, softmax_scale, num_splits, nullptr, nullptr, 0, 0,
+                          stream);
 }
 
 int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const float* k_scale,
@@ -870,11 +907,11 @@ int kivi_packed_decode_attention(const float* q, const uint8_t* k_codes, const f
                                  int32_t num_chunks, int32_t res_capacity, int32_t res_start,
                                  int32_t res_len, float softmax_scale, int32_t num_splits,
                                  void* stream) {
-    return attention_impl(q, 1, 1, nullptr, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
-                                 v_res, res_dtype, out, workspace, workspace_bytes, batch, q_heads,
-                                 kv_heads, head_dim, group_size_k, group_size_v, chunk_capacity,
-                                 num_chunks, res_capacity, res_start, res_len, softmax_scale,
-                                 num_splits, nullptr, nullptr, 0, 0, stream);
+    return attention_impl(q, 1, 1, nullptr, nullptr, 0, k_codes, k_scale, k_zero, v_codes, v_scale,
+                          v_zero, k_res, v_res, res_dtype, out, workspace, workspace_bytes, batch,
+                          q_heads, kv_heads, head_dim, group_size_k, group_size_v, chunk_capacity,
+                          num_chunks, res_capacity, res_start, res_len, softmax_scale, num_splits,
+                          nullptr, nullptr, 0, 0, stream);
 }
 
 int kivi_packed_decode_attention_noalloc(
@@ -898,11 +935,11 @@ int kivi_packed_decode_attention_noalloc(
     void* ws = nullptr;
     const int rc = scratch_for_current_device(&ws);
     if (rc) return rc;
-    return attention_impl(q, 1, 1, nullptr, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
-                                 v_res, res_dtype, out, ws, KIVI_NOALLOC_SCRATCH_BYTES, batch,
-                                 q_heads, kv_heads, head_dim, group_size_k, group_size_v,
-                                 chunk_capacity, num_chunks, res_capacity, res_start, res_len,
-                                 softmax_scale, num_splits, nullptr, nullptr, 0, 0, stream);
+    return attention_impl(q, 1, 1, nullptr, nullptr, 0, k_codes, k_scale, k_zero, v_codes, v_scale,
+                          v_zero, k_res, v_res, res_dtype, out, ws, KIVI_NOALLOC_SCRATCH_BYTES,
+                          batch, q_heads, kv_heads, head_dim, group_size_k, group_size_v,
+                          chunk_capacity, num_chunks, res_capacity, res_start, res_len,
+                          softmax_scale, num_splits, nullptr, nullptr, 0, 0, stream);
 }
 
 int kivi_packed_decode_attention_append(
@@ -932,12 +969,11 @@ int kivi_packed_decode_attention_append(
         return set_error(kErrInvalidArgument,
                          "new-token rows must be %d-byte aligned (strides multiples of 4)",
                          (int)vb);
-    return attention_impl(q, 1, 1, nullptr, k_codes, k_scale, k_zero, v_codes, v_scale, v_zero, k_res,
-                                 v_res, res_dtype, out, workspace, workspace_bytes, batch, q_heads,
-                                 kv_heads, head_dim, group_size_k, group_size_v, chunk_capacity,
-                                 num_chunks, res_capacity, res_start, res_len, softmax_scale,
-                                 num_splits, k_new, v_new, new_batch_stride, new_head_stride,
-                                 stream);
+    return attention_impl(q, 1, 1, nullptr, nullptr, 0, k_codes, k_scale, k_zero, v_codes, v_scale,
+                          v_zero, k_res, v_res, res_dtype, out, workspace, workspace_bytes, batch,
+                          q_heads, kv_heads, head_dim, group_size_k, group_size_v, chunk_capacity,
+                          num_chunks, res_capacity, res_start, res_len, softmax_scale, num_splits,
+                          k_new, v_new, new_batch_stride, new_head_stride, stream);
 }
 
 }  // extern "C"

@@ -73,7 +73,17 @@ struct AttnLaunch {
     // left-padded batch): positions before kv_start[b] -- quantised or in
     // the window -- take no weight.  nullptr: every position is visible.
     const int32_t* kv_start = nullptr;
+    // Optional per-sequence hidden positions (any padding pattern): bit p % 32
+    // of word hidden[b * hidden_stride + p / 32] set hides context position p
+    // of sequence b from every query token.  nullptr: none hidden.
+    const uint32_t* hidden = nullptr;
+    int64_t hidden_stride = 0;
 };
+
+// Bit p % 32 of a hidden-position row (see AttnLaunch::hidden).
+__device__ __forceinline__ bool position_hidden(const uint32_t* row, int p) {
+    return (row[p >> 5] >> (p & 31)) & 1u;
+}
 
 // Launches the matrix-core kernel (kLayoutMfma stores, Hq/Hkv in {1,2,4,8}).
 // With n_splits == 1 it writes `out`; otherwise partials, which the caller

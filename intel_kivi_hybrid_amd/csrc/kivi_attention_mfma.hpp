@@ -413,7 +413,8 @@ __device__ void merge_and_store(unsigned char* smem, const float* rstate, const 
         }
         if (!a.qr.real(h)) continue;    // a padding row
         if (a.n_splits == 1) {          // the only partial of its row: finish here
-            a.out[a.qr.row(b, kvh, h, a.Hq, D) + d] = acc / L;
+            // (a row with no visible position -- every one hidden -- gives 0)
+            a.out[a.qr.row(b, kvh, h, a.Hq, D) + d] = L > 0.f ? acc / L : 0.f;
             continue;
         }
         const int64_t row = (prow0 + h) * a.n_splits + split;
@@ -651,6 +652,10 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     const int64_t bh = (int64_t)b * a.Hkv + kvh;
     // Left padding: context positions before kv_lo take no weight (0: none).
     const int kv_lo = __builtin_amdgcn_readfirstlane(a.kv_start ? a.kv_start[b] : 0);
+    // Any other padding pattern: this sequence's hidden-position bits
+    // (AttnLaunch::hidden), one word per 32 positions; nullptr: none.
+    const uint32_t* hid_row = a.hidden ? a.hidden + b * a.hidden_stride : nullptr;
+    static_assert(G % 32 == 0, "chunks and residual passes hold whole hidden-position words");
 
     unsigned char* wl = smem + wave * S::wave_lds(NG);
     uint16_t* WA = reinterpret_cast<uint16_t*>(wl + S::OFF_WA);
@@ -915,8 +920,8 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     // lane group gq holds heads 2gq, 2gq+1.  Returns whether any running max
     // moved (then O and l are already rescaled and AL[slot] holds the factors).
     // `chunk` is the chunk's index: its tokens before kv_lo (a left-padded
-    // sequence) get score -inf and weight 0, on a wave-uniform branch that
-    // unpadded sequences never take.
+    // sequence) and those its hidden-position bits name get score -inf and
+    // weight 0, on a wave-uniform branch that unpadded sequences never take.
     // kc: the key corrections of the lane's key-side heads (head_corr).
     auto kside = [&](const ChunkRegs<S>& r, auto slot_c, int chunk, const float* kc) -> bool {
         constexpr int slot = decltype(slot_c)::value;
@@ -951,12 +956,28 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                                  kProdScale, kc[e]);
         }
         const int n_masked = kv_lo - chunk * G;       // leading tokens hidden by padding
-        if (__builtin_expect(n_masked > 0, 0)) {
+        // the chunk's hidden-position words (wave-uniform scalar loads)
+        uint32_t hid[G / 32];
+        uint32_t hid_any = 0;
+#pragma unroll
+        for (int i = 0; i < G / 32; ++i) hid[i] = 0;
+        if (__builtin_expect(hid_row != nullptr, 0)) {
+#pragma unroll
+            for (int i = 0; i < G / 32; ++i) {
+                hid[i] = hid_row[chunk * (G / 32) + i];
+                hid_any |= hid[i];
+            }
+        }
+        // token 16*nb + col of the chunk takes no weight
+        auto tok_hidden = [&](int nb) {
+            return 16 * nb + col < n_masked || ((hid[nb / 2] >> (16 * (nb % 2) + col)) & 1u);
+        };
+        const bool masked = n_masked > 0 || hid_any != 0;     // wave-uniform
+        if (__builtin_expect(masked, 0)) {
 #pragma unroll
             for (int e = 0; e < HPL; ++e) {
 #pragma unroll
-                for (int nb = 0; nb < NB; ++nb)
-                    sc[e][nb] = 16 * nb + col < n_masked ? -INFINITY : sc[e][nb];
+                for (int nb = 0; nb < NB; ++nb) sc[e][nb] = tok_hidden(nb) ? -INFINITY : sc[e][nb];
             }
         }
 #pragma unroll
@@ -1016,12 +1037,11 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             for (int nb = 0; nb < NB; ++nb) pv[e][nb] = exp2_fast(sc[e][nb] - m_run[e]);
         }
         // (a hidden token's weight is 0 even while the running max is -inf)
-        if (__builtin_expect(n_masked > 0, 0)) {
+        if (__builtin_expect(masked, 0)) {
 #pragma unroll
             for (int e = 0; e < HPL; ++e) {
 #pragma unroll
-                for (int nb = 0; nb < NB; ++nb)
-                    pv[e][nb] = 16 * nb + col < n_masked ? 0.f : pv[e][nb];
+                for (int nb = 0; nb < NB; ++nb) pv[e][nb] = tok_hidden(nb) ? 0.f : pv[e][nb];
             }
         }
 #pragma unroll
@@ -1177,8 +1197,13 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             else return load4_vec<kSrcF32>(p, i);
         };
 
+        static_assert(kResPass == 16, "a pass's positions lie in one hidden-position word");
         for (int t0 = r0; t0 < r1; t0 += kResPass) {
             const int n = min(kResPass, r1 - t0);
+            // the pass's hidden-position bits: positions n_chunks*G + t0 ..
+            // + 15 lie in one word, from bit t0 % 32 (G is a multiple of 32)
+            const uint32_t wh =
+                hid_row ? hid_row[(a.n_chunks * (G / 32)) + (t0 >> 5)] >> (t0 & 31) : 0u;
             // scores: lane (tk, qq) takes channel quads qq, qq+4, ... of token tk's row
             const int ktok = t0 + min(tk, n - 1);          // index in the window
             int slot = a.res_start + ktok;
@@ -1201,6 +1226,8 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                 vv[j] = load4(vnew ? a.v_new : a.v_res,
                               (vnew ? new_row : ((int64_t)bh * a.Rcap + vs) * D) + 4 * c4);
             }
+            // token tk of the pass is real, not before kv_lo and not hidden
+            const bool tseen = tk < n && t0 + tk >= r_lo && !((wh >> tk) & 1u);
             float sres[HG];
 #pragma unroll
             for (int h = 0; h < HG; ++h) {
@@ -1217,15 +1244,14 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                 acc += dpp<0xB1>(acc);        // quad_perm [1,0,3,2]
                 acc += dpp<0x4E>(acc);        // quad_perm [2,3,0,1]
                 // row h sees the window's first qr.visible(h) tokens
-                sres[h] = tk < n && t0 + tk >= r_lo && t0 + tk < a.qr.visible(h, a.res_len)
-                              ? acc : -INFINITY;
+                sres[h] = tseen && t0 + tk < a.qr.visible(h, a.res_len) ? acc : -INFINITY;
             }
 #pragma unroll
             for (int h = 0; h < HG; ++h) {
                 const float mnew = fmaxf(mr[h], wave_max(sres[h]));
                 const float alpha = mr[h] == -INFINITY ? 0.f : exp2_fast(mr[h] - mnew);
                 mr[h] = mnew;
-                const float p = tk < n && t0 + tk >= r_lo && t0 + tk < a.qr.visible(h, a.res_len)
+                const float p = tseen && t0 + tk < a.qr.visible(h, a.res_len)
                                     ? exp2_fast(sres[h] - mnew) : 0.f;
                 lr[h] = lr[h] * alpha + 0.25f * wave_sum(p);    // each token sits in 4 lanes
                 orr[h][0] *= alpha;

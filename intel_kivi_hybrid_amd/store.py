@@ -538,7 +538,8 @@ class PackedKVStore:
     def attention(self, q: torch.Tensor, softmax_scale: Optional[float] = None,
                   out: Optional[torch.Tensor] = None, num_splits: int = 0,
                   workspace: Optional[torch.Tensor] = None, causal: bool = True,
-                  kv_start=None) -> torch.Tensor:
+                  kv_start=None, key_mask: Optional[torch.Tensor] = None,
+                  hidden: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Fused attention over [packed history ; residual].
 
         ``q [B, Hq, D]`` (or ``[B, Hq, 1, D]``): one decode token per
@@ -546,13 +547,16 @@ class PackedKVStore:
         L > 1: L query tokens per sequence (see ``_C.packed_attention``;
         ``causal`` by default: they are the window's last L tokens); returns
         ``[B, L, Hq, D]`` fp32.  ``kv_start``: per-sequence first visible
-        position of a left-padded batch (``_C.packed_attention``)."""
+        position of a left-padded batch; ``key_mask`` ``[B, T]`` (nonzero =
+        attended) or its packed ``hidden`` words: any other padding pattern
+        (``_C.packed_attention``)."""
         from . import _C
-        if kv_start is not None and (q.dim() == 3 or q.shape[2] == 1):
+        masked = kv_start is not None or key_mask is not None or hidden is not None
+        if masked and (q.dim() == 3 or q.shape[2] == 1):
             q4 = q if q.dim() == 4 else q.unsqueeze(2)
             o = _C.packed_attention(q4, self, causal=True, softmax_scale=softmax_scale,
                                     num_splits=num_splits, workspace=workspace,
-                                    kv_start=kv_start)[:, 0]
+                                    kv_start=kv_start, key_mask=key_mask, hidden=hidden)[:, 0]
             if out is not None:
                 out.copy_(o.view_as(out))
                 return out
@@ -560,6 +564,6 @@ class PackedKVStore:
         if q.dim() == 4 and q.shape[2] > 1:
             return _C.packed_attention(q, self, causal=causal, softmax_scale=softmax_scale,
                                        out=out, num_splits=num_splits, workspace=workspace,
-                                       kv_start=kv_start)
+                                       kv_start=kv_start, key_mask=key_mask, hidden=hidden)
         return _C.packed_decode_attention(q, self, softmax_scale=softmax_scale, out=out,
                                           num_splits=num_splits, workspace=workspace)

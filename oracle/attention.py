@@ -13,13 +13,30 @@ from __future__ import annotations
 import numpy as np
 
 
-def decode_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None, kv_start=None):
+def _attend(qh, K, V, scale, seen):
+    """softmax(qh K^T * scale) V over the positions ``seen`` (bool [T]);
+    zeros when none is seen."""
+    if not seen.any():
+        return np.zeros((qh.shape[0], V.shape[1]))
+    K, V = K[seen], V[seen]
+    s = (qh @ K.T) * scale                       # [g, n]
+    s -= s.max(axis=1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=1, keepdims=True)
+    return p @ V
+
+
+def decode_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None, kv_start=None,
+                     visible=None):
     """q: [B, Hq, D]; k_hist/v_hist: [B, Hkv, Tq, D] dequantised history;
     k_res/v_res: [B, Hkv, Tr, D] fp32 residual.  Returns o [B, Hq, D] float64.
 
     ``kv_start`` (B ints, optional): sequence b attends to context positions
     kv_start[b] .. Tq+Tr-1 only -- a left-padded batch, whose HF attention
-    mask hides each sequence's leading pad positions.
+    mask hides each sequence's leading pad positions.  ``visible`` (bool
+    [B, Tq+Tr], optional): any key-padding pattern, position t of sequence b
+    attended only where visible[b, t] (HF's 2-D attention mask); a sequence
+    that sees no position gets zeros.
 
     Works one (batch, kv-head) at a time so that long contexts fit in memory.
     """
@@ -43,17 +60,16 @@ def decode_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None, kv_sta
             K = np.concatenate(parts_k, axis=0)          # [T, D]
             V = np.concatenate(parts_v, axis=0)
             s0 = 0 if kv_start is None else int(kv_start[b])
-            K, V = K[s0:], V[s0:]
+            seen = np.arange(K.shape[0]) >= s0
+            if visible is not None:
+                seen &= np.asarray(visible[b], dtype=bool)
             qh = q[b, kh * g:(kh + 1) * g]               # [g, D]
-            s = (qh @ K.T) * scale                       # [g, T]
-            s -= s.max(axis=1, keepdims=True)
-            p = np.exp(s)
-            p /= p.sum(axis=1, keepdims=True)
-            out[b, kh * g:(kh + 1) * g] = p @ V
+            out[b, kh * g:(kh + 1) * g] = _attend(qh, K, V, scale, seen)
     return out
 
 
-def prefix_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None, kv_start=None):
+def prefix_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None, kv_start=None,
+                     visible=None):
     """Causal attention of the window's last ``q_len`` tokens.
 
     q: [B, q_len, Hq, D] -- the queries of the ``q_len`` newest tokens, which
@@ -64,8 +80,9 @@ def prefix_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None, kv_sta
     the HF model's causal mask over [cache ; new tokens] in a forward of
     ``q_len`` tokens on a non-empty cache (the reference's own attention check
     uses q_len=3, tests/integration/test_attention_fix.py:19-36,91-93).
-    GQA and ``kv_start`` as in decode_attention.  Returns o [B, q_len, Hq, D]
-    float64.
+    GQA, ``kv_start`` and ``visible`` (hidden positions on top of the causal
+    rule; a query row that sees no position gets zeros) as in
+    decode_attention.  Returns o [B, q_len, Hq, D] float64.
     """
     q = np.asarray(q, dtype=np.float64)
     B, L, Hq, D = q.shape
@@ -89,12 +106,12 @@ def prefix_attention(q, k_hist, v_hist, k_res, v_res, softmax_scale=None, kv_sta
             V = np.concatenate(parts_v, axis=0)
             T = K.shape[0]
             s0 = 0 if kv_start is None else int(kv_start[b])
+            t = np.arange(T)
             for i in range(L):
                 n = T - L + i + 1                        # visible tokens of query i
+                seen = (t >= s0) & (t < n)
+                if visible is not None:
+                    seen &= np.asarray(visible[b], dtype=bool)
                 qh = q[b, i, kh * g:(kh + 1) * g]        # [g, D]
-                s = (qh @ K[s0:n].T) * scale             # [g, n - s0]
-                s -= s.max(axis=1, keepdims=True)
-                p = np.exp(s)
-                p /= p.sum(axis=1, keepdims=True)
-                out[b, i, kh * g:(kh + 1) * g] = p @ V[s0:n]
+                out[b, i, kh * g:(kh + 1) * g] = _attend(qh, K, V, scale, seen)
     return out

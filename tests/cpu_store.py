@@ -4,6 +4,7 @@ attended) can be checked without a GPU.  Test infrastructure only: it holds
 the residual window and the round-tripped history as CPU tensors, quantises
 with the C oracle codec and attends with the float64 oracle attention."""
 
+import numpy as np
 import torch
 
 from oracle import attention as oracle_attention
@@ -74,18 +75,25 @@ class CpuPackedStore:
                 flushes += 1
         return flushes
 
-    def attention(self, q, softmax_scale=None, causal=True, kv_start=None):
+    def attention(self, q, softmax_scale=None, causal=True, kv_start=None, hidden=None):
         starts = None if kv_start is None else [int(x) for x in kv_start]
+        vis = None
+        if hidden is not None:
+            # hidden-position words -> visibility: bit p % 32 of word p // 32
+            T = self.n_chunks * self.G + self.res_len
+            w = hidden.cpu().numpy().astype(np.uint32)
+            p = np.arange(T)
+            vis = ((w[:, p // 32] >> (p % 32).astype(np.uint32)) & 1) == 0
         if q.dim() == 4 and q.shape[2] > 1:
             # [B, Hq, L, D] -> [B, L, Hq, D]: the window's newest L tokens
             assert causal and q.shape[2] <= self.res_len
             o = oracle_attention.prefix_attention(q.transpose(1, 2).numpy(), self.hist_k.numpy(),
                                                   self.hist_v.numpy(), self.res_k.numpy(),
-                                                  self.res_v.numpy(), softmax_scale, starts)
+                                                  self.res_v.numpy(), softmax_scale, starts, vis)
             return torch.from_numpy(o).float()
         o = oracle_attention.decode_attention(q.numpy(), self.hist_k.numpy(),
                                               self.hist_v.numpy(), self.res_k.numpy(),
-                                              self.res_v.numpy(), softmax_scale, starts)
+                                              self.res_v.numpy(), softmax_scale, starts, vis)
         return torch.from_numpy(o).float()
 
     def grow_residual(self, capacity):

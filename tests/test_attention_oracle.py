@@ -15,6 +15,10 @@ oracle is checked here against:
     source (wrong scale, wrong head map, a dropped history or residual, V
     swapped for K, normalisation over the wrong axis) must fail the library
     comparison, so the comparison above pins those parts.
+The padding arguments are pinned the same way: ``kv_start`` and ``visible``
+(any key-padding pattern) against SDPA with the boolean mask HF builds,
+special cases (all visible, a leading run equal to kv_start, one visible
+position, none) and their own mutants.
 It also pins the vectorised history builder of the GPU tests against the
 per-chunk oracle quantise + dequantise.
 """
@@ -274,9 +278,11 @@ def test_padded_oracle_matches_sdpa_float64(shape):
 
 
 PAD_MUTANTS = {
-    "decode start ignored": ("K, V = K[s0:], V[s0:]", "K, V = K, V"),
-    "decode start off by one": ("K, V = K[s0:], V[s0:]", "K, V = K[s0 + 1:], V[s0 + 1:]"),
-    "prefix start ignored": ("K[s0:n].T", "K[:n].T"),
+    "decode start ignored": ("seen = np.arange(K.shape[0]) >= s0",
+                             "seen = np.arange(K.shape[0]) >= 0"),
+    "decode start off by one": ("seen = np.arange(K.shape[0]) >= s0",
+                                "seen = np.arange(K.shape[0]) > s0"),
+    "prefix start ignored": ("seen = (t >= s0) & (t < n)", "seen = t < n"),
 }
 
 
@@ -294,5 +300,126 @@ def test_padded_planted_mistakes_fail(name):
         try:
             worst = max(worst, _padded_err(mutant, shape, seed=len(shape)))
         except (ValueError, IndexError):
+            worst = np.inf
+    assert worst > 1e-6, f"mutant '{name}' passes (max err {worst:.2e})"
+
+
+# ---- any key-padding pattern: position t of sequence b hidden unless visible[b, t]
+VIS_SHAPES = [
+    # B, L, Hq, Hkv, D, Tq, Tr
+    (3, 1, 8, 2, 32, 64, 17),      # decode, GQA 4
+    (2, 3, 4, 4, 16, 32, 9),       # three causal query tokens, MHA
+    (2, 4, 6, 3, 16, 0, 12),       # no history
+]
+
+
+def _visibility(B, T, seed):
+    """Holes, right padding and a run hidden across the history/window edge;
+    the last position (the newest query token) always visible."""
+    rng = np.random.default_rng(seed)
+    vis = rng.random((B, T)) > 0.3
+    vis[0, T // 2:T - 1] = False                   # right padding before the new token
+    vis[-1, :T // 3] = False                        # a left-padding run
+    vis[:, T - 1] = True
+    return vis
+
+
+def _sdpa_visible(q, kh, vh, kr, vr, vis):
+    B, L, Hq, D = q.shape
+    Hkv = kr.shape[1]
+    K = torch.cat([kh, kr], dim=2).repeat_interleave(Hq // Hkv, dim=1)
+    V = torch.cat([vh, vr], dim=2).repeat_interleave(Hq // Hkv, dim=1)
+    T = K.shape[2]
+    t = torch.arange(T)
+    causal = t[None, :] <= (T - L + torch.arange(L))[:, None]                     # [L, T]
+    mask = causal[None, None] & torch.from_numpy(vis)[:, None, None]              # [B, 1, L, T]
+    o = torch.nn.functional.scaled_dot_product_attention(q.transpose(1, 2), K, V,
+                                                         attn_mask=mask)
+    return o.transpose(1, 2), mask[:, 0].any(-1)                                  # [B, L] rows seen
+
+
+def _visible_err(mod, shape, seed):
+    B, L, Hq, Hkv, D, Tq, Tr = shape
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, L, Hq, D, generator=g, dtype=torch.float64)
+    kh, vh = (torch.randn(B, Hkv, Tq, D, generator=g, dtype=torch.float64) for _ in range(2))
+    kr, vr = (torch.randn(B, Hkv, Tr, D, generator=g, dtype=torch.float64) for _ in range(2))
+    vis = _visibility(B, Tq + Tr, seed)
+    ref, seen = _sdpa_visible(q, kh, vh, kr, vr, vis)
+    args = (kh.numpy(), vh.numpy(), kr.numpy(), vr.numpy())
+    if L == 1:
+        out = mod.decode_attention(q[:, 0].numpy(), *args, visible=vis)[:, None]
+    else:
+        out = mod.prefix_attention(q.numpy(), *args, visible=vis)
+    rows = seen.numpy()
+    assert rows.any()
+    return float(np.abs(out[rows] - ref.numpy()[rows]).max())
+
+
+@pytest.mark.parametrize("shape", VIS_SHAPES)
+def test_visible_oracle_matches_sdpa_float64(shape):
+    """``visible`` against SDPA with the boolean mask (visible positions,
+    causal among the new tokens), on the rows that see a position."""
+    assert _visible_err(oracle_attention, shape, seed=len(shape) + shape[1]) < 1e-12
+
+
+def test_visible_special_cases():
+    """All visible is the unmasked result, a leading hidden run is kv_start,
+    one visible position gives that position's V row, none gives zeros."""
+    B, L, Hq, Hkv, D, Tq, Tr = 2, 3, 8, 2, 16, 32, 10
+    T = Tq + Tr
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal((B, L, Hq, D))
+    kh, vh = rng.standard_normal((2, B, Hkv, Tq, D))
+    kr, vr = rng.standard_normal((2, B, Hkv, Tr, D))
+    for fn, qq in ((decode_attention, q[:, -1]), (oracle_attention.prefix_attention, q)):
+        full = fn(qq, kh, vh, kr, vr)
+        assert np.array_equal(fn(qq, kh, vh, kr, vr, visible=np.ones((B, T), bool)), full)
+        starts = (5, 33)
+        lead = np.arange(T)[None, :] >= np.array(starts)[:, None]
+        assert np.array_equal(fn(qq, kh, vh, kr, vr, visible=lead),
+                              fn(qq, kh, vh, kr, vr, kv_start=starts))
+    one = np.zeros((B, T), bool)
+    one[0, 7] = True                     # a history position
+    one[1, Tq + 2] = True                # a window position
+    o = decode_attention(q[:, -1], kh, vh, kr, vr, visible=one)
+    assert np.allclose(o[0], np.repeat(vh[0, :, 7], Hq // Hkv, axis=0), rtol=0, atol=1e-15)
+    assert np.allclose(o[1], np.repeat(vr[1, :, 2], Hq // Hkv, axis=0), rtol=0, atol=1e-15)
+    none = np.zeros((B, T), bool)
+    assert not decode_attention(q[:, -1], kh, vh, kr, vr, visible=none).any()
+    # the first query token sees positions up to T - L only: hiding exactly
+    # those leaves its row empty (zeros) and the later rows not
+    early = np.ones((B, T), bool)
+    early[:, :T - L + 1] = False
+    o = oracle_attention.prefix_attention(q, kh, vh, kr, vr, visible=early)
+    assert not o[:, 0].any() and o[:, 1:].all()
+
+
+VIS_MUTANTS = {
+    "decode visible ignored": ("                seen &= np.asarray(visible[b], dtype=bool)\n"
+                               "            qh", "                pass\n            qh"),
+    "prefix visible ignored": ("                    seen &= np.asarray(visible[b], dtype=bool)",
+                               "                    pass"),
+    "visible shifted by one": ("np.asarray(visible[b], dtype=bool)",
+                               "np.roll(np.asarray(visible[b], dtype=bool), 1)"),
+    "visible inverted": ("seen &= np.asarray(visible[b], dtype=bool)",
+                         "seen &= ~np.asarray(visible[b], dtype=bool)"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(VIS_MUTANTS))
+def test_visible_planted_mistakes_fail(name):
+    old, new = VIS_MUTANTS[name]
+    path = os.path.abspath(oracle_attention.__file__)
+    with open(path) as f:
+        src = f.read()
+    assert old in src, f"mutation site for '{name}' not found"
+    mutant = types.ModuleType("oracle_visible_mutant")
+    exec(compile(src.replace(old, new), path, "exec"), mutant.__dict__)
+    worst = 0.0
+    for shape in VIS_SHAPES:
+        try:
+            worst = max(worst, _visible_err(mutant, shape, seed=len(shape) + shape[1]))
+        except (ValueError, IndexError, AssertionError):
             worst = np.inf
     assert worst > 1e-6, f"mutant '{name}' passes (max err {worst:.2e})"

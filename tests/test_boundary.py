@@ -44,7 +44,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_error_string():
     from intel_kivi_hybrid_amd import _native
     lib = _native.load()
-    assert lib.kivi_abi_version() == 5
+    assert lib.kivi_abi_version() == 6
     # invalid arguments are rejected on the host, before any launch
     rc = lib.kivi_quantize_keys_per_channel(None, None, None, None, 4, 32, None)
     assert rc == 1 and "null" in _native.last_error()

@@ -459,3 +459,56 @@ def test_hf_generate_left_padded_batch(hip_device):
     n, tot = _match(ours.reshape(-1).tolist(), want.reshape(-1).tolist())
     print(f"[packed-padded-generate] token match {n}/{tot}", flush=True)
     assert torch.equal(ours, want)
+
+
+@pytest.mark.parametrize("kind", ["right", "holes"])
+def test_padded_batch_any_pattern_follows_reference_flow(hip_device, kind):
+    """A right-padded batch (pad positions between each prompt and its new
+    tokens) or one with holes inside the prompts, decoded with one-token and
+    multi-token steps: the packed attention applies HF's mask through
+    hidden-position bits, and the logits agree with the reference flow's (HF
+    SDPA with the same mask over get_full_cache()).  Model on the CPU in both
+    arms."""
+    from transformers import GPT2Config, GPT2LMHeadModel
+    torch.manual_seed(41)
+    model = GPT2LMHeadModel(GPT2Config(n_layer=3, n_head=4, n_embd=256)).eval()
+    G, R = 32, 64
+    ours = pc.KiviPackedCache.from_model(model, device="cuda:0", group_size=G,
+                                         residual_length=R)
+    ref = _OracleShim.from_model(model, group_size=G, residual_length=R)
+    gen = torch.Generator().manual_seed(42)
+    lengths = [50, 37, 12]
+    T = max(lengths)
+    ids = torch.randint(1, model.config.vocab_size, (3, T), generator=gen)
+    mask = torch.zeros(3, T, dtype=torch.long)
+    for b, n in enumerate(lengths):
+        mask[b, :n] = 1
+        if kind == "holes":
+            mask[b, :n - 1] = (torch.rand(n - 1, generator=gen) > 0.3).long()
+    ids = ids * mask
+
+    def kw(n):
+        return dict(attention_mask=mask, position_ids=(mask.cumsum(-1) - 1).clamp(min=0)[:, -n:],
+                    use_cache=True)
+    with torch.no_grad(), pc.packed_attention(model):
+        model(ids, past_key_values=ours, **kw(T))
+    with torch.no_grad():
+        ref.add_tokens(model(ids, **kw(T)).past_key_values)
+    worst = 0.0
+    for n in [1, 1, 3, 1, 9, 1, 1, 30, 1, 2] + [1] * 20:
+        new = torch.randint(1, model.config.vocab_size, (3, n), generator=gen)
+        mask = torch.cat([mask, torch.ones(3, n, dtype=torch.long)], dim=1)
+        with torch.no_grad(), pc.packed_attention(model):
+            lo = model(new, past_key_values=ours, **kw(n)).logits
+        with torch.no_grad():
+            out = model(new, past_key_values=ref.get_full_cache(), **kw(n))
+        ref.add_tokens(out.past_key_values)
+        err = ((lo - out.logits).abs().max() / out.logits.abs().max()).item()
+        worst = max(worst, err)
+        assert err <= 1e-3, (n, err)
+        for lay in ours.layers:
+            lay.settle()
+    plan = ours._mask_memo[1]
+    assert plan[0] is None and plan[1] is not None      # the hidden-bits path ran
+    print(f"[packed-{kind}] worst logits rel err {worst:.2e}", flush=True)
+    assert ours.total_flushes == ref.total_flushes > 0

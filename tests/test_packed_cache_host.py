@@ -167,16 +167,82 @@ def test_unsupported_inputs_raise(cpu_store):
     model = _gpt2(2, 2, 64)
     cache = pc.KiviPackedCache.from_model(model, group_size=32, residual_length=32)
     with torch.no_grad(), pc.packed_attention(model):
-        model(torch.tensor([[1, 2, 3]]), past_key_values=cache, use_cache=True)
-        with pytest.raises(NotImplementedError, match="left-padded"):
-            model(torch.tensor([[4, 5]]), past_key_values=cache, use_cache=True,
-                  attention_mask=torch.tensor([[1, 0, 1, 1, 1]]))     # a hole, not padding
-    with torch.no_grad(), pc.packed_attention(model):
         with pytest.raises(RuntimeError, match="KiviPackedCache"):
             model(torch.tensor([[1, 2, 3]]), use_cache=False)
     with pytest.raises(ValueError, match="head_dim"):
         bad = pc.KiviPackedCache(2, 64, 2, group_size=32, residual_length=32)
         bad.update(torch.zeros(1, 2, 3, 48), torch.zeros(1, 2, 3, 48), 0)
+
+
+def test_hole_mask_follows_reference_flow(cpu_store):
+    """A mask with holes (positions hidden inside the context) reaches the
+    store as hidden-position words, and the logits are the reference flow's
+    (HF SDPA with the same mask over get_full_cache())."""
+    model = _gpt2(2, 2, 64, seed=3)
+    G, R = 32, 32
+    cache = pc.KiviPackedCache.from_model(model, group_size=G, residual_length=R)
+    ref = _OracleShim.from_model(model, group_size=G, residual_length=R)
+    gen = torch.Generator().manual_seed(4)
+    ids = torch.randint(1, model.config.vocab_size, (2, 40), generator=gen)
+    mask = torch.ones(2, 40, dtype=torch.long)
+    mask[0, 3:9] = 0
+    mask[1, 20:39] = 0                      # right padding before the last prompt token
+    with torch.no_grad(), pc.packed_attention(model):
+        model(ids, past_key_values=cache, use_cache=True, attention_mask=mask)
+    with torch.no_grad():
+        ref.add_tokens(model(ids, use_cache=True, attention_mask=mask).past_key_values)
+    for n in (1, 1, 3, 1, 1):
+        new = torch.randint(1, model.config.vocab_size, (2, n), generator=gen)
+        mask = torch.cat([mask, torch.ones(2, n, dtype=torch.long)], dim=1)
+        with torch.no_grad(), pc.packed_attention(model):
+            lo = model(new, past_key_values=cache, use_cache=True, attention_mask=mask).logits
+        with torch.no_grad():
+            out = model(new, past_key_values=ref.get_full_cache(), use_cache=True,
+                        attention_mask=mask)
+        ref.add_tokens(out.past_key_values)
+        err = ((lo - out.logits).abs().max() / out.logits.abs().max()).item()
+        assert err <= 1e-4, (n, err)
+        for lay in cache.layers:
+            lay.settle()
+    assert cache._mask_memo[1][1] is not None       # hidden words, not kv_start
+
+
+def _hf_mask(attend):
+    return attend[:, None]                            # [B, 1, q_len, kv_len]
+
+
+def test_mask_plan_paths():
+    """HF masks as the packed kernels take them: a leading hidden run is
+    kv_start, any other key-padding pattern hidden words (bit p % 32 of word
+    p // 32), a 0 / lowest-value float mask the same as the boolean one; an
+    additive bias or a per-query pattern other than causal is refused."""
+    class Owner:
+        _mask_memo = None
+    B, L, T = 3, 2, 70
+    t = torch.arange(T)
+    causal = t[None, :] <= (T - L + torch.arange(L))[:, None]
+    lead = t[None, :] >= torch.tensor([0, 5, 40])[:, None]
+    kv_start, hidden = pc._mask_plan(Owner(), _hf_mask(lead[:, None] & causal), L, T, "cpu")
+    assert hidden is None and kv_start.tolist() == [0, 5, 40]
+    vis = lead.clone()
+    vis[0, 33] = False                                # a hole in the second word
+    vis[2, 64:68] = False                             # right padding before the new tokens
+    kv_start, hidden = pc._mask_plan(Owner(), _hf_mask(vis[:, None] & causal), L, T, "cpu")
+    assert kv_start is None and hidden.dtype == torch.int32 and hidden.shape == (B, 3)
+    w = hidden.numpy().astype("uint32")
+    for b in range(B):
+        for p in range(T):
+            assert bool((w[b, p // 32] >> (p % 32)) & 1) == (not bool(vis[b, p])), (b, p)
+    low = torch.finfo(torch.float32).min
+    fm = torch.where(vis[:, None] & causal, 0.0, low)[:, None]
+    kv2, hidden2 = pc._mask_plan(Owner(), fm, L, T, "cpu")
+    assert kv2 is None and torch.equal(hidden2, hidden)
+    with pytest.raises(NotImplementedError, match="padded batch"):
+        pc._mask_plan(Owner(), torch.where(vis[:, None] & causal, 0.5, low)[:, None], L, T, "cpu")
+    odd = (vis[:, None] & causal).clone()
+    odd[1, 0, 10] = False                             # the first query hides one more position
+    with pytest.raises(NotImplementedError, match="padded batch"):
+        pc._mask_plan(Owner(), _hf_mask(odd), L, T, "cpu")
 
 
 def test_hf_generate_uses_the_cache(cpu_store):
