@@ -335,15 +335,19 @@ class KiviCache:
         return self._stores[layer] if self._fed[layer] else None
 
     def attention(self, layer: int, q: torch.Tensor, softmax_scale: Optional[float] = None,
-                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                  out: Optional[torch.Tensor] = None, kv_start=None,
+                  key_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Fused decode attention of one query token per sequence,
         ``q [B, Hq, D]``, over this layer's packed history and residual
-        window, straight from the 2-bit store (no dequantised copy)."""
+        window, straight from the 2-bit store (no dequantised copy).
+        ``kv_start`` / ``key_mask`` (``[B, T]`` over the layer's context,
+        nonzero = attended): a padded batch's hidden positions, as
+        ``PackedKVStore.attention`` takes them."""
         st = self.store(layer)
         if st is None:
             raise RuntimeError(f"layer {layer} holds no tokens yet")
         return st.attention(q.to(self.device, torch.float32), softmax_scale=softmax_scale,
-                            out=out)
+                            out=out, kv_start=kv_start, key_mask=key_mask)
 
     def __repr__(self):
         return (f"KiviCache(layers={self.num_layers}, head_dim={self.head_dim}, "

@@ -166,6 +166,15 @@ def test_fused_attention_through_cache(KiviCache, Hq):
         err = rel_err(out.cpu().numpy(), ref)
         print(f"[cache] fused attention layer {layer} Hq={Hq} rel_err={err:.2e}", flush=True)
         assert err <= 1e-3
+        # a padded batch: holes and right padding over the served context
+        T = k.shape[2]
+        vis = torch.rand(B, T, generator=torch.Generator().manual_seed(layer)) > 0.25
+        vis[1, 60:T - 1] = False
+        vis[:, T - 1] = True
+        out = ours.attention(layer, q.cuda(), key_mask=vis)
+        ref = decode_attention(q.numpy(), k.cpu().numpy(), v.cpu().numpy(), None, None,
+                               visible=vis.numpy())
+        assert rel_err(out.cpu().numpy(), ref) <= 1e-3
 
 
 class _FakeTokenizer:
