@@ -138,7 +138,10 @@ def time_calls(fn, iters, blocks=5):
     torch's current stream (the stream every launch here goes to) bracket
     blocks of back-to-back calls: the host issues a call in a fraction of its
     GPU time, so the queue never drains, and a block's time per call is the
-    kernels' duration plus the launch gaps, without host latency."""
+    kernels' duration plus the launch gaps, without host latency.  An
+    untimed call ahead of each block keeps the GPU busy while the block's
+    first call is issued (otherwise the start event would also time the
+    host's issue of that call)."""
     import torch
     settle_clocks(fn)
     per_block = max(1, iters // blocks)
@@ -146,6 +149,7 @@ def time_calls(fn, iters, blocks=5):
     for _ in range(blocks):
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
+        fn()
         e0.record()
         for _ in range(per_block):
             fn()
@@ -246,7 +250,7 @@ def decode_loop(st, q_all, k_new, v_new, steps, warmup, R):
             "gbs": total_bytes / (ms * 1e-3) / 1e9, "ms_per_step": ms / steps}
 
 
-def codec_bench(kt, v, G, iters=10):
+def codec_bench(kt, v, G, iters=50):
     """Config 2 through the ``_C`` ops on device-resident inputs: keys
     ``kt [B,H,D,Seq]`` quantised per channel along tokens, values
     ``v [B,H,Seq,D]`` per token along channels, both in groups of G.  Times
