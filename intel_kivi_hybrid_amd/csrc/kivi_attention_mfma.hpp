@@ -391,7 +391,7 @@ __device__ void combine_residual(unsigned char* smem, float* rstate) {
 // Combines the 4 chunk states (merge slots) and the combined residual state
 // of the workgroup and writes one partial (o, m, l) row per query head, or the
 // normalised output when the workgroup is the row's only split.
-template <int HG, int D>
+template <int HG, int D, bool MASK>
 __device__ void merge_and_store(unsigned char* smem, const float* rstate, const AttnLaunch& a,
                                 int split, int kvh, int b) {
     __syncthreads();
@@ -413,8 +413,10 @@ __device__ void merge_and_store(unsigned char* smem, const float* rstate, const 
         }
         if (!a.qr.real(h)) continue;    // a padding row
         if (a.n_splits == 1) {          // the only partial of its row: finish here
-            // (a row with no visible position -- every one hidden -- gives 0)
-            a.out[a.qr.row(b, kvh, h, a.Hq, D) + d] = L > 0.f ? acc / L : 0.f;
+            if constexpr (MASK)         // a row with no visible position gives 0
+                a.out[a.qr.row(b, kvh, h, a.Hq, D) + d] = L > 0.f ? acc / L : 0.f;
+            else
+                a.out[a.qr.row(b, kvh, h, a.Hq, D) + d] = acc / L;
             continue;
         }
         const int64_t row = (prow0 + h) * a.n_splits + split;
@@ -626,7 +628,7 @@ __device__ __forceinline__ void stage_meta(const ChunkRegs<S>& r, float* MT, int
 // time, so the value operand of every n-block is known statically and its
 // LDS reads can be issued ahead; NGC == 0 reads it from the launch.
 // R16: the residual ring holds bf16 or fp16 (a.res_dt) instead of fp32.
-template <class S, int NGC, bool R16>
+template <class S, int NGC, bool R16, bool MASK>
 __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, int kvh, int b) {
     constexpr int HG = S::HG, D = S::D, G = S::G, NSUB = S::NSUB, NB = G / 16;
     // Value operand items: (head, value group, TPI tokens).  8 tokens per
@@ -652,9 +654,9 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     const int64_t bh = (int64_t)b * a.Hkv + kvh;
     // Left padding: context positions before kv_lo take no weight (0: none).
     const int kv_lo = __builtin_amdgcn_readfirstlane(a.kv_start ? a.kv_start[b] : 0);
-    // Any other padding pattern: this sequence's hidden-position bits
-    // (AttnLaunch::hidden), one word per 32 positions; nullptr: none.
-    const uint32_t* hid_row = a.hidden ? a.hidden + b * a.hidden_stride : nullptr;
+    // Any other padding pattern (MASK instances only): this sequence's
+    // hidden-position bits (AttnLaunch::hidden), one word per 32 positions.
+    const uint32_t* hid_row = MASK ? a.hidden + b * a.hidden_stride : nullptr;
     static_assert(G % 32 == 0, "chunks and residual passes hold whole hidden-position words");
 
     unsigned char* wl = smem + wave * S::wave_lds(NG);
@@ -766,6 +768,19 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
     float2 smul[S::NMETA];
 #pragma unroll
     for (int i = 0; i < S::NMETA; ++i) smul[i] = meta_mul<S, PAIRED>(lane, i, NG);
+    // Hidden-position words of the wave's chunks (launches with hidden
+    // positions only): lane l holds those of the wave's chunk l, so a step
+    // reads its words with readlane.  A scalar load per step made each step
+    // wait for it at its next LDS wait (config 4: 103 -> 118 us); it remains
+    // only for a wave's chunks past its 64th.
+    uint32_t hid_lane[G / 32];
+    if constexpr (MASK) {
+        const int c = chunk_of(lane);
+#pragma unroll
+        for (int i = 0; i < G / 32; ++i)
+            hid_lane[i] = c >= 0 ? hid_row[(int64_t)c * (G / 32) + i] : 0u;
+    }
+    int hid_j = 0;       // the wave's chunk index of the next kside call
     // (the launch gives every workgroup at least one chunk, or the store room
     // for chunk 0, so c_last is a readable chunk and these loads need no
     // branch: a branch here would make the compiler wait for them before the
@@ -956,23 +971,28 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                                  kProdScale, kc[e]);
         }
         const int n_masked = kv_lo - chunk * G;       // leading tokens hidden by padding
-        // the chunk's hidden-position words (wave-uniform scalar loads)
+        // MASK: the chunk's hidden-position words (wave-uniform; kside runs
+        // once per chunk of the wave, in order)
         uint32_t hid[G / 32];
-        uint32_t hid_any = 0;
-#pragma unroll
-        for (int i = 0; i < G / 32; ++i) hid[i] = 0;
-        if (__builtin_expect(hid_row != nullptr, 0)) {
+        bool masked = n_masked > 0;                           // wave-uniform
+        if constexpr (MASK) {
+            uint32_t hid_any = 0;
 #pragma unroll
             for (int i = 0; i < G / 32; ++i) {
-                hid[i] = hid_row[chunk * (G / 32) + i];
+                hid[i] = hid_j < 64 ? __builtin_amdgcn_readlane(hid_lane[i], hid_j)
+                                    : hid_row[chunk * (G / 32) + i];
                 hid_any |= hid[i];
             }
+            ++hid_j;
+            masked = masked || hid_any != 0;
         }
         // token 16*nb + col of the chunk takes no weight
         auto tok_hidden = [&](int nb) {
-            return 16 * nb + col < n_masked || ((hid[nb / 2] >> (16 * (nb % 2) + col)) & 1u);
+            if constexpr (MASK)
+                return 16 * nb + col < n_masked || ((hid[nb / 2] >> (16 * (nb % 2) + col)) & 1u);
+            else
+                return 16 * nb + col < n_masked;
         };
-        const bool masked = n_masked > 0 || hid_any != 0;     // wave-uniform
         if (__builtin_expect(masked, 0)) {
 #pragma unroll
             for (int e = 0; e < HPL; ++e) {
@@ -1200,10 +1220,11 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
         static_assert(kResPass == 16, "a pass's positions lie in one hidden-position word");
         for (int t0 = r0; t0 < r1; t0 += kResPass) {
             const int n = min(kResPass, r1 - t0);
-            // the pass's hidden-position bits: positions n_chunks*G + t0 ..
-            // + 15 lie in one word, from bit t0 % 32 (G is a multiple of 32)
-            const uint32_t wh =
-                hid_row ? hid_row[(a.n_chunks * (G / 32)) + (t0 >> 5)] >> (t0 & 31) : 0u;
+            // MASK: the pass's hidden-position bits: positions n_chunks*G +
+            // t0 .. + 15 lie in one word, from bit t0 % 32 (G is a multiple
+            // of 32)
+            uint32_t wh = 0u;
+            if constexpr (MASK) wh = hid_row[(a.n_chunks * (G / 32)) + (t0 >> 5)] >> (t0 & 31);
             // scores: lane (tk, qq) takes channel quads qq, qq+4, ... of token tk's row
             const int ktok = t0 + min(tk, n - 1);          // index in the window
             int slot = a.res_start + ktok;
@@ -1226,8 +1247,9 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                 vv[j] = load4(vnew ? a.v_new : a.v_res,
                               (vnew ? new_row : ((int64_t)bh * a.Rcap + vs) * D) + 4 * c4);
             }
-            // token tk of the pass is real, not before kv_lo and not hidden
-            const bool tseen = tk < n && t0 + tk >= r_lo && !((wh >> tk) & 1u);
+            // MASK: token tk of the pass is real, not before kv_lo and not hidden
+            bool tseen = false;
+            if constexpr (MASK) tseen = tk < n && t0 + tk >= r_lo && !((wh >> tk) & 1u);
             float sres[HG];
 #pragma unroll
             for (int h = 0; h < HG; ++h) {
@@ -1244,15 +1266,24 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
                 acc += dpp<0xB1>(acc);        // quad_perm [1,0,3,2]
                 acc += dpp<0x4E>(acc);        // quad_perm [2,3,0,1]
                 // row h sees the window's first qr.visible(h) tokens
-                sres[h] = tseen && t0 + tk < a.qr.visible(h, a.res_len) ? acc : -INFINITY;
+                if constexpr (MASK)
+                    sres[h] = tseen && t0 + tk < a.qr.visible(h, a.res_len) ? acc : -INFINITY;
+                else
+                    sres[h] = tk < n && t0 + tk >= r_lo && t0 + tk < a.qr.visible(h, a.res_len)
+                                  ? acc : -INFINITY;
             }
 #pragma unroll
             for (int h = 0; h < HG; ++h) {
                 const float mnew = fmaxf(mr[h], wave_max(sres[h]));
                 const float alpha = mr[h] == -INFINITY ? 0.f : exp2_fast(mr[h] - mnew);
                 mr[h] = mnew;
-                const float p = tseen && t0 + tk < a.qr.visible(h, a.res_len)
-                                    ? exp2_fast(sres[h] - mnew) : 0.f;
+                float p;
+                if constexpr (MASK)
+                    p = tseen && t0 + tk < a.qr.visible(h, a.res_len) ? exp2_fast(sres[h] - mnew)
+                                                                       : 0.f;
+                else
+                    p = tk < n && t0 + tk >= r_lo && t0 + tk < a.qr.visible(h, a.res_len)
+                            ? exp2_fast(sres[h] - mnew) : 0.f;
                 lr[h] = lr[h] * alpha + 0.25f * wave_sum(p);    // each token sits in 4 lanes
                 orr[h][0] *= alpha;
                 orr[h][1] *= alpha;
@@ -1476,7 +1507,7 @@ __device__ void wave_path(unsigned char* smem, const AttnLaunch& a, int split, i
             slot[HG * D + HG + khead(e)] = l_tot[e];
         }
     }
-    merge_and_store<HG, D>(smem, rstate, a, split, kvh, b);
+    merge_and_store<HG, D, MASK>(smem, rstate, a, split, kvh, b);
 }
 
 // Occupancy target: three waves per SIMD for head_dim 64 with G=32 and up to
@@ -1497,7 +1528,7 @@ constexpr int attn_waves_per_eu() {
            : (D <= 64 || (D <= 128 && (HG <= 4 || G <= 32))) ? 2 : 1;
 }
 
-template <int HG, int D, int G, int NGC, bool R16>
+template <int HG, int D, int G, int NGC, bool R16, bool MASK>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(attn_waves_per_eu<HG, D, G>())))
 void attn_mfma_kernel(AttnLaunch a) {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -1508,7 +1539,7 @@ void attn_mfma_kernel(AttnLaunch a) {
                       attn_waves_per_eu<HG, D, G>() * S::lds(S::NGMAX) <= 160 * 1024,
                   "occupancy target exceeds the CU's LDS");
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    wave_path<S, NGC, R16>(smem, a, split, kvh, b);
+    wave_path<S, NGC, R16, MASK>(smem, a, split, kvh, b);
 }
 
 int max_lds_per_block() {
@@ -1530,7 +1561,19 @@ int launch_shape(const AttnLaunch& a, hipStream_t st) {
                          "group_size_v=%d needs %d bytes of LDS per workgroup; the device "
                          "allows %d", HG, D, G, a.Gv, lds, lds_limit);
     const dim3 grid(a.n_splits, a.Hkv, a.B);
-    attn_mfma_kernel<HG, D, G, NGC, R16><<<grid, kBlock, lds, st>>>(a);
+    // Launches with hidden positions run their own instances (MASK), so that
+    // every other launch runs exactly the code it ran without mask support.
+    // With the mask's code in the same instances, hipcc 7.2 scheduled a VALU
+    // write into the dead zero-row element of an accumulating MFMA 8 wait
+    // states after it, and the MFMA's later write of that register clobbered
+    // the value: timing-dependent wrong scores at head_dim 64 with one query
+    // head per kv head; keeping the element live moved the problem to run-to-
+    // run differences at config 4.  The MASK instances were checked on their
+    // own (every instance family, long contexts, repeated calls).
+    if (a.hidden)
+        attn_mfma_kernel<HG, D, G, NGC, R16, true><<<grid, kBlock, lds, st>>>(a);
+    else
+        attn_mfma_kernel<HG, D, G, NGC, R16, false><<<grid, kBlock, lds, st>>>(a);
     return check_launch("packed_decode_attention (mfma)");
 }
 

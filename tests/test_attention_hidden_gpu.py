@@ -60,6 +60,7 @@ CASES = [
     (2, 8, 2, 64, 16, 16, 32, 200, 4, 3, "right"),         # generic, multi-token, splits
     (2, 8, 2, 128, 32, 32, 128, 100, 1, 0, "holes"),       # no chunk yet: window pass
     (2, 8, 2, 128, 32, 32, 128, 100, 3, 0, "right"),       # the same, 3 query tokens
+    (1, 8, 2, 128, 32, 32, 128, 12300, 1, 1, "holes"),     # one split: > 64 chunks per wave
 ]
 
 
