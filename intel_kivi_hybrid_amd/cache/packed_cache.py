@@ -183,8 +183,9 @@ class KiviPackedLayer(CacheLayerMixin):
                              f"heads but got {B} x {H}; call reset() before a new batch")
         self.settle()
         n = key_states.shape[-2]
-        k = key_states.to(self.owner.device)
-        v = value_states.to(self.owner.device)
+        k, v = key_states, value_states
+        if k.device != st.device or v.device != st.device:
+            k, v = k.to(st.device), v.to(st.device)
         if self.get_seq_length() == 0:
             # Prompt: attention reads these tensors, the store takes them
             # (every owed chunk in one flush launch).
@@ -219,19 +220,22 @@ class KiviPackedLayer(CacheLayerMixin):
         step does its flushes now; a longer one leaves them to the next
         update."""
         st = self.store
-        L = query.shape[2]
+        B, Hq, L, D = query.shape
+        # (each decode step calls this once per layer: no-op conversions are
+        # skipped, since each costs about a microsecond of host time)
+        native = query.dtype == torch.float32 and query.device == st.device
+        q = query if native else query.to(st.device, torch.float32)
         if L == 1:
-            q = query[:, :, 0, :].to(st.device, torch.float32).contiguous()
-            o = st.attention(q, softmax_scale=scaling, kv_start=kv_start,
-                             hidden=hidden).unsqueeze(1)
+            # [B, Hq, 1, D] is the decode kernel's query as it stands
+            o = st.attention(q.contiguous(), softmax_scale=scaling, kv_start=kv_start,
+                             hidden=hidden).view(B, 1, Hq, D)
         else:
-            q = query.to(st.device, torch.float32)
             o = st.attention(q, softmax_scale=scaling, causal=True, kv_start=kv_start,
                              hidden=hidden)
         self._awaiting_attention = False
         if L == 1:
             self.settle()
-        return o.to(query.device, query.dtype)
+        return o if native else o.to(query.device, query.dtype)
 
     # ------------------------------------------------------------ edits
     def crop(self, tokens_to_remove: int) -> None:

@@ -91,6 +91,8 @@ class CpuPackedStore:
                                                   self.hist_v.numpy(), self.res_k.numpy(),
                                                   self.res_v.numpy(), softmax_scale, starts, vis)
             return torch.from_numpy(o).float()
+        if q.dim() == 4:                      # [B, Hq, 1, D]: one token, as [B, Hq, D]
+            q = q[:, :, 0]
         o = oracle_attention.decode_attention(q.numpy(), self.hist_k.numpy(),
                                               self.hist_v.numpy(), self.res_k.numpy(),
                                               self.res_v.numpy(), softmax_scale, starts, vis)
