@@ -469,22 +469,31 @@ def packed_decode_attention(q, store, softmax_scale=None, out=None, num_splits=0
     token per sequence, straight from a :class:`PackedKVStore`.
 
     q: [B, Hq, D] or [B, Hq, 1, D] fp32 on the store's device.  Returns
-    ``out`` ([B, Hq, D] fp32), launched on the current stream (asynchronous)."""
-    _check_tensor(q, "q", torch.float32)
-    B, Hq, D = store.B, q.shape[1], store.D
-    _check(q.dim() in (3, 4) and q.shape[0] == B and q.shape[-1] == D
-           and (q.dim() == 3 or q.shape[2] == 1),
-           "q must be [B, Hq, D] or [B, Hq, 1, D] matching the store, got ", tuple(q.shape))
-    _check(q.device == store.device, "q must be on the store's device")
+    ``out`` ([B, Hq, D] fp32), launched on the current stream (asynchronous).
+
+    A decode step makes this call once per layer, so the checks are ordered
+    for the common case: one combined test each, the detailed messages only
+    on failure."""
+    if not (isinstance(q, torch.Tensor) and q.is_cuda and q.dtype is torch.float32
+            and q.is_contiguous()):
+        _check_tensor(q, "q", torch.float32)
+    B, D = store.B, store.D
+    shp = q.shape
+    nd = len(shp)
+    if not ((nd == 3 or (nd == 4 and shp[2] == 1)) and shp[0] == B and shp[-1] == D):
+        _fail("q must be [B, Hq, D] or [B, Hq, 1, D] matching the store, got ", tuple(shp))
+    Hq = shp[1]
+    dev = q.get_device()
+    _check(dev == device_index(store.device), "q must be on the store's device")
     if out is None:
-        out = torch.empty(B, Hq, D, dtype=torch.float32, device=q.device)
+        out = q.new_empty((B, Hq, D))
     else:
         _check_tensor(out, "out", torch.float32)
         _check(out.numel() == B * Hq * D, "out must hold B*Hq*D elements")
     scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
     need = store.workspace_bytes(Hq, num_splits)
     if workspace is None:
-        workspace = _workspace(q.device, need)
+        workspace = _workspace(dev, need)
     elif need:
         _check(workspace.is_contiguous() and workspace.numel() * workspace.element_size() >= need,
                "workspace must be contiguous and hold ", need, " bytes")
@@ -495,7 +504,7 @@ def packed_decode_attention(q, store, softmax_scale=None, out=None, num_splits=0
         # the staged token goes into the ring within this launch
         kn, vn = pend
         # (plain ints for the pointers: the entry points' argtypes convert them)
-        with on_device(q.device):
+        with on_device(dev):
             _native.check(_lib.kivi_packed_decode_attention_append(
                 q.data_ptr(), kn.data_ptr(), vn.data_ptr(), kn.stride(0), kn.stride(1),
                 store.k_codes.data_ptr(), store.k_scale.data_ptr(), store.k_zero.data_ptr(),
@@ -504,10 +513,10 @@ def packed_decode_attention(q, store, softmax_scale=None, out=None, num_splits=0
                 workspace.data_ptr() if workspace is not None else 0, ws_bytes,
                 B, Hq, store.H, D, store.G, store.Gv, store.capacity, store.n_chunks, store.R,
                 store.res_start, store.res_len, scale, int(num_splits),
-                stream_handle(q.device)), "packed_decode_attention")
+                stream_handle(dev)), "packed_decode_attention")
         store._pending = None
         return out
-    with on_device(q.device):
+    with on_device(dev):
         _native.check(_lib.kivi_packed_decode_attention(
             q.data_ptr(), store.k_codes.data_ptr(), store.k_scale.data_ptr(),
             store.k_zero.data_ptr(), store.v_codes.data_ptr(), store.v_scale.data_ptr(),
@@ -515,7 +524,7 @@ def packed_decode_attention(q, store, softmax_scale=None, out=None, num_splits=0
             out.data_ptr(), workspace.data_ptr() if workspace is not None else 0, ws_bytes,
             B, Hq, store.H, D, store.G, store.Gv, store.capacity, store.n_chunks, store.R,
             store.res_start, store.res_len, scale, int(num_splits),
-            stream_handle(q.device)), "packed_decode_attention")
+            stream_handle(dev)), "packed_decode_attention")
     return out
 
 

@@ -14,14 +14,21 @@ import contextlib
 import torch
 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+# the current device's index without torch.cuda.current_device()'s Python
+# wrapper (the C++ side initialises the runtime itself when it has to)
+_current = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
 _NULL = contextlib.nullcontext()
 
 
-def device_index(device: torch.device) -> int:
-    return device.index if device.index is not None else torch.cuda.current_device()
+def device_index(device) -> int:
+    """The index of ``device``: a torch.device (no index: the current
+    device) or an int, which is returned as it is."""
+    if isinstance(device, int):
+        return device
+    return device.index if device.index is not None else _current()
 
 
-def stream_handle(device: torch.device) -> int:
+def stream_handle(device) -> int:
     """The HIP stream handle of ``device``'s current stream (the stream
     ``torch.cuda.current_stream(device)`` names)."""
     if _raw_stream is not None:
@@ -29,9 +36,10 @@ def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def on_device(device: torch.device):
-    """A context in which ``device`` is the current device: no switch when it
-    already is."""
-    if torch.cuda.current_device() == device_index(device):
+def on_device(device):
+    """A context in which ``device`` (a torch.device or an index) is the
+    current device: no switch when it already is."""
+    idx = device_index(device)
+    if _current() == idx:
         return _NULL
-    return torch.cuda.device(device)
+    return torch.cuda.device(idx)

@@ -184,7 +184,8 @@ class KiviPackedLayer(CacheLayerMixin):
         self.settle()
         n = key_states.shape[-2]
         k, v = key_states, value_states
-        if k.device != st.device or v.device != st.device:
+        dev = st.device.index
+        if k.get_device() != dev or v.get_device() != dev:
             k, v = k.to(st.device), v.to(st.device)
         if self.get_seq_length() == 0:
             # Prompt: attention reads these tensors, the store takes them
@@ -223,7 +224,7 @@ class KiviPackedLayer(CacheLayerMixin):
         B, Hq, L, D = query.shape
         # (each decode step calls this once per layer: no-op conversions are
         # skipped, since each costs about a microsecond of host time)
-        native = query.dtype == torch.float32 and query.device == st.device
+        native = query.dtype is torch.float32 and query.get_device() == st.device.index
         q = query if native else query.to(st.device, torch.float32)
         if L == 1:
             # [B, Hq, 1, D] is the decode kernel's query as it stands

@@ -26,7 +26,7 @@ from typing import Optional
 
 import torch
 
-from . import _native
+from . import _C, _native
 from ._device import on_device, stream_handle
 
 _lib = _native.load()
@@ -151,10 +151,10 @@ class PackedKVStore:
         self.G, self.Gv, self.R = group_size, gv, residual_capacity
         # 1: codes stored in matrix-core operand order, 0: plain byte order
         self.code_layout = int(_lib.kivi_store_code_layout(head_dim, group_size, gv))
-        self.device = torch.device(device)
         self.keep_history = keep_history
         self.k_res = torch.zeros(batch, kv_heads, residual_capacity, head_dim,
-                                 dtype=residual_dtype, device=self.device)
+                                 dtype=residual_dtype, device=torch.device(device))
+        self.device = self.k_res.device      # with its index ("cuda" names the current one)
         self.v_res = torch.zeros_like(self.k_res)
         self.res_start = 0
         self.res_len = 0
@@ -276,7 +276,9 @@ class PackedKVStore:
                 or k.shape[3] != self.D:
             raise ValueError(f"new tokens must be [B={self.B}, Hkv={self.H}, n, D={self.D}] for "
                              f"both K and V, got {tuple(k.shape)} and {tuple(v.shape)}")
-        k, v = k.to(self.device), v.to(self.device)
+        dev = self.device.index
+        if k.get_device() != dev or v.get_device() != dev:
+            k, v = k.to(self.device), v.to(self.device)
         if self.k_res.dtype != torch.float32:
             k, v = k.to(self.k_res.dtype), v.to(self.k_res.dtype)
         elif k.dtype not in _SRC_DTYPES or v.dtype != k.dtype:
@@ -550,7 +552,6 @@ class PackedKVStore:
         position of a left-padded batch; ``key_mask`` ``[B, T]`` (nonzero =
         attended) or its packed ``hidden`` words: any other padding pattern
         (``_C.packed_attention``)."""
-        from . import _C
         masked = kv_start is not None or key_mask is not None or hidden is not None
         if masked and (q.dim() == 3 or q.shape[2] == 1):
             q4 = q if q.dim() == 4 else q.unsqueeze(2)
