@@ -257,7 +257,10 @@ class PackedKVStore:
         exactly; any strides with contiguous channels).  The window must have
         room (callers flush first)."""
         self._commit()
-        k, v = self._token_source(k, v)
+        self._append_source(*self._token_source(k, v))
+
+    def _append_source(self, k: torch.Tensor, v: torch.Tensor) -> None:
+        """append() of tokens that _token_source has already prepared."""
         n = k.shape[2]
         if self.res_len + n > self.R:
             raise RuntimeError(f"residual window overflow ({self.res_len} + {n} > {self.R})")
@@ -320,7 +323,9 @@ class PackedKVStore:
             skip += used - from_ring
             done += m
         if skip < n:
-            self.append(k[:, :, skip:], v[:, :, skip:])
+            if skip:
+                k, v = k[:, :, skip:], v[:, :, skip:]
+            self._append_source(k, v)
         return n_flush
 
     def _flush_run(self, k: torch.Tensor, v: torch.Tensor, n_chunks: int) -> None:
