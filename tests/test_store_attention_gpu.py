@@ -291,3 +291,21 @@ def test_split_merge_head_dim_96_negative_scores(store_cls):
         err = rel_err(out, ref)
         print(f"[attn] D=96 negative scores, {splits} splits: rel_err={err:.3e}", flush=True)
         assert err <= ATTN_TOL
+
+
+def test_store_on_device_without_index(store_cls):
+    """A store made with ``device="cuda"`` is on the current device by index,
+    so queries on that device (``cuda:0``) are its own: decode and
+    multi-token attention give the bits of a store made with ``"cuda:0"``."""
+    B, Hq, Hkv, D, G, R, T = 2, 8, 2, 64, 32, 64, 300
+    print("[attn] store on device 'cuda'", flush=True)
+    k, v = make_kv(B, Hkv, T, D, seed=31)
+    plain = store_cls(B, Hkv, D, G, R, "cuda")
+    named = store_cls(B, Hkv, D, G, R, "cuda:0")
+    assert plain.device == torch.device("cuda", torch.cuda.current_device())
+    fill_store(plain, k, v, R)
+    fill_store(named, k, v, R)
+    q = seeded_q(B, Hq, D, seed=32).cuda()
+    assert torch.equal(plain.attention(q), named.attention(q))
+    q3 = torch.randn(B, Hq, 3, D, generator=torch.Generator().manual_seed(33)).cuda()
+    assert torch.equal(plain.attention(q3), named.attention(q3))
