@@ -13,8 +13,10 @@ Also reported: the attention kernel alone against the 8 TB/s HBM roofline
 (``roofline``: context 8192 = 8064 quantised + a full window of 128; HBM
 traffic from two rocprofv3 counter passes in the same run), configs 3 and 5
 at their stated token counts, the config-2 codec ops through ``_C``
-(quantise, dequantise, round-trip), the batched prefill flush, and CPU
-baselines of the reference path timed on the host over the same K/V bits.
+(quantise, dequantise, round-trip), the batched prefill flush, greedy
+decoding end to end (GPT-2 as the reference times it; a Llama-3-8B-shaped
+model at serving scale), and CPU baselines of the reference path timed on
+the host over the same K/V bits.
 
 Algorithmic bytes (per (batch, kv-head)):
   attention : D*Tq/4 + 8*D*Tq/Gk + Tq*D/4 + 8*Tq*D/Gv + 2*r*Tr*D + 8*(Hq/Hkv)*D
@@ -31,6 +33,7 @@ Algorithmic bytes (per (batch, kv-head)):
 from __future__ import annotations
 
 import argparse
+import contextlib
 import json
 import os
 import sys
@@ -695,6 +698,145 @@ def e2e_gpt2(dev, n_tokens=200, G=32, R=64, prompt_len=40, reps=3, log=print):
 
 
 # --------------------------------------------------------------------------
+# End to end at serving scale: config 4's attention geometry inside a
+# Llama-3-8B-shaped model (no reference figure: the reference times GPT-2 only).
+# --------------------------------------------------------------------------
+def e2e_llama(dev, B=16, context=8192, steps=32, layers=4, G=32, R=128, reps=3, log=print):
+    """Seeded random-init Llama-3-8B shape (hidden 4096, MLP 14336, 32 query /
+    8 kv heads, head_dim 128, vocab 128256) cut to ``layers`` layers, bf16 on
+    the GPU; B sequences of ``context`` seeded prompt tokens, then ``steps``
+    decode steps of one token per sequence, the same seeded tokens in every
+    arm (identical work per arm and comparable final logits: a random-init
+    model's greedy choices part at the first small difference), timed for
+    four caches:
+    * bf16 ``DynamicCache`` (transformers' default: K/V concatenated every
+      step, SDPA over them);
+    * bf16 ``StaticCache`` (preallocated for context + steps, SDPA over the
+      whole buffer with a mask);
+    * ``KiviPackedCache`` (2-bit store, bf16 residual ring of R tokens, the
+      packed attention kernel; the prompt attends with SDPA, as in the other
+      arms, and is then quantised);
+    * ``KiviCache`` driven as the reference's generate() drives it
+      (get_full_cache() before each forward, add_tokens() after): the same
+      KIVI arithmetic served as a dequantised bf16 cache to SDPA, so the
+      packed arm's logits are also compared with it.
+    Each arm: the prompt forward untimed (last position's logits only), then
+    ``steps`` forwards of one token per sequence with no host sync inside the
+    timed region; one untimed run, then ``reps`` timed runs with the arms in
+    turn, the median reported.  tok/s = B * steps / seconds.  Fidelity
+    against the bf16 ``DynamicCache``: max |logit difference| / max |logit|
+    and the mean cosine similarity of the final step's logits rows, and the
+    same of the packed arm against the served KIVI cache (the same
+    quantisation).  On a random-init model 2-bit K/V move the logits far
+    more than on a trained one: its attention spreads over hundreds of
+    tokens of zero-mean values, so the output is of the order of the
+    quantisation noise averaged over them; both KIVI arms differ from bf16
+    alike and agree with each other."""
+    import torch
+    from transformers import DynamicCache, LlamaConfig, LlamaForCausalLM, StaticCache
+    from intel_kivi_hybrid_amd import KiviCache, KiviPackedCache
+    from intel_kivi_hybrid_amd.cache.packed_cache import packed_attention
+    torch.manual_seed(0)
+    cfg = LlamaConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336,
+                      num_hidden_layers=layers, num_attention_heads=32, num_key_value_heads=8,
+                      max_position_embeddings=context + steps + 8, rope_theta=500000.0)
+    model = LlamaForCausalLM(cfg).eval().to(dev, torch.bfloat16)
+    ids = torch.randint(0, cfg.vocab_size, (B, context),
+                        generator=torch.Generator().manual_seed(1)).to(dev)
+    dec = torch.randint(0, cfg.vocab_size, (B, steps),
+                        generator=torch.Generator().manual_seed(2)).to(dev)
+
+    def static_cache():
+        return StaticCache(config=cfg, max_cache_len=context + steps)
+
+    def packed_cache():
+        return KiviPackedCache.from_model(model, device=dev, group_size=G, residual_length=R)
+
+    @torch.no_grad()
+    def run_served():
+        cache = KiviCache.from_model(model, device=dev, group_size=G, residual_length=R)
+        pos = torch.arange(context + steps, device=dev)
+        out = model(ids, use_cache=True, cache_position=pos[:context], logits_to_keep=1)
+        cache.add_tokens(out.past_key_values)
+        del out
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            out = model(dec[:, i:i + 1], past_key_values=cache.get_full_cache(), use_cache=True,
+                        cache_position=pos[context + i:context + i + 1])
+            cache.add_tokens(out.past_key_values)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        return out.logits[:, -1].float(), dt, cache
+
+    @torch.no_grad()
+    def run(make, packed):
+        if make is None:
+            return run_served()
+        ctx = packed_attention(model) if packed else contextlib.nullcontext()
+        with ctx:
+            cache = make()
+            pos = torch.arange(context + steps, device=dev)      # positions made up front
+            model(ids, past_key_values=cache, use_cache=True, cache_position=pos[:context],
+                  logits_to_keep=1)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for i in range(steps):
+                out = model(dec[:, i:i + 1], past_key_values=cache, use_cache=True,
+                            cache_position=pos[context + i:context + i + 1])
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+        return out.logits[:, -1].float(), dt, cache
+
+    arms = (("bf16_dynamic", DynamicCache, False), ("bf16_static", static_cache, False),
+            ("kivi_packed", packed_cache, True), ("kivi_served", None, False))
+    for _, make, packed in arms:
+        run(make, packed)
+        torch.cuda.empty_cache()
+    times, logits_of, caches = {n: [] for n, _, _ in arms}, {}, {}
+    for _ in range(reps):
+        for name, make, packed in arms:
+            logits, dt, cache = run(make, packed)
+            times[name].append(dt)
+            logits_of[name] = logits
+            if name.startswith("kivi"):
+                caches[name] = cache.get_stats(0)
+            del cache
+            torch.cuda.empty_cache()
+    kv_bf16 = 2 * B * cfg.num_key_value_heads * (context + steps) * 128 * 2
+    res = {}
+    for name, _, _ in arms:
+        dt = sorted(times[name])[len(times[name]) // 2]
+        r = {"ms_per_step": round(dt / steps * 1e3, 3), "tok_s": round(B * steps / dt, 1),
+             "seconds_all": [round(t, 4) for t in times[name]]}
+        if name != "bf16_dynamic":
+            ref, got = logits_of["bf16_dynamic"], logits_of[name]
+            err = ((got - ref).abs().max() / ref.abs().max()).item()
+            r["logits_rel_err_vs_dynamic"] = float(f"{err:.3e}")
+            r["logits_cosine_vs_dynamic"] = round(
+                torch.nn.functional.cosine_similarity(got, ref, dim=-1).mean().item(), 6)
+            r["speedup_vs_dynamic"] = round(sorted(times["bf16_dynamic"])[reps // 2] / dt, 3)
+        if name == "kivi_packed":
+            ref, got = logits_of["kivi_served"], logits_of[name]
+            err = ((got - ref).abs().max() / ref.abs().max()).item()
+            r["logits_rel_err_vs_served"] = float(f"{err:.3e}")
+            r["logits_cosine_vs_served"] = round(
+                torch.nn.functional.cosine_similarity(got, ref, dim=-1).mean().item(), 6)
+        if name in caches:          # the KIVI accounting of get_stats (2-bit store + window)
+            r["layer0_kivi_bytes"] = caches[name]["kivi_bytes"]
+        else:
+            r["layer0_kv_bytes"] = kv_bf16
+        res[name] = r
+        log(f"[bench] e2e llama {name}: {r}")
+    res["config"] = {"model": f"Llama-3-8B shape cut to {layers} layers (hidden 4096, MLP 14336, "
+                              f"32/8 heads, head_dim 128, vocab 128256), seeded random init, "
+                              f"bf16, on the GPU", "batch": B, "prompt_tokens": context,
+                     "decode_steps": steps, "group_size": G, "residual": R, "timed_runs": reps}
+    del model
+    return res
+
+
+# --------------------------------------------------------------------------
 CONFIG4 = (64, 32, 8, 128, 8192, 128, 32)      # B, Hq, Hkv, D, context, R, G
 PRECISION = ("fp32 inputs and outputs; 2-bit codes with fp32 scales/zeros, bit-exact to the "
              "reference codec; attention products on bf16 matrix cores with fp32 accumulation, "
@@ -715,7 +857,7 @@ def main():
                     help="skip the two rocprofv3 counter passes behind roofline.traffic")
     ap.add_argument("--only", choices=["config4", "attention", "gqa8", "ring16", "b1",
                                        "config3", "config5", "codec", "prefill", "copy",
-                                       "traffic", "cache1", "e2e"],
+                                       "traffic", "cache1", "e2e", "e2e_llama"],
                     default=None,
                     help="run one workload (for profiling); 'gqa8' is attention of 64 query "
                          "heads over config 4's store (8 query heads per kv head); 'ring16' "
@@ -725,7 +867,9 @@ def main():
                          "a plain 512 MiB device copy for calibrating the FETCH_SIZE / "
                          "WRITE_SIZE counters; 'traffic' is the workload of the counter passes; "
                          "'cache1' is config 1's KiviCache loop; 'e2e' is GPT-2 greedy "
-                         "decoding with and without the KIVI cache")
+                         "decoding with and without the KIVI cache; 'e2e_llama' is greedy "
+                         "decoding of a 4-layer Llama-3-8B-shaped bf16 model at B=16, 8K "
+                         "context with transformers' caches and the packed cache")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the KIVI hot path here is built and "
@@ -938,6 +1082,12 @@ def main():
         extra["e2e_gpt2"] = e2e_gpt2(dev, log=log)
         torch.cuda.empty_cache()
         if only == "e2e":
+            return
+
+    if only in (None, "e2e_llama"):
+        extra["e2e_llama"] = e2e_llama(dev, log=log)
+        torch.cuda.empty_cache()
+        if only == "e2e_llama":
             return
 
     qb = None
