@@ -447,15 +447,39 @@ Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
     }
     p.mfma = p.layout == kLayoutMfma;
     if (p.mfma) {
-        // Aim for ~2048 chunk waves in flight (8 per CU) with >= 2 chunks per
-        // wave.  Few (batch, kv-head) pairs take many splits: B=1, 32/8 heads
-        // measured 16.4 us at 2K context with 8 splits (2 chunks per wave)
-        // against 21.4 us with 2 (8 per wave), 16.6 us at 8K with 32 against
-        // 22.0 us with 8 (attention + merge).  Large batches need no split.
-        constexpr int kWavesPerGroup = 4, kTargetWaves = 2048, kMinChunksPerWave = 2;
+        // Head_dim 128 (two workgroups per CU): the larger of two split
+        // counts, then at least 2 chunks per wave:
+        // (a) the most splits whose workgroups still fit the chip at once
+        //     (512: two per CU) while every wave keeps >= 16 chunks, so that
+        //     one wave per workgroup takes the residual window alone;
+        // (b) enough splits for 256 workgroups (one per CU).
+        // Swept over B = 1-64 sequences at 2K-32K contexts (32/8 heads, the
+        // best split count per shape against this rule's): B=12 at 8K takes
+        // 4 splits (31.5 us; the 2048-wave target below took 6: 39.6 us, 576
+        // workgroups, the last 64 in a second round), B=24 2 (50.2 against
+        // 60.0 us), B=8 4 (24.4 against 27.3 us), B=2 16 (17.3 against
+        // 19.0 us); one sequence keeps 32, and configs 3, 4 and 5 keep 1, 1
+        // and 16.
+        // Other head dims aim for ~2048 chunk waves in flight with >= 2
+        // chunks per wave: at head_dim 64 (three workgroups per CU, half the
+        // bytes per chunk) that stayed ahead (B=16 and 4, 12/12 heads, 8K:
+        // 28.0 and 15.2 us against 31.0 and 16.7 us with the rule above).
+        constexpr int kWavesPerGroup = 4, kMinChunksPerWave = 2;
+        constexpr int kSlots = 512, kCUs = 256;        // MI355X: 256 CUs, two workgroups each
+        constexpr int kMinChunksForOneResWave = 16, kTargetWaves = 2048;
         int S = splits_hint;
         if (S <= 0) {
-            S = (kTargetWaves + kWavesPerGroup * B * Hkv - 1) / (kWavesPerGroup * B * Hkv);
+            const int pairs = B * Hkv;
+            if (D == 128) {
+                int sa = 1;
+                for (int s = 2; s <= kMaxSplits && (int64_t)pairs * s <= kSlots; ++s)
+                    if ((n_chunks + kWavesPerGroup * s - 1) / (kWavesPerGroup * s) >=
+                        kMinChunksForOneResWave)
+                        sa = s;
+                S = max(max(sa, kCUs / pairs), 1);
+            } else {
+                S = (kTargetWaves + kWavesPerGroup * pairs - 1) / (kWavesPerGroup * pairs);
+            }
             const int cap = (n_chunks + kWavesPerGroup * kMinChunksPerWave - 1) /
                             (kWavesPerGroup * kMinChunksPerWave);
             S = min(S, max(cap, 1));
@@ -472,7 +496,6 @@ Plan make_plan(int B, int Hkv, int D, int G, int Gv, int n_chunks, int res_len,
         p.chunks_per_wave = (n_chunks + kWavesPerGroup * S - 1) / (kWavesPerGroup * S);
         p.n_qsplits = (n_chunks + kWavesPerGroup * p.chunks_per_wave - 1) /
                       (kWavesPerGroup * p.chunks_per_wave);
-        constexpr int kMinChunksForOneResWave = 16;
         constexpr int kEarlyPerPassX2 = 6;        // 3 chunk steps per residual pass
         if (res_len > 0 && p.chunks_per_wave >= kMinChunksForOneResWave) {
             p.res_waves = 1;
