@@ -512,3 +512,49 @@ def test_padded_batch_any_pattern_follows_reference_flow(hip_device, kind):
     assert plan[0] is None and plan[1] is not None      # the hidden-bits path ran
     print(f"[packed-{kind}] worst logits rel err {worst:.2e}", flush=True)
     assert ours.total_flushes == ref.total_flushes > 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@torch.no_grad()
+def test_half_precision_logits_match_served_cache(hip_device, dtype):
+    """A half-precision Llama (GQA 4:1, head_dim 128) decodes the same
+    seeded tokens over a 1K-token prompt with the packed cache (2-bit store,
+    16-bit residual ring, the fused kernel) and with KiviCache driven as the
+    reference's generate() drives it (the same quantisation, served to SDPA
+    as a dequantised cache of the model's dtype): the final logits agree to
+    within the served cache's 16-bit rounding (cosine >= 0.999, max
+    difference <= 5 % of the largest logit)."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+    from intel_kivi_hybrid_amd import KiviCache, KiviPackedCache
+    torch.manual_seed(4)
+    cfg = LlamaConfig(vocab_size=2048, hidden_size=1024, intermediate_size=2048,
+                      num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2,
+                      max_position_embeddings=2048)
+    model = LlamaForCausalLM(cfg).eval().to(hip_device, dtype)
+    B, T, steps, G, R = 2, 1000, 40, 32, 64
+    ids = torch.randint(0, cfg.vocab_size, (B, T), generator=torch.Generator().manual_seed(5))
+    dec = torch.randint(0, cfg.vocab_size, (B, steps), generator=torch.Generator().manual_seed(6))
+    ids, dec = ids.to(hip_device), dec.to(hip_device)
+    pos = torch.arange(T + steps, device=hip_device)
+
+    packed = KiviPackedCache.from_model(model, device="cuda:0", group_size=G, residual_length=R)
+    with pc.packed_attention(model):
+        model(ids, past_key_values=packed, use_cache=True, cache_position=pos[:T])
+        for i in range(steps):
+            a = model(dec[:, i:i + 1], past_key_values=packed, use_cache=True,
+                      cache_position=pos[T + i:T + i + 1]).logits[:, -1].float()
+
+    served = KiviCache.from_model(model, device="cuda:0", group_size=G, residual_length=R)
+    out = model(ids, use_cache=True, cache_position=pos[:T])
+    served.add_tokens(out.past_key_values)
+    for i in range(steps):
+        out = model(dec[:, i:i + 1], past_key_values=served.get_full_cache(), use_cache=True,
+                    cache_position=pos[T + i:T + i + 1])
+        served.add_tokens(out.past_key_values)
+    b = out.logits[:, -1].float()
+    assert packed.total_flushes == served.total_flushes > 0
+    cos = torch.nn.functional.cosine_similarity(a, b, dim=-1).min().item()
+    rel = ((a - b).abs().max() / b.abs().max()).item()
+    print(f"[packed-half] {dtype}: cosine {cos:.6f}, max diff {rel:.3e} of the largest logit",
+          flush=True)
+    assert cos >= 0.999 and rel <= 5e-2
