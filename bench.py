@@ -863,7 +863,8 @@ def main():
                          "heads over config 4's store (8 query heads per kv head); 'ring16' "
                          "is config-4 attention over a store whose residual ring is bf16 (a "
                          "bf16 model's packed cache); 'b1' is config 4's shape for one "
-                         "sequence (B=1: the split plan and its merge); 'copy' is "
+                         "sequence (B=1: the split plan and its merge) and for 16 and 24 "
+                         "sequences; 'copy' is "
                          "a plain 512 MiB device copy for calibrating the FETCH_SIZE / "
                          "WRITE_SIZE counters; 'traffic' is the workload of the counter passes; "
                          "'cache1' is config 1's KiviCache loop; 'e2e' is GPT-2 greedy "
@@ -1001,6 +1002,25 @@ def main():
         log(f"[bench] one sequence, 100 tokens all in the window: {a0['avg_us']:.1f} us per call")
         extra["attention_b1_window_only"] = {k_: a0[k_] for k_ in ("avg_us", "Tq", "Tr")}
         del s0, k, v
+        # mid batches at config 4's heads and context (the split plan's
+        # middle ground: 4 and 2 splits), each with a second store called
+        # in turn so that the MALL cannot serve the bytes
+        for Bm in (16, 24):
+            k, v = synth_kv(Bm, H1, T1, D1, 1234 + 43 + Bm)
+            sts = []
+            for _ in range(3 if Bm == 16 else 2):
+                s_ = make_store(k[:, :, :T1 - 1], v[:, :, :T1 - 1], G1, G1, R1, dev)
+                s_.append(k[:, :, -1:].to(dev), v[:, :, -1:].to(dev))
+                sts.append(s_)
+            del k, v
+            qm = (torch.randn(Bm, Hq1, D1, generator=torch.Generator().manual_seed(43))
+                  * D1 ** -0.5).to(dev)
+            am = time_attention(sts[0], qm, args.attn_iters, rotate=sts[1:])
+            log(f"[bench] B={Bm} (config 4's heads, context {T1}): {am['avg_us']:.1f} us per "
+                f"call, {am['gbs']:.0f} GB/s, {am['splits']} splits")
+            extra[f"attention_b{Bm}"] = {k_: am[k_] for k_ in ("avg_us", "gbs", "Tq", "Tr",
+                                                              "splits")}
+            del sts
         torch.cuda.empty_cache()
 
     if only in (None, "config3"):
