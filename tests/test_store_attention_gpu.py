@@ -309,3 +309,29 @@ def test_store_on_device_without_index(store_cls):
     assert torch.equal(plain.attention(q), named.attention(q))
     q3 = torch.randn(B, Hq, 3, D, generator=torch.Generator().manual_seed(33)).cuda()
     assert torch.equal(plain.attention(q3), named.attention(q3))
+
+
+@pytest.mark.parametrize("B,T,splits", [(8, 4096, 4), (12, 8192, 4), (24, 8192, 2)])
+def test_attention_mid_batch_plans(store_cls, B, T, splits):
+    """Mid batches at config 4's heads run the split plan's middle ground:
+    256 workgroups with 8 chunks per wave (B=8, 4K context), 384 with 16
+    (B=12, 8K: one wave per workgroup takes the window) and 384 with 32 (B=24,
+    8K), each split merged; the automatic plan's split count is the one
+    stated, and the output matches the float64 oracle at 1e-3."""
+    Hq, Hkv, D, G, R = 32, 8, 128, 32, 128
+    k, v = make_kv(B, Hkv, T, D, seed=T + B)
+    st = store_cls(B, Hkv, D, G, R, "cuda:0", chunk_capacity=T // G + 1)
+    st.extend(k.cuda(), v.cuda(), flush_at=R)
+    ws = st.workspace_bytes(Hq)
+    assert ws == B * Hkv * 4 * splits * (D + 2) * 4
+    print(f"[attn] mid batch B={B} T={T}: chunks={st.n_chunks} res={st.res_len} "
+          f"splits={splits}", flush=True)
+    q = seeded_q(B, Hq, D, seed=B)
+    out = st.attention(q.cuda())
+    torch.cuda.synchronize()
+    kh, vh = oracle_history(k, v, st.n_chunks, G, G)
+    q0 = st.n_chunks * G
+    ref = decode_attention(q.numpy(), kh, vh, k[:, :, q0:].numpy(), v[:, :, q0:].numpy())
+    err = rel_err(out.cpu().numpy(), ref)
+    print(f"[attn]   rel_err={err:.3e}", flush=True)
+    assert err <= ATTN_TOL
