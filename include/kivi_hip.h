@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define KIVI_HIP_ABI_VERSION 6
+#define KIVI_HIP_ABI_VERSION 7
 
 #define KIVI_OK 0
 #define KIVI_ERR_INVALID_ARGUMENT 1
@@ -193,6 +193,20 @@ int kivi_store_append(const void* k_new, const void* v_new, int32_t new_dtype,
                       int64_t new_token_stride, int32_t new_tokens, void* k_res, void* v_res,
                       int32_t res_dtype, int32_t batch, int32_t kv_heads, int32_t head_dim, int32_t res_capacity,
                       int32_t slot, void* stream);
+
+/* kivi_store_append for n_layers layers of one model in as few launches as
+ * possible (16 layers per launch): layer l's new tokens k_new[l]/v_new[l]
+ * with element strides new_strides[3l..3l+2] (batch, head, token) go to its
+ * ring k_res[l]/v_res[l] from slot slots[l].  The shapes, element types and
+ * ring capacity are shared; host arrays of n_layers entries.  Replaces the
+ * per-layer residual append of KiviCache.add_tokens's layer loop
+ * (manager.py:187-231: each layer's new K/V appended to its residual), one
+ * launch per step instead of one per layer. */
+int kivi_store_append_layers(int32_t n_layers, const void* const* k_new, const void* const* v_new,
+                             const int64_t* new_strides, int32_t new_dtype, int32_t new_tokens,
+                             void* const* k_res, void* const* v_res, int32_t res_dtype,
+                             int32_t batch, int32_t kv_heads, int32_t head_dim,
+                             int32_t res_capacity, const int32_t* slots, void* stream);
 
 /* Code layout of a store with these shapes: 1 (matrix-core operand order)
  * when head_dim is 64, 128 or 256, group_size_k is 32 or 64 and

@@ -50,6 +50,9 @@ SIGNATURES = {
                                 _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     "kivi_store_append": [_vp, _vp, _i32, _i64, _i64, _i64, _i32, _vp, _vp, _i32, _i32, _i32,
                           _i32, _i32, _i32, _vp],
+    # host arrays (ctypes arrays or their addresses) for the per-layer fields
+    "kivi_store_append_layers": [_i32, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _i32, _i32, _i32,
+                                 _i32, _i32, _vp, _vp],
     "kivi_store_code_layout": [_i32, _i32, _i32],
     "kivi_packed_decode_attention_supported": [_i32, _i32, _i32, _i32, _i32],
     "kivi_packed_decode_attention_workspace_size": [_i32, _i32, _i32, _i32, _i32, _i32, _i32,

@@ -29,7 +29,7 @@ from transformers.cache_utils import DynamicCache
 
 from ..config.model_config import detect_model_config
 from ..extension.loader import kivi_native  # noqa: F401  (fails loudly without the HIP library)
-from ..store import PackedKVStore
+from ..store import PackedKVStore, append_layers
 
 __all__ = ["KiviCache"]
 
@@ -165,6 +165,10 @@ class KiviCache:
         if past_key_values is not self._cache_view:
             self._cache_view_valid = False
 
+        # Layers whose window takes this step's tokens without a flush are
+        # appended together after the loop (one launch for all of them); the
+        # others flush and append on their own, as before.
+        appends = []
         for i, (k, v) in enumerate(_iter_kv_layers(past_key_values)):
             if self.batch_size is None:
                 self.batch_size = k.shape[0]
@@ -199,16 +203,22 @@ class KiviCache:
                 f"get_full_cache(). Silently skipping here would drop this "
                 f"step's KV and corrupt all subsequent attention.")
 
+            fed = self._fed[i]
             store = self._store_for(i, k.shape[0], k.shape[1], new_k.shape[2])
             self._serve_device[i] = k.device
             self._serve_dtype[i] = k.dtype if k.dtype in (torch.bfloat16, torch.float16) \
                 else torch.float32
             # fp32, bf16 and fp16 K/V are read as they are (widening to fp32
             # is exact, as the reference's .float() is, manager.py:210-214).
+            if fed and store.res_len + new_k.shape[2] < self.R:
+                appends.append((store, new_k, new_v))
+                continue
             flushes = store.extend(new_k, new_v, flush_at=self.R)
             if flushes:
                 self._record_flushes(i, flushes)
                 self._cache_view_valid = False
+        if appends:
+            append_layers(*zip(*appends))
 
     def get_full_cache(self) -> DynamicCache:
         """The cache to pass as ``past_key_values`` to the next forward pass

@@ -648,10 +648,9 @@ __device__ __forceinline__ uint2 load4_raw16(const void* p, int64_t i, bool vec)
     return make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
 }
 
+// Element quad i of one append (i < a.total).
 template <int SRC, int RES>
-__global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= a.total) return;
+__device__ __forceinline__ void append_quad(const AppendArgs& a, int64_t i) {
     const int d4n = a.D / 4;
     const int d4 = (int)(i % d4n);
     const int64_t r = i / d4n;
@@ -669,6 +668,43 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
         reinterpret_cast<uint2*>(a.k_res)[dst] = load4_raw16(a.k_new, off, a.vec);
         reinterpret_cast<uint2*>(a.v_res)[dst] = load4_raw16(a.v_new, off, a.vec);
     }
+}
+
+template <int SRC, int RES>
+__global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < a.total) append_quad<SRC, RES>(a, i);
+}
+
+// Several layers' appends in one launch (blockIdx.y = layer within the
+// launch): the per-layer pointers, strides and slots travel in the kernel
+// arguments, the shapes are shared.
+constexpr int kMaxAppendLayers = 16;
+
+struct AppendLayer {
+    const void* k_new;
+    const void* v_new;
+    int64_t sb, sh, st;
+    void* k_res;
+    void* v_res;
+    int slot;
+    bool vec;
+};
+
+struct AppendLayers {
+    AppendLayer layer[kMaxAppendLayers];
+    int64_t total;                 // B * H * n * D/4 per layer
+    int H, D, n, Rcap;
+};
+
+template <int SRC, int RES>
+__global__ __launch_bounds__(256) void append_layers_kernel(AppendLayers a) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.total) return;
+    const AppendLayer& l = a.layer[blockIdx.y];
+    const AppendArgs one{l.k_new, l.v_new, l.sb, l.sh, l.st, l.k_res, l.v_res, a.total, a.H,
+                         a.D, a.n, a.Rcap, l.slot, l.vec};
+    append_quad<SRC, RES>(one, i);
 }
 
 }  // namespace
@@ -848,4 +884,84 @@ extern "C" int kivi_store_append(const void* k_new, const void* v_new, int32_t n
         }
     }
     return check_launch("store_append");
+}
+
+extern "C" int kivi_store_append_layers(int32_t n_layers, const void* const* k_new,
+                                        const void* const* v_new, const int64_t* new_strides,
+                                        int32_t new_dtype, int32_t new_tokens,
+                                        void* const* k_res, void* const* v_res,
+                                        int32_t res_dtype, int32_t batch, int32_t kv_heads,
+                                        int32_t head_dim, int32_t res_capacity,
+                                        const int32_t* slots, void* stream) {
+    if (n_layers < 0) return set_error(kErrInvalidArgument, "n_layers %d < 0", n_layers);
+    if (n_layers == 0 || new_tokens == 0) return 0;
+    if (!k_new || !v_new || !new_strides || !k_res || !v_res || !slots)
+        return set_error(kErrInvalidArgument, "null layer array");
+    if (batch <= 0 || kv_heads <= 0)
+        return set_error(kErrInvalidArgument, "batch and kv_heads must be positive");
+    if (head_dim <= 0 || head_dim % 4)
+        return set_error(kErrInvalidArgument, "head_dim must be positive and divisible by 4");
+    if (new_dtype < kSrcF32 || new_dtype > kSrcF16)
+        return set_error(kErrInvalidArgument, "new_dtype %d is not 0 (f32), 1 (bf16) or 2 (f16)",
+                         new_dtype);
+    if (res_dtype != kSrcF32 && res_dtype != new_dtype)
+        return set_error(kErrInvalidArgument,
+                         "res_dtype %d: the ring is f32 (0) or of the new tokens' type (%d)",
+                         res_dtype, new_dtype);
+    if (res_capacity <= 0 || new_tokens < 0 || new_tokens > res_capacity)
+        return set_error(kErrInvalidArgument, "%d new tokens exceed the ring capacity %d",
+                         new_tokens, res_capacity);
+    const int esize = new_dtype == kSrcF32 ? 4 : 2;
+    const int64_t vb = 4 * esize;
+    AppendLayers a{};
+    a.total = (int64_t)batch * kv_heads * new_tokens * (head_dim / 4);
+    a.H = kv_heads;
+    a.D = head_dim;
+    a.n = new_tokens;
+    a.Rcap = res_capacity;
+    hipStream_t st = (hipStream_t)stream;
+    for (int l0 = 0; l0 < n_layers; l0 += kMaxAppendLayers) {
+        const int nl = n_layers - l0 < kMaxAppendLayers ? n_layers - l0 : kMaxAppendLayers;
+        for (int j = 0; j < nl; ++j) {
+            const int l = l0 + j;
+            const int64_t* str = new_strides + 3 * (int64_t)l;
+            if (!k_new[l] || !v_new[l] || !k_res[l] || !v_res[l])
+                return set_error(kErrInvalidArgument, "null tensor pointer (layer %d)", l);
+            if (str[0] < 0 || str[1] < 0 || str[2] < 0)
+                return set_error(kErrInvalidArgument, "negative new-token strides (layer %d)", l);
+            if (slots[l] < 0 || slots[l] >= res_capacity)
+                return set_error(kErrInvalidArgument, "slot %d outside [0, %d) (layer %d)",
+                                 slots[l], res_capacity, l);
+            if ((uintptr_t)k_res[l] % 16 || (uintptr_t)v_res[l] % 16)
+                return set_error(kErrInvalidArgument,
+                                 "residual ring must be 16-byte aligned (layer %d)", l);
+            AppendLayer& e = a.layer[j];
+            e.k_new = k_new[l];
+            e.v_new = v_new[l];
+            e.sb = str[0];
+            e.sh = str[1];
+            e.st = str[2];
+            e.k_res = k_res[l];
+            e.v_res = v_res[l];
+            e.slot = slots[l];
+            e.vec = (uintptr_t)k_new[l] % vb == 0 && (uintptr_t)v_new[l] % vb == 0 &&
+                    (str[0] * esize) % vb == 0 && (str[1] * esize) % vb == 0 &&
+                    (str[2] * esize) % vb == 0;
+        }
+        const dim3 grid((unsigned)((a.total + 255) / 256), (unsigned)nl);
+        if (res_dtype == kSrcBF16) {
+            append_layers_kernel<kSrcBF16, kSrcBF16><<<grid, 256, 0, st>>>(a);
+        } else if (res_dtype == kSrcF16) {
+            append_layers_kernel<kSrcF16, kSrcF16><<<grid, 256, 0, st>>>(a);
+        } else {
+            switch (new_dtype) {
+                case kSrcBF16: append_layers_kernel<kSrcBF16, kSrcF32><<<grid, 256, 0, st>>>(a); break;
+                case kSrcF16: append_layers_kernel<kSrcF16, kSrcF32><<<grid, 256, 0, st>>>(a); break;
+                default: append_layers_kernel<kSrcF32, kSrcF32><<<grid, 256, 0, st>>>(a); break;
+            }
+        }
+        const int rc = check_launch("store_append_layers");
+        if (rc) return rc;
+    }
+    return 0;
 }

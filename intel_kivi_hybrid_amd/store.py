@@ -130,6 +130,58 @@ def decode_geometry_error(q_heads: int, kv_heads: int, head_dim: int, group_size
     return None if rc == 0 else _native.last_error()
 
 
+def append_layers(stores, ks, vs) -> None:
+    """``stores[i].append(ks[i], vs[i])`` for one step of several stores (a
+    model's layers), with one launch per 16 layers (kivi_store_append_layers)
+    for the layers that share the first one's shapes, ring type, input type
+    and strides and take their inputs as they are (on the store's device,
+    channels contiguous, K and V alike); any other layer is appended on its
+    own.  Every window must have room (callers flush first)."""
+    n = len(stores)
+    if n == 0:
+        return
+    st0, k0 = stores[0], ks[0]
+    shape, dtype, strides = k0.shape, k0.dtype, k0.stride()
+    ok = (k0.dim() == 4 and dtype in _SRC_DTYPES and strides[3] == 1 and
+          (st0.k_res.dtype == torch.float32 or st0.k_res.dtype == dtype) and
+          tuple(shape) == (st0.B, st0.H, shape[2], st0.D))
+    batch, rest = [], []
+    for st, k, v in zip(stores, ks, vs):
+        if (ok and k.shape == shape and v.shape == shape and k.dtype is dtype and
+                v.dtype is dtype and k.stride() == strides and v.stride() == strides and
+                k.get_device() == st.device.index and v.get_device() == st.device.index and
+                st.B == st0.B and st.H == st0.H and st.D == st0.D and st.R == st0.R and
+                st.k_res.dtype is st0.k_res.dtype and st.device == st0.device):
+            batch.append((st, k, v))
+        else:
+            rest.append((st, k, v))
+    for st, k, v in rest:
+        st.append(k, v)
+    if not batch:
+        return
+    m, ntok = len(batch), shape[2]
+    for st, _, _ in batch:
+        st._commit()
+        if st.res_len + ntok > st.R:
+            raise RuntimeError(f"residual window overflow ({st.res_len} + {ntok} > {st.R})")
+    kp, vp = (ctypes.c_void_p * m)(), (ctypes.c_void_p * m)()
+    kr, vr = (ctypes.c_void_p * m)(), (ctypes.c_void_p * m)()
+    sl = (ctypes.c_int32 * m)()
+    for i, (st, k, v) in enumerate(batch):
+        kp[i], vp[i] = k.data_ptr(), v.data_ptr()
+        kr[i], vr[i] = st.k_res.data_ptr(), st.v_res.data_ptr()
+        sl[i] = (st.res_start + st.res_len) % st.R
+    sd = (ctypes.c_int64 * (3 * m))(*(strides[:3] * m))
+    with on_device(st0.device):
+        _native.check(_lib.kivi_store_append_layers(
+            m, ctypes.addressof(kp), ctypes.addressof(vp), ctypes.addressof(sd),
+            _SRC_DTYPES[dtype], ntok, ctypes.addressof(kr), ctypes.addressof(vr),
+            st0.res_dtype_code, st0.B, st0.H, st0.D, st0.R, ctypes.addressof(sl),
+            _stream(st0.device)), "kivi_store_append_layers")
+    for st, _, _ in batch:
+        st.res_len += ntok
+
+
 class PackedKVStore:
     """Residual ring + packed chunks for one layer (all on ``device``)."""
 

@@ -44,7 +44,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_error_string():
     from intel_kivi_hybrid_amd import _native
     lib = _native.load()
-    assert lib.kivi_abi_version() == 6
+    assert lib.kivi_abi_version() == 7
     # invalid arguments are rejected on the host, before any launch
     rc = lib.kivi_quantize_keys_per_channel(None, None, None, None, 4, 32, None)
     assert rc == 1 and "null" in _native.last_error()
@@ -181,6 +181,25 @@ def test_store_entry_points_reject_bad_arguments():
     rc = lib.kivi_store_append(p, p, 7, 0, 0, 0, 1, p, p, 0, 1, 1, 8, 4, 0, None)
     assert rc == 1 and "new_dtype 7" in _native.last_error()
     rc = lib.kivi_store_append(p, p, 0, 0, 0, 0, 1, p, p, 1, 1, 1, 8, 4, 0, None)
+    assert rc == 1 and "res_dtype 1" in _native.last_error()
+    # several layers' appends: per-layer arrays checked entry by entry
+    ptrs = (ctypes.c_void_p * 2)(p, p)
+    strides = (ctypes.c_int64 * 6)(0, 0, 0, 0, 0, 0)
+    slots = (ctypes.c_int32 * 2)(0, 4)
+    ap = ctypes.addressof
+    assert lib.kivi_store_append_layers(0, None, None, None, 0, 1, None, None, 0, 1, 1, 8, 4,
+                                        None, None) == 0
+    rc = lib.kivi_store_append_layers(-1, None, None, None, 0, 1, None, None, 0, 1, 1, 8, 4,
+                                      None, None)
+    assert rc == 1 and "n_layers -1" in _native.last_error()
+    rc = lib.kivi_store_append_layers(2, ap(ptrs), None, ap(strides), 0, 1, ap(ptrs), ap(ptrs),
+                                      0, 1, 1, 8, 4, ap(slots), None)
+    assert rc == 1 and "null layer array" in _native.last_error()
+    rc = lib.kivi_store_append_layers(2, ap(ptrs), ap(ptrs), ap(strides), 0, 1, ap(ptrs),
+                                      ap(ptrs), 0, 1, 1, 8, 4, ap(slots), None)
+    assert rc == 1 and "slot 4 outside [0, 4) (layer 1)" in _native.last_error()
+    rc = lib.kivi_store_append_layers(2, ap(ptrs), ap(ptrs), ap(strides), 2, 1, ap(ptrs),
+                                      ap(ptrs), 1, 1, 1, 8, 4, ap(slots), None)
     assert rc == 1 and "res_dtype 1" in _native.last_error()
     # flush of more chunks than the run holds
     rc = lib.kivi_store_flush_chunks(p, p, 0, p, p, 0, 0, 0, 8, 3, p, p, p, p, p, p, None, None,

@@ -103,3 +103,40 @@ def test_staged_token_is_committed_before_other_uses(store_cls):
     # non-fp32 or unaligned tokens take the separate append at once
     st.stage_token(k[:, :, 0:1].to(torch.bfloat16).cuda(), v[:, :, 0:1].to(torch.bfloat16).cuda())
     assert st._pending is None and st.res_len == 9
+
+
+@pytest.mark.parametrize("ring,src", [(torch.float32, torch.float32),
+                                      (torch.float32, torch.bfloat16),
+                                      (torch.bfloat16, torch.bfloat16)])
+def test_append_layers_matches_per_layer_appends(store_cls, ring, src):
+    """One step's tokens for 20 layers (two launches of the multi-layer
+    append: 16 + 4 layers), from strided views like a DynamicCache's, into
+    rings at different positions, equal bit for bit the per-layer appends;
+    a layer whose input has another type is appended on its own."""
+    from intel_kivi_hybrid_amd.store import append_layers
+    L, B, H, D, G, R = 20, 2, 3, 64, 32, 48
+    print(f"[append] {L} layers, ring {ring}, new tokens {src}", flush=True)
+    a = [store_cls(B, H, D, G, R, "cuda:0", residual_dtype=ring) for _ in range(L)]
+    b = [store_cls(B, H, D, G, R, "cuda:0", residual_dtype=ring) for _ in range(L)]
+    for i in range(L):                       # windows at different fill levels and starts
+        k, v = make_kv(B, H, 20 + 3 * i, D, seed=i)
+        for st in (a[i], b[i]):
+            st.extend(k.to(ring).cuda(), v.to(ring).cuda(), flush_at=R)
+    ks, vs = [], []
+    for i in range(L):
+        k, v = make_kv(B, H, 40, D, seed=100 + i)     # a cache of 40 tokens; the step's
+        kc = k.transpose(1, 2).contiguous().transpose(1, 2).to(src).cuda()
+        vc = v.transpose(1, 2).contiguous().transpose(1, 2).to(src).cuda()
+        ks.append(kc[:, :, -1:])                      # newest token, a strided view
+        vs.append(vc[:, :, -1:])
+    ks[7] = ks[7].float() if src != torch.float32 else ks[7].half()   # not batchable:
+    vs[7] = vs[7].float() if src != torch.float32 else vs[7].half()   # appended alone
+    if ring != torch.float32:
+        ks[7], vs[7] = ks[7].to(ring), vs[7].to(ring)
+    append_layers(a, ks, vs)
+    for st, k, v in zip(b, ks, vs):
+        st.append(k, v)
+    torch.cuda.synchronize()
+    for i in range(L):
+        assert (a[i].res_start, a[i].res_len) == (b[i].res_start, b[i].res_len)
+        assert torch.equal(a[i].k_res, b[i].k_res) and torch.equal(a[i].v_res, b[i].v_res), i
