@@ -169,56 +169,60 @@ class KiviCache:
         # appended together after the loop (one launch for all of them); the
         # others flush and append on their own, as before.
         appends = []
-        for i, (k, v) in enumerate(_iter_kv_layers(past_key_values)):
-            if self.batch_size is None:
-                self.batch_size = k.shape[0]
-                self.num_kv_heads = k.shape[1]
-            else:
-                assert k.shape[0] == self.batch_size, (
-                    f"KiviCache batch size changed mid-session "
-                    f"({self.batch_size} -> {k.shape[0]}) at layer {i}. "
-                    f"Call reset() before starting a new request/batch.")
-            assert k.shape[-1] == self.head_dim, (
-                f"KiviCache was built for head_dim {self.head_dim} but layer {i} "
-                f"has key head_dim {k.shape[-1]}")
+        try:
+            for i, (k, v) in enumerate(_iter_kv_layers(past_key_values)):
+                if self.batch_size is None:
+                    self.batch_size = k.shape[0]
+                    self.num_kv_heads = k.shape[1]
+                else:
+                    assert k.shape[0] == self.batch_size, (
+                        f"KiviCache batch size changed mid-session "
+                        f"({self.batch_size} -> {k.shape[0]}) at layer {i}. "
+                        f"Call reset() before starting a new request/batch.")
+                assert k.shape[-1] == self.head_dim, (
+                    f"KiviCache was built for head_dim {self.head_dim} but layer {i} "
+                    f"has key head_dim {k.shape[-1]}")
 
-            new_start = 0
-            if self._fed[i]:
-                new_start = self._quant_token_count[i] + self._stores[i].res_len
-                assert k.shape[2] >= new_start, (
-                    f"KiviCache desync at layer {i}: expected past length "
-                    f"{new_start} but got {k.shape[2]}. add_tokens() must be "
-                    f"called exactly once per forward pass, seeded by "
-                    f"get_full_cache().")
-                new_k = k[:, :, new_start:, :]
-                new_v = v[:, :, new_start:, :]
-            else:
-                new_k, new_v = k, v
+                new_start = 0
+                if self._fed[i]:
+                    new_start = self._quant_token_count[i] + self._stores[i].res_len
+                    assert k.shape[2] >= new_start, (
+                        f"KiviCache desync at layer {i}: expected past length "
+                        f"{new_start} but got {k.shape[2]}. add_tokens() must be "
+                        f"called exactly once per forward pass, seeded by "
+                        f"get_full_cache().")
+                    new_k = k[:, :, new_start:, :]
+                    new_v = v[:, :, new_start:, :]
+                else:
+                    new_k, new_v = k, v
 
-            assert new_k.shape[2] > 0, (
-                f"KiviCache desync at layer {i}: the forward pass produced "
-                f"no tokens beyond the {new_start} already tracked. "
-                f"add_tokens() was called twice on the same forward output, "
-                f"or the model was fed a past_key_values not obtained from "
-                f"get_full_cache(). Silently skipping here would drop this "
-                f"step's KV and corrupt all subsequent attention.")
+                assert new_k.shape[2] > 0, (
+                    f"KiviCache desync at layer {i}: the forward pass produced "
+                    f"no tokens beyond the {new_start} already tracked. "
+                    f"add_tokens() was called twice on the same forward output, "
+                    f"or the model was fed a past_key_values not obtained from "
+                    f"get_full_cache(). Silently skipping here would drop this "
+                    f"step's KV and corrupt all subsequent attention.")
 
-            fed = self._fed[i]
-            store = self._store_for(i, k.shape[0], k.shape[1], new_k.shape[2])
-            self._serve_device[i] = k.device
-            self._serve_dtype[i] = k.dtype if k.dtype in (torch.bfloat16, torch.float16) \
-                else torch.float32
-            # fp32, bf16 and fp16 K/V are read as they are (widening to fp32
-            # is exact, as the reference's .float() is, manager.py:210-214).
-            if fed and store.res_len + new_k.shape[2] < self.R:
-                appends.append((store, new_k, new_v))
-                continue
-            flushes = store.extend(new_k, new_v, flush_at=self.R)
-            if flushes:
-                self._record_flushes(i, flushes)
-                self._cache_view_valid = False
-        if appends:
-            append_layers(*zip(*appends))
+                fed = self._fed[i]
+                store = self._store_for(i, k.shape[0], k.shape[1], new_k.shape[2])
+                self._serve_device[i] = k.device
+                self._serve_dtype[i] = k.dtype if k.dtype in (torch.bfloat16, torch.float16) \
+                    else torch.float32
+                # fp32, bf16 and fp16 K/V are read as they are (widening to fp32
+                # is exact, as the reference's .float() is, manager.py:210-214).
+                if fed and store.res_len + new_k.shape[2] < self.R:
+                    appends.append((store, new_k, new_v))
+                    continue
+                flushes = store.extend(new_k, new_v, flush_at=self.R)
+                if flushes:
+                    self._record_flushes(i, flushes)
+                    self._cache_view_valid = False
+        finally:
+            # (layers before a failed check keep this step's tokens, as when
+            # each layer appended on its own)
+            if appends:
+                append_layers(*zip(*appends))
 
     def get_full_cache(self) -> DynamicCache:
         """The cache to pass as ``past_key_values`` to the next forward pass
