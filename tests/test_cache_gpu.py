@@ -89,6 +89,34 @@ def test_desync_and_batch_change_raise(KiviCache):
         c.add_tokens(FakeModel(1, 2, 8, "in_place", batch=3).forward(9))
 
 
+def test_failed_check_keeps_earlier_layers_tokens(KiviCache):
+    """A step whose third layer fails its check (no new token) still files
+    the token of the two layers before it, as per-layer appends did; the
+    other layers' tokens stay out."""
+    from transformers import DynamicCache
+    L, B, H, D = 4, 1, 2, 8
+    c = KiviCache(L, D, H, device="cuda:0", group_size=4, residual_length=8)
+    g = torch.Generator().manual_seed(3)
+    k0 = [torch.randn(B, H, 5, D, generator=g).cuda() for _ in range(L)]
+    v0 = [torch.randn(B, H, 5, D, generator=g).cuda() for _ in range(L)]
+    first = DynamicCache()
+    for i in range(L):
+        first.update(k0[i], v0[i], i)
+    c.add_tokens(first)
+    step = DynamicCache()
+    for i in range(L):
+        n = 5 if i == 2 else 6                      # layer 2 brings no new token
+        kx = torch.cat([k0[i], torch.randn(B, H, 1, D, generator=g).cuda()], 2)[:, :, :n]
+        vx = torch.cat([v0[i], torch.randn(B, H, 1, D, generator=g).cuda()], 2)[:, :, :n]
+        step.update(kx, vx, i)
+    with pytest.raises(AssertionError, match="no tokens beyond"):
+        c.add_tokens(step)
+    assert [c.store(i).res_len for i in range(L)] == [6, 6, 5, 5]
+    for i in (0, 1):
+        kr, vr = c.store(i).residual()
+        assert torch.equal(kr, step.layers[i].keys) and torch.equal(vr, step.layers[i].values)
+
+
 def test_reset_and_reuse_with_new_batch(KiviCache):
     c = KiviCache(2, 16, 2, device="cuda:0", group_size=4, residual_length=8)
     ref = KiviCacheOracle(2, 16, 2, 4, 8)
